@@ -1,0 +1,119 @@
+/*
+ * kda355.h -- C ABI of the MI355X (gfx950) KDA library libkda355.so.
+ *
+ * KDA (Kimi Delta Attention): the gated delta rule with a per-key-channel decay, head dim K = V = 128, fp32
+ * state stored V-major [V][K] (128 x 128 floats = 64 KiB per (sequence, head)).
+ *
+ * Every entry point takes a POD argument struct of raw device pointers, element strides and sizes plus a
+ * hipStream_t, launches asynchronously on that stream and returns a status code.  Nothing here allocates device
+ * memory, synchronizes, or keeps per-call global state, so every launch entry point is safe inside HIP-graph
+ * capture and re-entrant across threads and streams.  bf16 / fp16 tensors are passed as `const void*`.
+ *
+ * Status codes: 0 = launched; KDA355_EINVAL (-1) = invalid arguments (nothing launched, kda355_last_error()
+ * names the argument); KDA355_ELAUNCH (-2) = the HIP launch failed.
+ *
+ * Which reference interface each entry point replaces (caoshiyi/eat-kernels paths):
+ *   kda355_recurrent_launch       vLLM fused_recurrent_kda as called by the Kimi layer
+ *                                 (kda/mi350x/benchmark/vllm_reference/kda.py:488-502, 560-575) and the recurrent
+ *                                 core of the decode kernel's `run` binding (kda/mi350x/kda/decode/kda_v14_b.cu:
+ *                                 3266-3312, slot rules `slots()` :1013-1042)
+ *   kda355_spec_commit_launch     the commit of an accepted draft length (kda/mi350x/reference.py:117-121 reads the
+ *                                 state after token a-1; this copies it to the sequence's pool slot)
+ *   kda355_prefill_plan           kda_build_meta (kda/mi350x/kda/prefill/kernel.h:100-102) and prepare_prod
+ *                                 (kda/mi350x/kda/prefill/main.cpp:103-130): host-only schedule tables
+ *   kda355_prefill_workspace_bytes  kda_workspace_floats (kda/mi350x/kda/prefill/kernel.h:90-91)
+ *   kda355_prefill_launch         kda_prefill_kernel_launch (kda/mi350x/kda/prefill/kernel.h:33-56) with the
+ *                                 KdaPool production contract (kernel.h:19-31)
+ */
+#ifndef KDA355_H
+#define KDA355_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* kda355_stream_t; /* == hipStream_t */
+
+#define KDA355_EINVAL (-1)
+#define KDA355_ELAUNCH (-2)
+#define KDA355_HEAD_DIM 128
+#define KDA355_CHUNK 64
+
+/* ------------------------------------------------------------------------------------------------ recurrent */
+
+/* flags of KdaRecurrentArgs */
+#define KDA355_REC_NORMALIZE_QK 1u  /* q, k <- x * rsqrt(sum x^2 + 1e-6) in the kernel (kda/mi350x/reference.py:159-160) */
+#define KDA355_REC_RAW_GATE 2u      /* g is bf16 raw_g: g = lower_bound * sigmoid(exp(A_log[h]) * (raw_g + dt_bias[h,k])) */
+#define KDA355_REC_RAW_BETA 4u      /* beta is bf16 raw_beta: beta = sigmoid(raw_beta) */
+#define KDA355_REC_PER_TOKEN 8u     /* write the state after every token t to write_idx[n, t] (spec verify);
+                                       otherwise the final state goes back to the read row (plain decode) */
+#define KDA355_REC_SLOT0_RESERVED 16u /* row 0 of read_pool is the padding slot: never read, never written */
+#define KDA355_REC_WRITE_SLOT0_RESERVED 32u /* the same rule for write_pool (PER_TOKEN destinations) */
+
+/*
+ * Recurrent decode / speculative verify over B sequences x S tokens (T = B*S rows, row n*S + t is token t of
+ * sequence n), H heads.  Per (n, h):
+ *     read row   r = read_idx[n * read_idx_stride + (num_accepted ? clamp(num_accepted[n], 1, S) - 1 : 0)]
+ *     S0         = read_pool[r]      (a padding row -- outside [0, read_slots), or 0 with SLOT0_RESERVED -- is
+ *                                     never read; the sequence is skipped and its output rows are zero)
+ *     per token: S *= exp(g_t) (key axis);  u = beta_t (v_t - S k_t);  S += u k_t^T;  o_t = scale * S q_t
+ *     writes     PER_TOKEN: write_pool[write_idx[n*S + t]] = state after token t (padding rows skipped);
+ *                otherwise read_pool[r] = final state.
+ * The reference's spec-verify mapping (kda/mi350x/reference.py:135-143,168-171) is read_pool == write_pool,
+ * read_idx == write_idx == state_indices [B, S], read_idx_stride = S, num_accepted given, PER_TOKEN.
+ */
+typedef struct KdaRecurrentArgs {
+    const void* q;              /* bf16 [T, H, 128], row stride qkv_row_stride elements */
+    const void* k;
+    const void* v;
+    const void* g;              /* fp32 [T, H, 128] log-decay, or bf16 raw_g with RAW_GATE; row stride g_row_stride */
+    const void* beta;           /* fp32 [T, H] activated, or bf16 raw_beta with RAW_BETA; row stride beta_row_stride */
+    const float* A_log;         /* [H]        (RAW_GATE only) */
+    const float* dt_bias;       /* [H * 128]  (RAW_GATE only) */
+    float* read_pool;           /* [read_slots, H, 128, 128] fp32 V-major, slot stride read_slot_stride floats */
+    float* write_pool;          /* PER_TOKEN destination pool (may equal read_pool) */
+    const int32_t* read_idx;    /* [B, read_idx_stride] */
+    const int32_t* num_accepted;/* [B] or NULL */
+    const int32_t* write_idx;   /* [B, S] (PER_TOKEN) or NULL */
+    void* out;                  /* bf16 [T, H, 128], row stride out_row_stride elements */
+    int64_t qkv_row_stride, g_row_stride, beta_row_stride, out_row_stride;
+    int64_t read_slot_stride, read_slots, write_slot_stride, write_slots;
+    int32_t B, S, H, read_idx_stride;
+    float scale, lower_bound;
+    uint32_t flags;
+    int32_t reserved;
+} KdaRecurrentArgs;
+
+int kda355_recurrent_launch(const KdaRecurrentArgs* args, kda355_stream_t stream);
+
+/*
+ * Commit of an accepted draft length: for each sequence n with a = clamp(num_accepted[n], 1, S),
+ * pool[pool_idx[n]] = scratch[scratch_idx[n*S + a - 1]] (all H heads; padding rows skipped as above).
+ */
+typedef struct KdaSpecCommitArgs {
+    const float* scratch;       /* [scratch_slots, H, 128, 128] */
+    float* pool;                /* [pool_slots, H, 128, 128] */
+    const int32_t* scratch_idx; /* [B, S] */
+    const int32_t* pool_idx;    /* [B] */
+    const int32_t* num_accepted;/* [B] */
+    int64_t scratch_slot_stride, scratch_slots, pool_slot_stride, pool_slots;
+    int32_t B, S, H;
+    uint32_t flags;             /* KDA355_REC_SLOT0_RESERVED applies to the pool (scratch rows may use 0) */
+} KdaSpecCommitArgs;
+
+int kda355_spec_commit_launch(const KdaSpecCommitArgs* args, kda355_stream_t stream);
+
+/* ------------------------------------------------------------------------------------------------ misc */
+
+/* Human-readable reason of the last KDA355_EINVAL / KDA355_ELAUNCH on the calling thread ("" if none). */
+const char* kda355_last_error(void);
+/* Library version (major * 10000 + minor * 100 + patch). */
+int kda355_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KDA355_H */
