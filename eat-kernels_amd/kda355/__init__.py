@@ -1,11 +1,15 @@
 """kda355: MI355X-native (gfx950) KDA -- Kimi Delta Attention, head dim 128 -- behind the reference's API surfaces.
 
+    from kda355 import chunk_kda, kda_prefill                      # plain prefill calls (fla / reference forms)
+    from kda355 import prefill_prepare, prefill                    # vLLM-ROCm Kimi serving prefill (paged pool)
     from kda355 import fused_recurrent_kda, spec_commit           # decode / speculative verify on a state pool
 
 Every entry point runs the hand-written HIP kernels of libkda355.so (include/kda355.h).  There is no CPU or PyTorch
 fallback: calling on CPU tensors raises TypeError, and a missing library raises RuntimeError.
 """
 from ._lib import LIB_PATH, lib  # noqa: F401
+from .prefill import chunk_kda, kda_prefill, plan, prefill, prefill_prepare  # noqa: F401
 from .recurrent import fused_recurrent_kda, spec_commit  # noqa: F401
 
-__all__ = ["fused_recurrent_kda", "spec_commit", "lib", "LIB_PATH"]
+__all__ = ["chunk_kda", "kda_prefill", "plan", "prefill", "prefill_prepare", "fused_recurrent_kda", "spec_commit",
+           "lib", "LIB_PATH"]

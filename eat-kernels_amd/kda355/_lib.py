@@ -54,9 +54,9 @@ class KdaPrefillPlanIn(ctypes.Structure):
 
 class KdaPrefillPlan(ctypes.Structure):
     _fields_ = [
-        ("T", I64), ("N", I32), ("H", I32), ("num_chunks", I32), ("num_pieces", I32), ("max_piece_chunks", I32),
-        ("vslices", I32), ("table_words", I64), ("workspace_bytes", I64), ("magic", U32), ("flags", U32),
-        ("ck_rows", I64),
+        ("T", I64), ("N", I32), ("H", I32), ("num_chunks", I32), ("num_chains", I32), ("max_chain_chunks", I32),
+        ("ck_every", I32), ("table_words", I64), ("workspace_bytes", I64), ("ck_rows", I64), ("magic", U32),
+        ("flags", U32), ("reserved", I32), ("reserved2", I32),
     ]
 
 
@@ -91,13 +91,12 @@ def lib():
         L.kda355_recurrent_launch.restype = ctypes.c_int
         L.kda355_spec_commit_launch.argtypes = [ctypes.POINTER(KdaSpecCommitArgs), P]
         L.kda355_spec_commit_launch.restype = ctypes.c_int
-        if hasattr(L, "kda355_prefill_plan"):
-            L.kda355_prefill_plan.argtypes = [ctypes.POINTER(KdaPrefillPlanIn), ctypes.POINTER(KdaPrefillPlan), P, I64]
-            L.kda355_prefill_plan.restype = ctypes.c_int
-            L.kda355_prefill_workspace_bytes.argtypes = [ctypes.POINTER(KdaPrefillPlan)]
-            L.kda355_prefill_workspace_bytes.restype = I64
-            L.kda355_prefill_launch.argtypes = [ctypes.POINTER(KdaPrefillArgs), P]
-            L.kda355_prefill_launch.restype = ctypes.c_int
+        L.kda355_prefill_plan.argtypes = [ctypes.POINTER(KdaPrefillPlanIn), ctypes.POINTER(KdaPrefillPlan), P, I64]
+        L.kda355_prefill_plan.restype = ctypes.c_int
+        L.kda355_prefill_workspace_bytes.argtypes = [ctypes.POINTER(KdaPrefillPlan)]
+        L.kda355_prefill_workspace_bytes.restype = I64
+        L.kda355_prefill_launch.argtypes = [ctypes.POINTER(KdaPrefillArgs), P]
+        L.kda355_prefill_launch.restype = ctypes.c_int
         L.kda355_last_error.restype = ctypes.c_char_p
         L.kda355_version.restype = ctypes.c_int
         _lib = L

@@ -1,0 +1,363 @@
+"""Chunked KDA prefill (host side of kda355_prefill_plan / kda355_prefill_launch).
+
+Three surfaces, each mirroring a reference interface:
+
+  * chunk_kda(q, k, v, g, beta, scale, initial_state, output_final_state, cu_seqlens, ...) -> (o, final_state)
+      the fla plain call as the reference invokes it (kda/b200/bench.py:108-117, kda/mi350x_plain/bench.py:83-92);
+      g / beta are used as given unless use_gate_in_kernel / use_beta_sigmoid_in_kernel ask for the raw forms.
+  * kda_prefill(q, k, v, raw_g, raw_beta, A_log, dt_bias, initial_state, cu_seqlens, scale, lower_bound, meta,
+                **serving_kwargs) -> (out, new_state[, checkpoints])
+      kda/mi350x_plain/kda_mi350x.py:37-46 (gates in the kernel), plus the B200 serving keywords
+      (kda/b200/kda_b200.py:15-24): ssm_state_indices (pool form), state_checkpoints / checkpoint_cu_starts /
+      checkpoint_every_n_tokens (every-n rows, fp32 or bf16).
+  * prefill_prepare(cu_seqlens_cpu, num_heads, checkpoint_offsets, checkpoint_state_indices, device) -> meta
+    prefill(q, k, v, raw_g, raw_beta, A_log, dt_bias, scale, lower_bound, state_cache, state_indices,
+            has_initial_state, cu_seqlens, out, checkpoint_offsets, checkpoint_state_indices, meta) -> None
+      the vLLM-ROCm Kimi serving convention (kda/mi350x/kda/kernel.py:100-147, kda/mi350x/CONTRACT.md:14-50): paged
+      fp32 pool read / written in place, has_initial_state, one checkpoint row per sequence, strided raw_beta,
+      output into the caller's slice, no host synchronization inside prefill().
+Errors: TypeError for dtype / device, ValueError for shapes, strides and a meta from another layout (the reference
+raises RuntimeError from TORCH_CHECK at kda/mi350x/kda/prefill/main.cpp:145-174; a ValueError is a RuntimeError-free
+subclass of Exception, so callers catching Exception see both).
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import torch
+
+from . import _lib
+
+D = 128
+CHUNK = 64
+
+PF_NORMALIZE_QK = 1
+PF_RAW_GATE = 2
+PF_RAW_BETA = 4
+PF_POOL = 8
+PF_CK_SINGLE = 16
+PF_CK_EVERY = 32
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+class PrefillMeta:
+    """Schedule of one batch layout: the host plan, its device table and the layout it was made for."""
+
+    def __init__(self, plan, tables, num_heads, ck_every, any_ck, lens):
+        self.plan = plan
+        self.lens = lens            # host int64 [N] sequence lengths
+        self.tables = tables
+        self.H = num_heads
+        self.N = plan.N
+        self.T = plan.T
+        self.ck_every = ck_every
+        self.any_ck = any_ck
+
+    @property
+    def workspace_bytes(self):
+        return int(self.plan.workspace_bytes)
+
+    @property
+    def ck_rows(self):
+        return int(self.plan.ck_rows)
+
+
+def plan(cu_seqlens, num_heads, checkpoint_offsets=None, ck_every=0, device=None):
+    """Host-only schedule from the layout (never the data); one H2D copy of the table when device is a GPU."""
+    cu = np.ascontiguousarray(torch.as_tensor(cu_seqlens).detach().cpu().numpy(), dtype=np.int64)
+    N = cu.size - 1
+    if N < 1:
+        raise ValueError("kda355: cu_seqlens needs at least 2 entries")
+    ck = None
+    if checkpoint_offsets is not None:
+        ck = np.ascontiguousarray(torch.as_tensor(checkpoint_offsets).detach().cpu().numpy(), dtype=np.int32)
+        if ck.size != N:
+            raise ValueError("kda355: checkpoint_offsets must have N entries")
+    pin = _lib.KdaPrefillPlanIn()
+    pin.cu_seqlens = ctypes.c_void_p(cu.ctypes.data)
+    pin.ck_offsets = ctypes.c_void_p(ck.ctypes.data) if ck is not None else None
+    pin.N, pin.H, pin.ck_every = N, int(num_heads), int(ck_every)
+    pl = _lib.KdaPrefillPlan()
+    L = _lib.lib()
+    _lib.check(L.kda355_prefill_plan(ctypes.byref(pin), ctypes.byref(pl), None, 0), "prefill_plan")
+    tab = np.zeros(int(pl.table_words), np.int32)
+    _lib.check(L.kda355_prefill_plan(ctypes.byref(pin), ctypes.byref(pl), ctypes.c_void_p(tab.ctypes.data), tab.size),
+               "prefill_plan")
+    t = torch.from_numpy(tab)
+    if device is not None and torch.device(device).type == "cuda":
+        t = t.to(device)
+    any_ck = ck is not None and bool(np.any(ck > 0))
+    return PrefillMeta(pl, t, int(num_heads), int(ck_every), any_ck, np.diff(cu))
+
+
+def _need(name, t, dtype, device):
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"kda355: {name} must be a tensor")
+    if t.dtype != dtype:
+        raise TypeError(f"kda355: {name} must be {dtype}, got {t.dtype}")
+    if t.device != device:
+        raise TypeError(f"kda355: {name} must be on {device}, got {t.device}")
+
+
+def _tok_rows(name, t, T, H, last):
+    """[1, T, H, last] (or [1, T, H]) with dense heads; returns the token stride."""
+    shape = (1, T, H, last) if last else (1, T, H)
+    if tuple(t.shape) != shape:
+        raise ValueError(f"kda355: {name} must be {list(shape)}, got {list(t.shape)}")
+    if last:
+        if (t.stride(3) != 1 and last > 1) or (t.stride(2) != last and H > 1):
+            raise ValueError(f"kda355: {name} must be dense within a token")
+    elif t.stride(2) != 1 and H > 1:
+        raise ValueError(f"kda355: {name} rows must be dense over heads")
+    return t.stride(1) if T > 1 else H * max(last, 1)
+
+
+def _pool_stride(name, pool, H):
+    if pool.dim() != 4 or tuple(pool.shape[1:]) != (H, D, D):
+        raise ValueError(f"kda355: {name} must be [slots, {H}, 128, 128], got {list(pool.shape)}")
+    if pool.stride(3) != 1 or pool.stride(2) != D or pool.stride(1) != D * D:
+        raise ValueError(f"kda355: {name} rows must be dense")
+    return pool.stride(0) if pool.shape[0] > 1 else H * D * D
+
+
+def _launch(meta, q, k, v, gt, bt, out, flags, scale, lower_bound, A_log=None, dt_bias=None, pool=None, idx=None,
+            has_init=None, init=None, final=None, ck_pool=None, ck_idx=None, ck_bf16=False, workspace=None):
+    dev = q.device
+    T, H = q.shape[1], q.shape[2]
+    if meta.T != T or meta.H != H:
+        raise ValueError(f"kda355: meta was prepared for another layout (T/H {meta.T}/{meta.H} vs {T}/{H})")
+    if meta.tables.device != dev:
+        raise ValueError("kda355: meta was prepared for another device")
+    if workspace is None:
+        workspace = torch.empty(max(meta.workspace_bytes, 256), dtype=torch.uint8, device=dev)
+    elif workspace.numel() * workspace.element_size() < meta.workspace_bytes or workspace.device != dev:
+        raise ValueError("kda355: workspace too small or on another device")
+    a = _lib.KdaPrefillArgs()
+    a.q, a.k, a.v, a.g, a.beta = _ptr(q), _ptr(k), _ptr(v), _ptr(gt), _ptr(bt)
+    a.A_log, a.dt_bias = _ptr(A_log), _ptr(dt_bias)
+    a.out = _ptr(out)
+    a.qkv_row_stride = q.stride(1) if T > 1 else H * D
+    a.g_row_stride = gt.stride(1) if T > 1 else H * D
+    a.beta_row_stride = bt.stride(1) if T > 1 else H
+    a.out_row_stride = out.stride(1) if T > 1 else H * D
+    if pool is not None:
+        a.state_pool, a.state_idx, a.has_initial_state = _ptr(pool), _ptr(idx), _ptr(has_init)
+        a.state_slot_stride, a.state_slots = _pool_stride("state_cache", pool, H), pool.shape[0]
+        flags |= PF_POOL
+    else:
+        a.initial_state, a.final_state = _ptr(init), _ptr(final)
+    if ck_pool is not None:
+        a.ck_pool, a.ck_idx = _ptr(ck_pool), _ptr(ck_idx)
+        a.ck_slot_stride, a.ck_slots = _pool_stride("checkpoint pool", ck_pool, H), ck_pool.shape[0]
+        a.ck_dtype = 1 if ck_bf16 else 0
+    a.tables = _ptr(meta.tables)
+    a.workspace = _ptr(workspace)
+    a.T, a.N, a.H = T, meta.N, H
+    a.scale, a.lower_bound = float(scale), float(lower_bound)
+    a.flags = flags
+    a.plan = ctypes.pointer(meta.plan)
+    stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    _lib.check(_lib.lib().kda355_prefill_launch(ctypes.byref(a), stream), "prefill")
+
+
+def _check_qkv(q, k, v):
+    if not isinstance(q, torch.Tensor) or q.dim() != 4 or q.shape[0] != 1 or q.shape[3] != D:
+        raise ValueError(f"kda355: q must be [1, T, H, 128], got {list(getattr(q, 'shape', []))}")
+    dev = q.device
+    if dev.type != "cuda":
+        raise TypeError("kda355: tensors must be on a GPU")
+    T, H = q.shape[1], q.shape[2]
+    strides = []
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        _need(name, t, torch.bfloat16, dev)
+        strides.append(_tok_rows(name, t, T, H, D))
+    if len(set(strides)) != 1:
+        raise ValueError("kda355: q, k, v must share one token stride")
+    return dev, T, H
+
+
+def chunk_kda(q, k, v, g, beta, scale=None, initial_state=None, output_final_state=True, cu_seqlens=None,
+              use_qk_l2norm_in_kernel=True, use_gate_in_kernel=False, use_beta_sigmoid_in_kernel=False,
+              A_log=None, dt_bias=None, lower_bound=-5.0, state_v_first=True, meta=None, out=None, workspace=None,
+              **unused):
+    """fla chunk_kda plain call. q, k, v [1, T, H, 128] bf16; g [1, T, H, 128] (fp32 log-decay, or the raw gate with
+    use_gate_in_kernel); beta [1, T, H] (fp32 activated, or logits with use_beta_sigmoid_in_kernel); initial_state
+    [N, H, 128(V), 128(K)] fp32 or None; cu_seqlens [N+1] (None: one sequence).  meta: a plan(...) result for this
+    layout (skips the host read of cu_seqlens).  Returns (o [1, T, H, 128] bf16, final_state [N, H, 128, 128] fp32
+    or None)."""
+    if not state_v_first:
+        raise ValueError("kda355: only the value-first state layout [N, H, V, K] is supported (state_v_first=True)")
+    dev, T, H = _check_qkv(q, k, v)
+    if scale is None:
+        scale = D ** -0.5
+    flags = PF_NORMALIZE_QK if use_qk_l2norm_in_kernel else 0
+    if use_gate_in_kernel:
+        _need("g", g, torch.bfloat16 if g.dtype == torch.bfloat16 else torch.float32, dev)
+        if g.dtype != torch.bfloat16:
+            g = g.bfloat16()
+        flags |= PF_RAW_GATE
+        if A_log is None or dt_bias is None:
+            raise ValueError("kda355: use_gate_in_kernel needs A_log and dt_bias")
+        _need("A_log", A_log, torch.float32, dev)
+        _need("dt_bias", dt_bias, torch.float32, dev)
+        A_log, dt_bias = A_log.reshape(-1).contiguous(), dt_bias.reshape(-1).contiguous()
+        if A_log.numel() != H or dt_bias.numel() != H * D:
+            raise ValueError("kda355: A_log must be [H] and dt_bias [H*128]")
+    else:
+        _need("g", g, torch.float32, dev)
+    _tok_rows("g", g, T, H, D)
+    if use_beta_sigmoid_in_kernel:
+        if beta.dtype != torch.bfloat16:
+            beta = beta.bfloat16()
+        flags |= PF_RAW_BETA
+    else:
+        _need("beta", beta, torch.float32, dev)
+    _tok_rows("beta", beta, T, H, 0)
+    if meta is None:
+        cu = torch.tensor([0, T], dtype=torch.int64) if cu_seqlens is None else cu_seqlens
+        meta = plan(cu, H, device=dev)
+    N = meta.N
+    if initial_state is not None:
+        _need("initial_state", initial_state, torch.float32, dev)
+        if tuple(initial_state.shape) != (N, H, D, D):
+            raise ValueError(f"kda355: initial_state must be [{N}, {H}, 128, 128], got {list(initial_state.shape)}")
+        initial_state = initial_state.contiguous()
+    if out is None:
+        out = torch.empty(1, T, H, D, dtype=torch.bfloat16, device=dev)
+    else:
+        _need("out", out, torch.bfloat16, dev)
+        _tok_rows("out", out, T, H, D)
+    final = torch.empty(N, H, D, D, dtype=torch.float32, device=dev)
+    _launch(meta, q, k, v, g, beta, out, flags, scale, lower_bound, A_log, dt_bias, init=initial_state, final=final,
+            workspace=workspace)
+    return out, (final if output_final_state else None)
+
+
+def kda_prefill(q, k, v, raw_g, raw_beta, A_log, dt_bias, initial_state, cu_seqlens=None, scale=None,
+                lower_bound=-5.0, meta=None, *, ssm_state_indices=None, state_checkpoints=None,
+                checkpoint_cu_starts=None, checkpoint_every_n_tokens=0):
+    """kda/mi350x_plain/kda_mi350x.py:37-46 (gates, beta sigmoid and q/k norm in the kernel) with the B200 serving
+    keywords (kda/b200/kda_b200.py:15-24):
+      ssm_state_indices int32 [N]: initial_state is a pool [P, H, 128, 128]; sequence i reads and updates slot
+          ssm_state_indices[i] in place and the returned final state is the pool itself;
+      state_checkpoints fp32 / bf16 [C, H, 128, 128] with checkpoint_cu_starts int64 [N+1] and
+          checkpoint_every_n_tokens n (multiple of 64): row checkpoint_cu_starts[i] + j = state before token j*n.
+    Returns (output, final_state) or (output, final_state, state_checkpoints)."""
+    dev, T, H = _check_qkv(q, k, v)
+    if scale is None:
+        scale = D ** -0.5
+    _need("raw_g", raw_g, torch.bfloat16, dev)
+    _tok_rows("raw_g", raw_g, T, H, D)
+    _need("raw_beta", raw_beta, torch.bfloat16, dev)
+    _tok_rows("raw_beta", raw_beta, T, H, 0)
+    _need("A_log", A_log, torch.float32, dev)
+    _need("dt_bias", dt_bias, torch.float32, dev)
+    if A_log.numel() != H or dt_bias.numel() != H * D:
+        raise ValueError("kda355: A_log must be [H] and dt_bias [H*128]")
+    A_log, dt_bias = A_log.reshape(-1).contiguous(), dt_bias.reshape(-1).contiguous()
+    every = int(checkpoint_every_n_tokens or 0)
+    if every and (every % CHUNK or state_checkpoints is None or checkpoint_cu_starts is None):
+        raise ValueError("kda355: checkpoints need state_checkpoints, checkpoint_cu_starts and n a multiple of 64")
+    if meta is None or (every and meta.ck_every != every):
+        cu = torch.tensor([0, T], dtype=torch.int64) if cu_seqlens is None else cu_seqlens
+        meta = plan(cu, H, ck_every=every, device=dev)
+    N = meta.N
+    flags = PF_NORMALIZE_QK | PF_RAW_GATE | PF_RAW_BETA
+    out = torch.empty(1, T, H, D, dtype=torch.bfloat16, device=dev)
+    ck_pool = ck_idx = None
+    ck_bf16 = False
+    if every:
+        if state_checkpoints.dtype not in (torch.float32, torch.bfloat16) or state_checkpoints.device != dev:
+            raise TypeError("kda355: state_checkpoints must be fp32 or bf16 on the device")
+        ck_bf16 = state_checkpoints.dtype == torch.bfloat16
+        ck_pool = state_checkpoints
+        starts = checkpoint_cu_starts.to(device=dev, dtype=torch.int64)
+        counts = (meta.lens + every - 1) // every
+        ck_idx = _ck_row_table(starts[:-1], counts, dev)
+        flags |= PF_CK_EVERY
+    if ssm_state_indices is not None:
+        pool = initial_state
+        _need("initial_state", pool, torch.float32, dev)
+        _need("ssm_state_indices", ssm_state_indices, torch.int32, dev)
+        if ssm_state_indices.dim() != 1 or ssm_state_indices.numel() != N or not ssm_state_indices.is_contiguous():
+            raise ValueError("kda355: ssm_state_indices must be a contiguous int32 [N] tensor")
+        has_init = torch.ones(N, dtype=torch.bool, device=dev)
+        _launch(meta, q, k, v, raw_g, raw_beta, out, flags, scale, lower_bound, A_log, dt_bias, pool=pool,
+                idx=ssm_state_indices, has_init=has_init, ck_pool=ck_pool, ck_idx=ck_idx, ck_bf16=ck_bf16)
+        final = pool
+    else:
+        init = None
+        if initial_state is not None and initial_state.numel():
+            _need("initial_state", initial_state, torch.float32, dev)
+            if tuple(initial_state.shape) != (N, H, D, D):
+                raise ValueError(f"kda355: initial_state must be [{N}, {H}, 128, 128]")
+            init = initial_state.contiguous()
+        final = torch.empty(N, H, D, D, dtype=torch.float32, device=dev)
+        _launch(meta, q, k, v, raw_g, raw_beta, out, flags, scale, lower_bound, A_log, dt_bias, init=init, final=final,
+                ck_pool=ck_pool, ck_idx=ck_idx, ck_bf16=ck_bf16)
+    return (out, final, state_checkpoints) if every else (out, final)
+
+
+def _ck_row_table(starts, counts, dev):
+    """Flattened row ids starts[n] + j, j < counts[n] (device int32)."""
+    counts_t = torch.as_tensor(counts, device=dev)
+    rep = torch.repeat_interleave(starts, counts_t)
+    base = torch.repeat_interleave(torch.cumsum(counts_t, 0) - counts_t, counts_t)
+    j = torch.arange(int(counts_t.sum()), device=dev) - base
+    return (rep + j).to(torch.int32).contiguous()
+
+
+# ------------------------------------------------------------------------------------------------ serving
+def prefill_prepare(cu_seqlens, num_heads, checkpoint_offsets=None, checkpoint_state_indices=None, device=None):
+    """kda/mi350x/kda/kernel.py:100-110: per-step schedule from host copies of the layout, shared by every layer.
+    Offsets that are not positive multiples of 64 within their sequence plan no checkpoint (the reference's
+    prepare_prod rule, kda/mi350x/kda/prefill/main.cpp:110-118)."""
+    dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+    offs = checkpoint_offsets if (checkpoint_offsets is not None and checkpoint_state_indices is not None) else None
+    return plan(cu_seqlens, num_heads, checkpoint_offsets=offs, device=dev)
+
+
+def prefill(q, k, v, raw_g, raw_beta, A_log, dt_bias, scale, lower_bound, state_cache, state_indices,
+            has_initial_state, cu_seqlens, out, checkpoint_offsets=None, checkpoint_state_indices=None, meta=None,
+            workspace=None):
+    """kda/mi350x/kda/kernel.py:131-147 (contract kda/mi350x/CONTRACT.md:32-50).  In place: writes `out` and the pool
+    rows state_indices[n] (final states) and checkpoint_state_indices[n] (state after checkpoint_offsets[n] tokens);
+    nothing else.  No host synchronization when meta is given."""
+    dev, T, H = _check_qkv(q, k, v)
+    if meta is None:
+        meta = prefill_prepare(cu_seqlens, H, checkpoint_offsets, checkpoint_state_indices, dev)
+    _need("raw_g", raw_g, torch.bfloat16, dev)
+    _tok_rows("raw_g", raw_g, T, H, D)
+    _need("raw_beta", raw_beta, torch.bfloat16, dev)
+    _tok_rows("raw_beta", raw_beta, T, H, 0)
+    _need("A_log", A_log, torch.float32, dev)
+    _need("dt_bias", dt_bias, torch.float32, dev)
+    if A_log.numel() != H or dt_bias.numel() != H * D or not A_log.is_contiguous() or not dt_bias.is_contiguous():
+        raise ValueError("kda355: A_log must be contiguous [H] and dt_bias contiguous [H*128]")
+    _need("state_cache", state_cache, torch.float32, dev)
+    _need("state_indices", state_indices, torch.int32, dev)
+    _need("has_initial_state", has_initial_state, torch.bool, dev)
+    N = meta.N
+    if state_indices.dim() != 1 or state_indices.numel() != N or not state_indices.is_contiguous():
+        raise ValueError("kda355: state_indices must be a contiguous int32 [N] tensor")
+    if has_initial_state.numel() != N or not has_initial_state.is_contiguous():
+        raise ValueError("kda355: has_initial_state must be a contiguous bool [N] tensor")
+    _need("out", out, torch.bfloat16, dev)
+    _tok_rows("out", out, T, H, D)
+    ck_given = checkpoint_offsets is not None and checkpoint_state_indices is not None
+    if meta.any_ck and not ck_given:
+        raise ValueError("kda355: meta was prepared with checkpoints but no checkpoint tensors were passed")
+    flags = PF_NORMALIZE_QK | PF_RAW_GATE | PF_RAW_BETA
+    ck_pool = ck_idx = None
+    if ck_given and meta.any_ck:
+        _need("checkpoint_state_indices", checkpoint_state_indices, torch.int32, dev)
+        if checkpoint_state_indices.numel() != N or not checkpoint_state_indices.is_contiguous():
+            raise ValueError("kda355: checkpoint_state_indices must be a contiguous int32 [N] tensor")
+        ck_pool, ck_idx = state_cache, checkpoint_state_indices
+        flags |= PF_CK_SINGLE
+    _launch(meta, q, k, v, raw_g, raw_beta, out, flags, scale, lower_bound, A_log, dt_bias, pool=state_cache,
+            idx=state_indices, has_init=has_initial_state, ck_pool=ck_pool, ck_idx=ck_idx, workspace=workspace)

@@ -105,6 +105,89 @@ typedef struct KdaSpecCommitArgs {
 
 int kda355_spec_commit_launch(const KdaSpecCommitArgs* args, kda355_stream_t stream);
 
+/* ------------------------------------------------------------------------------------------------ prefill */
+
+/* flags of KdaPrefillPlanIn / KdaPrefillArgs */
+#define KDA355_PF_NORMALIZE_QK 1u  /* q, k <- x / max(|x|, 1e-6) in the kernel (kda/mi350x/reference.py:59-60) */
+#define KDA355_PF_RAW_GATE 2u      /* g is bf16 raw_g: g = lower_bound * sigmoid(exp(A_log[h]) * (raw_g + dt_bias[h,k])) */
+#define KDA355_PF_RAW_BETA 4u      /* beta is bf16 raw_beta (any row stride): beta = sigmoid(raw_beta) */
+#define KDA355_PF_POOL 8u          /* states live in a paged pool: read state_pool[state_idx[n]] when has_initial_state[n]
+                                      (else start from zero and never read the row), write the final state there */
+#define KDA355_PF_CK_SINGLE 16u    /* one checkpoint per sequence: the state after ck_offsets[n] tokens (a positive
+                                      multiple of 64, <= the length; planned on the host) goes to ck_pool[ck_idx[n]]
+                                      when ck_idx[n] >= 0 (kda/mi350x/reference.py:38-41,52-57) */
+#define KDA355_PF_CK_EVERY 32u     /* every-n checkpoints: row j of sequence n (j < ceil(len_n / ck_every)) is the state
+                                      before token j * ck_every, stored to ck_pool[ck_idx[row_start_n + j]] with
+                                      row_start_n = sum of the earlier sequences' row counts (kda/b200/kda_b200.py:19-22) */
+
+/* Host-side plan input: the layout only (never the data). */
+typedef struct KdaPrefillPlanIn {
+    const int64_t* cu_seqlens;  /* host [N + 1] token offsets */
+    const int32_t* ck_offsets;  /* host [N] single-checkpoint offsets (tokens) or NULL */
+    int32_t N, H;
+    int32_t ck_every;           /* every-n interval in tokens (multiple of 64) or 0 */
+    int32_t num_cus;            /* 0: default */
+    uint32_t flags;
+    int32_t reserved;
+} KdaPrefillPlanIn;
+
+/* Filled by kda355_prefill_plan. */
+typedef struct KdaPrefillPlan {
+    int64_t T;
+    int32_t N, H, num_chunks, num_chains, max_chain_chunks, ck_every;
+    int64_t table_words;        /* int32 words of the schedule table (copy it to the device once per layout) */
+    int64_t workspace_bytes;    /* device workspace the launch needs (256-byte aligned) */
+    int64_t ck_rows;            /* every-n rows the layout writes (sum over n of ceil(len_n / ck_every)) */
+    uint32_t magic, flags;
+    int32_t reserved, reserved2;
+} KdaPrefillPlan;
+
+/*
+ * Schedule of one batch layout (host only, no device call).  Call once with tables == NULL to get
+ * plan->table_words, then with a host buffer of that many int32 words, and copy the buffer to the device.
+ */
+int kda355_prefill_plan(const KdaPrefillPlanIn* in, KdaPrefillPlan* plan, int32_t* tables, int64_t capacity);
+int64_t kda355_prefill_workspace_bytes(const KdaPrefillPlan* plan);
+
+/*
+ * Chunked prefill over a packed varlen batch (T tokens, N sequences, H heads):
+ *   q, k, v [T, H, 128] bf16; g [T, H, 128] fp32 log-decay or bf16 raw gate; beta [T, H] fp32 or bf16 raw;
+ *   out [T, H, 128] bf16.  Per (n, h) the token recurrence of kda/mi350x/reference.py:85-91 with scale.
+ * States: KDA355_PF_POOL -> state_pool [state_slots, H, 128, 128] (rows dense, slot stride state_slot_stride floats),
+ * else initial_state [N, H, 128, 128] (NULL = zeros) and final_state [N, H, 128, 128], contiguous.
+ * Checkpoint rows go to ck_pool (fp32, or bf16 rounded to nearest even when ck_dtype == 1), slot stride in elements.
+ * Rows outside [0, slots) are skipped.  Asynchronous on `stream`; no host synchronization.
+ */
+typedef struct KdaPrefillArgs {
+    const void* q;
+    const void* k;
+    const void* v;
+    const void* g;
+    const void* beta;
+    const float* A_log;
+    const float* dt_bias;
+    void* out;
+    float* state_pool;
+    const int32_t* state_idx;        /* [N] */
+    const uint8_t* has_initial_state;/* [N] bool */
+    const float* initial_state;
+    float* final_state;
+    void* ck_pool;
+    const int32_t* ck_idx;           /* CK_SINGLE: [N] rows; CK_EVERY: [ck_rows] rows */
+    const int32_t* tables;           /* device copy of the plan's schedule table */
+    void* workspace;                 /* >= plan->workspace_bytes, 256-byte aligned */
+    int64_t qkv_row_stride, g_row_stride, beta_row_stride, out_row_stride;  /* elements between tokens */
+    int64_t state_slot_stride, state_slots, ck_slot_stride, ck_slots;
+    int64_t T;
+    int32_t N, H;
+    float scale, lower_bound;
+    uint32_t flags;
+    int32_t ck_dtype;                /* 0 fp32, 1 bf16 */
+    const KdaPrefillPlan* plan;
+} KdaPrefillArgs;
+
+int kda355_prefill_launch(const KdaPrefillArgs* args, kda355_stream_t stream);
+
 /* ------------------------------------------------------------------------------------------------ misc */
 
 /* Human-readable reason of the last KDA355_EINVAL / KDA355_ELAUNCH on the calling thread ("" if none). */

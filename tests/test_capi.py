@@ -44,12 +44,38 @@ def test_struct_layout_matches_header():
     import subprocess
     import tempfile
     from kda355 import _lib
-    src = '#include "kda355.h"\n#include <stdio.h>\nint main(){printf("%zu %zu\\n", sizeof(KdaRecurrentArgs), ' \
-          'sizeof(KdaSpecCommitArgs));return 0;}\n'
+    src = '#include "kda355.h"\n#include <stdio.h>\nint main(){printf("%zu %zu %zu %zu %zu\\n", ' \
+          'sizeof(KdaRecurrentArgs), sizeof(KdaSpecCommitArgs), sizeof(KdaPrefillPlanIn), sizeof(KdaPrefillPlan), ' \
+          'sizeof(KdaPrefillArgs));return 0;}\n'
     with tempfile.TemporaryDirectory() as d:
         (Path(d) / "m.c").write_text(src)
         subprocess.run(["gcc", "-I", str(ROOT / "include"), str(Path(d) / "m.c"), "-o", str(Path(d) / "m")],
                        check=True)
         sizes = subprocess.run([str(Path(d) / "m")], capture_output=True, text=True, check=True).stdout.split()
-    assert int(sizes[0]) == ctypes.sizeof(_lib.KdaRecurrentArgs)
-    assert int(sizes[1]) == ctypes.sizeof(_lib.KdaSpecCommitArgs)
+    mirrors = [_lib.KdaRecurrentArgs, _lib.KdaSpecCommitArgs, _lib.KdaPrefillPlanIn, _lib.KdaPrefillPlan,
+               _lib.KdaPrefillArgs]
+    assert [int(x) for x in sizes] == [ctypes.sizeof(m) for m in mirrors]
+
+
+def test_prefill_plan_host_only():
+    """The schedule is built on the host from the layout alone: chunk counts, every-n row counts, bad layouts."""
+    import numpy as np
+    from kda355 import _lib
+    L = _lib.lib()
+    cu = np.array([0, 100, 100, 300, 4396], np.int64)
+    pin = _lib.KdaPrefillPlanIn()
+    pin.cu_seqlens = ctypes.c_void_p(cu.ctypes.data)
+    pin.N, pin.H, pin.ck_every = 4, 8, 128
+    pl = _lib.KdaPrefillPlan()
+    assert L.kda355_prefill_plan(ctypes.byref(pin), ctypes.byref(pl), None, 0) == 0
+    assert pl.num_chunks == 2 + 0 + 4 + 64 and pl.T == 4396 and pl.ck_rows == 1 + 0 + 2 + 32
+    assert L.kda355_prefill_workspace_bytes(ctypes.byref(pl)) == pl.num_chunks * 8 * 82432
+    tab = np.zeros(pl.table_words, np.int32)
+    assert L.kda355_prefill_plan(ctypes.byref(pin), ctypes.byref(pl), ctypes.c_void_p(tab.ctypes.data), tab.size) == 0
+    assert L.kda355_prefill_plan(ctypes.byref(pin), ctypes.byref(pl), ctypes.c_void_p(tab.ctypes.data), 3) == _lib.EINVAL
+    bad = np.array([0, 10, 5], np.int64)
+    pin.cu_seqlens, pin.N = ctypes.c_void_p(bad.ctypes.data), 2
+    assert L.kda355_prefill_plan(ctypes.byref(pin), ctypes.byref(pl), None, 0) == _lib.EINVAL
+    assert b"non-decreasing" in L.kda355_last_error()
+    pin.cu_seqlens, pin.N, pin.ck_every = ctypes.c_void_p(cu.ctypes.data), 4, 100
+    assert L.kda355_prefill_plan(ctypes.byref(pin), ctypes.byref(pl), None, 0) == _lib.EINVAL

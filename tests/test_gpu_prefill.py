@@ -1,0 +1,339 @@
+"""GPU parity of the chunked prefill (kda355_prefill_launch) against the fp64 CPU oracle.
+
+Bars (north star): output max-abs error beyond bf16 storage rounding <= 2e-2 x RMS(ref); final / checkpoint states
+relative Frobenius <= 1e-3 (bf16 checkpoint rows: <= the bf16 rounding of the reference row + 1e-3); which pool rows
+are written is bit-exact and every other byte of the pool and of the output's parent buffer is unchanged.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import OUT_TOL, STATE_TOL, config_inputs, f32, gen, out_err, rel_frob
+
+pytestmark = pytest.mark.gpu
+D = 128
+DEV = torch.device("cuda", 0)
+
+
+def _kda():
+    import kda355
+    return kda355
+
+
+def _say(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def _cu(lens):
+    return np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+
+
+def _check_out(got, ref, what):
+    ex, raw, rel = out_err(f32(got), ref)
+    assert ex <= OUT_TOL, f"{what}: output excess {ex:.3e} (raw {raw:.3e}, relL2 {rel:.3e})"
+    return ex
+
+
+def _plain_case(oracle, H, lens, seed, init=True, gscale=1.0, heads_checked=None):
+    kda = _kda()
+    _say(f"plain H={H} lens={lens[:10]} init={init} seed={seed}")
+    g = gen(seed)
+    T = int(sum(lens))
+    q, k, v, gg, beta = config_inputs(T, H, g)
+    gg = gg * gscale
+    N = len(lens)
+    h0 = torch.randn(N, H, D, D, generator=g) * 0.02 if init else None
+    cu = torch.tensor(_cu(lens), dtype=torch.int32)
+    o, fin = kda.chunk_kda(q[None].to(DEV), k[None].to(DEV), v[None].to(DEV), gg[None].to(DEV), beta[None].to(DEV),
+                           initial_state=h0.to(DEV) if init else None, output_final_state=True, cu_seqlens=cu.to(DEV))
+    torch.cuda.synchronize()
+    hs = list(range(H)) if heads_checked is None else heads_checked
+    sel = lambda x: np.ascontiguousarray(f32(x)[:, hs])  # noqa: E731
+    ro, rf = oracle.prefill_plain(sel(q), sel(k), sel(v), sel(gg), sel(beta), _cu(lens),
+                                  initial_state=None if h0 is None else sel(h0), precision=64)
+    _check_out(o[0][:, hs], ro, f"H={H} lens={lens[:6]}")
+    got = f32(fin)[:, hs]
+    for n in range(N):
+        e = rel_frob(got[n], rf[n])
+        assert e <= STATE_TOL, f"H={H} seq {n} (len {lens[n]}): final state relF {e:.3e}"
+
+
+def test_config0_single_sequence(oracle):
+    _plain_case(oracle, 4, [1024], 0, init=False)
+
+
+def test_varlen_with_initial_states(oracle):
+    _plain_case(oracle, 4, [300, 64, 1, 1000, 77], 1)
+
+
+def test_ragged_tiny_and_empty(oracle):
+    _plain_case(oracle, 3, [1, 17, 33, 0, 1, 63, 65, 128, 2], 2)
+
+
+def test_other_head_counts(oracle):
+    for i, (H, lens) in enumerate([(1, [700]), (8, [37, 200]), (16, [129, 64])]):
+        _plain_case(oracle, H, lens, 10 + i)
+
+
+def test_slow_and_fast_decay(oracle):
+    _plain_case(oracle, 2, [2048, 500], 20, gscale=0.01)   # long memory: cross-chunk state carries
+    _plain_case(oracle, 2, [1000], 21, gscale=4.0)         # fast decay
+
+
+def test_config1_layout_subset_of_heads(oracle):
+    """Config 1 (8 sequences, lengths U[256, 8192] from seed 1, H = 32); the oracle checks 4 of the 32 heads."""
+    rng = np.random.default_rng(1)
+    lens = [int(x) for x in rng.integers(256, 8193, size=8)]
+    _plain_case(oracle, 32, lens, 1, heads_checked=[0, 9, 22, 31])
+
+
+def _raw_inputs(g, T, H):
+    q = torch.randn(T, H, D, generator=g).bfloat16()
+    k = torch.randn(T, H, D, generator=g).bfloat16()
+    v = torch.randn(T, H, D, generator=g).bfloat16()
+    raw_g = torch.randn(T, H, D, generator=g).bfloat16()
+    raw_b = torch.randn(T, H, generator=g).bfloat16()
+    A_log = torch.log(torch.empty(H).uniform_(1.0, 16.0, generator=g))
+    dt = torch.exp(torch.rand(H * D, generator=g) * (math.log(0.1) - math.log(0.001)) + math.log(0.001)).clamp(min=1e-4)
+    dt_bias = dt + torch.log(-torch.expm1(-dt))
+    return q, k, v, raw_g, raw_b, A_log, dt_bias
+
+
+def _oracle_gated(oracle, q, k, v, raw_g, raw_b, A_log, dt_bias, lb=-5.0):
+    qn, kn = oracle.l2norm_clamp(f32(q)), oracle.l2norm_clamp(f32(k))
+    gl = oracle.gate(f32(raw_g), f32(A_log), f32(dt_bias), lb)
+    bt = oracle.sigmoid(f32(raw_b))
+    return qn, kn, f32(v), gl, bt
+
+
+@pytest.mark.parametrize("gates", ["b200", "spectrum", "slow"])
+def test_kda_prefill_raw_gates(oracle, gates):
+    """kda_prefill (gates, beta sigmoid and norms in the kernel), including test_slowdecay's gate regimes."""
+    kda = _kda()
+    H, lens = 4, [1500, 64, 333]
+    _say(f"kda_prefill gates={gates}")
+    g = gen(30)
+    T = sum(lens)
+    q, k, v, raw_g, raw_b, A_log, dt_bias = _raw_inputs(g, T, H)
+    if gates != "b200":
+        lo, hi = (-14.0, 2.0) if gates == "spectrum" else (-12.0, -6.0)
+        A_log = torch.zeros(H)
+        dt_bias = torch.linspace(lo, hi, D).repeat(H)
+    h0 = torch.randn(len(lens), H, D, D, generator=g) * 0.25
+    cu = torch.tensor(_cu(lens), dtype=torch.int64)
+    o, fin = kda.kda_prefill(q[None].to(DEV), k[None].to(DEV), v[None].to(DEV), raw_g[None].to(DEV),
+                             raw_b[None].to(DEV), A_log.to(DEV), dt_bias.to(DEV), h0.to(DEV), cu.to(DEV))
+    torch.cuda.synchronize()
+    qn, kn, vf, gl, bt = _oracle_gated(oracle, q, k, v, raw_g, raw_b, A_log, dt_bias)
+    ro, rf, _ = oracle.chains(qn, kn, vf, gl, bt, _cu(lens), D ** -0.5, f32(h0), precision=64)
+    _check_out(o[0], ro, f"gates={gates}")
+    for n in range(len(lens)):
+        assert rel_frob(f32(fin[n]), rf[n]) <= STATE_TOL, f"gates={gates} seq {n}"
+
+
+def _pages(slots, H, taps, g):
+    """vLLM hybrid page layout (kda/mi350x/CONTRACT.md:60-67): conv state then SSM state per padded page."""
+    dim = H * D
+    conv_bytes = taps * 3 * dim * 2
+    page = -(-(conv_bytes + H * D * D * 4 + 4096) // 256) * 256
+    raw = torch.randint(0, 256, (slots * page,), dtype=torch.uint8, generator=g).to(DEV)
+    ssm = torch.as_strided(raw.view(torch.float32), (slots, H, D, D), (page // 4, D * D, D, 1), conv_bytes // 4)
+    ssm.copy_((torch.randn(slots, H, D, D, generator=g) * 0.05).to(DEV))
+    return raw, ssm
+
+
+def test_serving_pool_checkpoints_page_layout(oracle):
+    """prefill_prepare + prefill on the page layout: has_initial_state with NaN rows, one checkpoint per sequence,
+    strided raw_beta, out a slice behind 256 leading rows; only out and the named rows change."""
+    kda = _kda()
+    H = 4
+    lens = [777, 64, 1, 130, 1024, 17, 255]
+    hinit = [1, 0, 1, 0, 1, 1, 0]
+    ck_off = [704, 64, 0, 0, 1024, 0, 192]
+    _say(f"serving pool H={H} lens={lens}")
+    g = gen(40)
+    T, N = sum(lens), len(lens)
+    q, k, v, raw_g, raw_b, A_log, dt_bias = _raw_inputs(g, T, H)
+    slots = 3 * N + 5
+    raw, ssm = _pages(slots, H, 3, g)
+    perm = torch.randperm(slots - 1, generator=g) + 1
+    sidx = perm[:N].to(torch.int32)
+    cidx = torch.tensor([int(perm[N + n]) if ck_off[n] > 0 else -1 for n in range(N)], dtype=torch.int32)
+    for n in range(N):                                   # rows that must not be read: NaN
+        if not hinit[n]:
+            ssm[int(sidx[n])] = float("nan")
+        if ck_off[n] > 0:
+            ssm[int(cidx[n])] = float("nan")
+    before = raw.clone()
+    pool0 = ssm.cpu().numpy().copy()
+    Wp = 4 * H * D + D + H + 8                           # input projection row: beta is a strided column slice
+    proj = torch.randn(T, Wp, generator=g).bfloat16().to(DEV)
+    proj[:, 4 * H * D + D:4 * H * D + D + H] = raw_b.to(DEV)
+    beta_view = proj[:, 4 * H * D + D:4 * H * D + D + H][None]
+    parent = torch.full((1, 256 + T + 7, H, D), 3.0, dtype=torch.bfloat16, device=DEV)
+    out = parent[:, 256:256 + T]
+    parent_before = parent.clone()
+    cu_cpu = torch.tensor(_cu(lens), dtype=torch.int32)
+    meta = kda.prefill_prepare(cu_cpu, H, torch.tensor(ck_off, dtype=torch.int32), cidx, device=DEV)
+    kda.prefill(q[None].to(DEV), k[None].to(DEV), v[None].to(DEV), raw_g[None].to(DEV), beta_view, A_log.to(DEV),
+                dt_bias.to(DEV), D ** -0.5, -5.0, ssm, sidx.to(DEV), torch.tensor(hinit, dtype=torch.bool).to(DEV),
+                cu_cpu.to(DEV), out, torch.tensor(ck_off, dtype=torch.int32).to(DEV), cidx.to(DEV), meta=meta)
+    torch.cuda.synchronize()
+    ro, rnew = oracle.prefill_serving(f32(q), f32(k), f32(v), f32(raw_g), f32(raw_b), f32(A_log), f32(dt_bias), -5.0,
+                                      D ** -0.5, pool0, sidx.numpy(), np.array(hinit, bool), _cu(lens),
+                                      np.array(ck_off), cidx.numpy(), precision=64)
+    _check_out(out[0], ro, "serving")
+    got = ssm.cpu().numpy()
+    written = [int(s) for s in sidx] + [int(c) for c in cidx if c >= 0]
+    for r in written:
+        e = rel_frob(got[r], rnew[r])
+        assert e <= STATE_TOL, f"pool row {r}: relF {e:.3e}"
+    # every byte outside out and the written rows unchanged
+    exp_raw = before.clone()
+    exp_ssm = torch.as_strided(exp_raw.view(torch.float32), ssm.shape, ssm.stride(), ssm.storage_offset())
+    for r in written:
+        exp_ssm[r] = ssm[r]
+    assert torch.equal(raw, exp_raw), "bytes outside the written rows changed"
+    assert torch.equal(parent[:, :256], parent_before[:, :256]) and torch.equal(parent[:, 256 + T:],
+                                                                                  parent_before[:, 256 + T:])
+
+
+def test_serving_no_sync_with_meta():
+    """prefill() with a meta does not synchronize with the device (CONTRACT.md:48-50 host gate)."""
+    kda = _kda()
+    H, lens = 2, [100, 50]
+    g = gen(41)
+    T = sum(lens)
+    q, k, v, raw_g, raw_b, A_log, dt_bias = _raw_inputs(g, T, H)
+    pool = torch.zeros(4, H, D, D, device=DEV)
+    cu = torch.tensor(_cu(lens), dtype=torch.int32)
+    meta = kda.prefill_prepare(cu, H, device=DEV)
+    args = [x[None].to(DEV) for x in (q, k, v, raw_g, raw_b)]
+    out = torch.empty(1, T, H, D, dtype=torch.bfloat16, device=DEV)
+    idx = torch.tensor([1, 2], dtype=torch.int32, device=DEV)
+    hi = torch.zeros(2, dtype=torch.bool, device=DEV)
+    cud, A, dtb = cu.to(DEV), A_log.to(DEV), dt_bias.to(DEV)
+    torch.cuda.synchronize()
+    torch.cuda.set_sync_debug_mode("error")
+    try:
+        kda.prefill(*args, A, dtb, D ** -0.5, -5.0, pool, idx, hi, cud, out, meta=meta,
+                    workspace=torch.empty(meta.workspace_bytes, dtype=torch.uint8, device=DEV))
+    finally:
+        torch.cuda.set_sync_debug_mode("default")
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
+
+
+@pytest.mark.parametrize("every", [64, 256])
+def test_every_n_checkpoints_fp32_and_bf16(oracle, every):
+    """B200 every-n rows (kda/b200/test_kda_b200.py:213-240): fp32 rows match the oracle; bf16 rows are exactly the
+    fp32 rows rounded to nearest even; output and pool are identical across checkpoint dtypes."""
+    kda = _kda()
+    H, lens = 4, [300, 64, 1, 1000, 77]
+    _say(f"every-n every={every}")
+    g = gen(50 + every)
+    T, N = sum(lens), len(lens)
+    q, k, v, raw_g, raw_b, A_log, dt_bias = _raw_inputs(g, T, H)
+    P = N + 3
+    pool0 = torch.randn(P, H, D, D, generator=g) * 0.25
+    idx = torch.randperm(P, generator=g)[:N].to(torch.int32)
+    counts = [-(-L // every) for L in lens]
+    ccs = torch.tensor(_cu(counts), dtype=torch.int64)
+    C = int(sum(counts))
+    got = {}
+    for dt in (torch.float32, torch.bfloat16):
+        pool = pool0.clone().to(DEV)
+        ck = torch.full((C, H, D, D), float("nan"), device=DEV, dtype=dt)
+        res = kda.kda_prefill(q[None].to(DEV), k[None].to(DEV), v[None].to(DEV), raw_g[None].to(DEV),
+                              raw_b[None].to(DEV), A_log.to(DEV), dt_bias.to(DEV), pool,
+                              torch.tensor(_cu(lens)).to(DEV), ssm_state_indices=idx.to(DEV), state_checkpoints=ck,
+                              checkpoint_cu_starts=ccs.to(DEV), checkpoint_every_n_tokens=every)
+        torch.cuda.synchronize()
+        assert len(res) == 3 and res[2] is ck and res[1] is pool
+        got[dt] = (res[0].clone(), pool.clone(), ck)
+    assert torch.equal(got[torch.float32][0], got[torch.bfloat16][0]), "output differs across checkpoint dtypes"
+    assert torch.equal(got[torch.float32][1], got[torch.bfloat16][1]), "pool differs across checkpoint dtypes"
+    assert torch.equal(got[torch.float32][2].to(torch.bfloat16), got[torch.bfloat16][2]), "bf16 rows != RNE(fp32 rows)"
+    qn, kn, vf, gl, bt = _oracle_gated(oracle, q, k, v, raw_g, raw_b, A_log, dt_bias)
+    S0 = f32(pool0)[idx.numpy()]
+    ro, rf, rows, starts = oracle.checkpoints_every_n(qn, kn, vf, gl, bt, _cu(lens), every, initial_state=S0,
+                                                      normalize_qk=False, precision=64)
+    assert list(starts) == list(ccs.numpy())
+    _check_out(got[torch.float32][0][0], ro, f"every={every}")
+    ck32 = f32(got[torch.float32][2])
+    ck16 = f32(got[torch.bfloat16][2])
+    for r in range(C):
+        assert rel_frob(ck32[r], rows[r]) <= STATE_TOL, f"fp32 checkpoint row {r}"
+        rne = oracle.bf16_round(rows[r])
+        assert rel_frob(ck16[r], rows[r]) <= rel_frob(rne, rows[r]) + STATE_TOL, f"bf16 checkpoint row {r}"
+    fin = f32(got[torch.float32][1])
+    for n in range(N):
+        assert rel_frob(fin[int(idx[n])], rf[n]) <= STATE_TOL
+
+
+def test_graph_capture_prefill(oracle):
+    """The launch is capturable: replay after refilling q/k/v/g/beta and the initial states in place."""
+    kda = _kda()
+    H, lens = 2, [200, 70]
+    T, N = sum(lens), len(lens)
+    _say("prefill graph capture")
+    g = gen(60)
+    cu = torch.tensor(_cu(lens), dtype=torch.int32)
+    meta = kda.plan(cu, H, device=DEV)
+    ws = torch.empty(meta.workspace_bytes, dtype=torch.uint8, device=DEV)
+    bufs = [torch.empty(1, T, H, D, dtype=torch.bfloat16, device=DEV) for _ in range(3)]
+    gbuf = torch.empty(1, T, H, D, device=DEV)
+    bbuf = torch.empty(1, T, H, device=DEV)
+    h0 = torch.empty(N, H, D, D, device=DEV)
+    out = torch.empty(1, T, H, D, dtype=torch.bfloat16, device=DEV)
+
+    def call():
+        return kda.chunk_kda(*bufs, gbuf, bbuf, initial_state=h0, meta=meta, out=out, workspace=ws)
+
+    q, k, v, gg, beta = config_inputs(T, H, g)
+    for b, x in zip(bufs, (q, k, v)):
+        b.copy_(x[None])
+    gbuf.copy_(gg[None])
+    bbuf.copy_(beta[None])
+    h0.zero_()
+    call()
+    torch.cuda.synchronize()
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr):
+        _, fin = call()
+    for rep in range(2):
+        q, k, v, gg, beta = config_inputs(T, H, g)
+        init = torch.randn(N, H, D, D, generator=g) * 0.02
+        for b, x in zip(bufs, (q, k, v)):
+            b.copy_(x[None])
+        gbuf.copy_(gg[None])
+        bbuf.copy_(beta[None])
+        h0.copy_(init)
+        torch.cuda.synchronize()
+        gr.replay()
+        torch.cuda.synchronize()
+        ro, rf = oracle.prefill_plain(f32(q), f32(k), f32(v), f32(gg), f32(beta), _cu(lens), initial_state=f32(init),
+                                      precision=64)
+        _check_out(out[0], ro, f"replay {rep}")
+        for n in range(N):
+            assert rel_frob(f32(fin[n]), rf[n]) <= STATE_TOL
+
+
+def test_prefill_errors():
+    kda = _kda()
+    H, T = 2, 10
+    q = torch.zeros(1, T, H, D, dtype=torch.bfloat16, device=DEV)
+    g = torch.zeros(1, T, H, D, device=DEV)
+    b = torch.zeros(1, T, H, device=DEV)
+    cu = torch.tensor([0, T], dtype=torch.int32, device=DEV)
+    with pytest.raises(TypeError):
+        kda.chunk_kda(q, q, q, g.double(), b, cu_seqlens=cu)
+    with pytest.raises(ValueError):
+        kda.chunk_kda(q, q, q, g, b, cu_seqlens=cu, initial_state=torch.zeros(2, H, D, D, device=DEV))
+    meta = kda.plan(torch.tensor([0, 5, T]), H, device=DEV)
+    with pytest.raises(ValueError):                      # meta of another layout
+        kda.chunk_kda(q[:, :5], q[:, :5], q[:, :5], g[:, :5], b[:, :5], meta=meta)
+    with pytest.raises(TypeError):
+        kda.chunk_kda(q.cpu(), q.cpu(), q.cpu(), g.cpu(), b.cpu())
