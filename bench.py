@@ -1,0 +1,401 @@
+#!/usr/bin/env python3
+"""KDA on one MI355X: chunked prefill throughput (the headline), recurrent decode, speculative verify, long prefill.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs c1,c3,c4,c2] [--cpu-seconds 10]
+
+Prints ONE JSON line on stdout.  `value` is the prefill throughput of configuration 1: the
+fla `chunk_kda` plain call over 8 varlen sequences (lengths U[256, 8192] from seed 1, 38,881 tokens), H = 32,
+head dim 128, bf16 q/k/v, fp32 g (log-decay) and beta (activated), fp32 initial states ~N(0, 0.02) -- in tokens/s,
+with every input resident in HBM before the timed region.  A step is one call over the whole batch.
+
+The other configurations are reported beside it (never as `value`):
+  decode       configs[3]: B = 256 x 1 token, H = 32, fp32 pool of 4096 slots, captured in a HIP graph, us/step
+  spec_verify  configs[4]: B = 64 x 4 draft tokens at H = 64 and 96, pool of 1024 slots, per-token states into a
+               [64*4, H, 128, 128] scratch, then the accepted length committed to the pool slot (one graph)
+  long_prefill configs[2]: one sequence of 131,072 tokens, H = 32, paged fp32 pool of 64 slots at a seeded slot,
+               bf16 checkpoints every 4096 tokens into 32 seeded rows
+
+Roofline: prefill is bound by HBM at these shapes (arithmetic intensity ~120 FLOP/B, below the bf16 ridge of ~312),
+so `roofline` is the HBM fraction of the prefill launch: compulsory bytes (q, k, v, out bf16; g fp32; beta fp32;
+initial + final states fp32) / the launch's average duration from HIP events on the launch stream.  The MFMA fraction
+of the chunked-matmul FLOPs is reported beside it.  `traffic` is the measured HBM bytes per launch from the committed
+rocprofv3 FETCH_SIZE / WRITE_SIZE summary (profiles/prefill_c1_traffic.md), or null.
+
+`cpu_baseline` times the CPU restatement of the reference's fp32 token recurrence (oracle/, OpenMP over the
+(sequence, head) chains) on the same configuration-1 workload on this host; it is a reported baseline, not the target.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import re
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (str(ROOT), str(ROOT / "eat-kernels_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "KDA prefill tok/s (H=32, 32K varlen) + decode µs/step B=256; % of roofline"
+D = 128
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+MFMA_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 / fp16 MFMA
+C1_LENS_SEED = 1
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+# ------------------------------------------------------------------------------------------------ work formulas
+def prefill_flops(lens):
+    """Chunked-matmul FLOPs: per chunk of c tokens per head 6cKV + 4c^2K + 2c^2K + 4c^2V + (2/3)c^3."""
+    K = V = D
+    tot = 0.0
+    for L in lens:
+        full, tail = divmod(int(L), 64)
+        for c, cnt in ((64, full), (tail, 1 if tail else 0)):
+            tot += cnt * (6 * c * K * V + 4 * c * c * K + 2 * c * c * K + 4 * c * c * V + (2.0 / 3.0) * c ** 3)
+    return tot
+
+
+def prefill_bytes(T, H, N, g_bytes=4, beta_bytes=4, init=True, ck_rows=0, ck_row_bytes=0):
+    """Compulsory HBM bytes: q, k, v, out (bf16), g, beta per token-head; state read (if any) + write per (seq, head);
+    checkpoint rows."""
+    per_tok = 3 * 2 * D + g_bytes * D + beta_bytes + 2 * D
+    return T * H * per_tok + N * H * D * D * 4 * (2 if init else 1) + ck_rows * H * ck_row_bytes
+
+
+def read_traffic(name):
+    """Measured HBM bytes per launch from a committed rocprofv3 summary (line `traffic_bytes_per_launch: N`)."""
+    f = ROOT / "profiles" / name
+    if not f.exists():
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", f.read_text())
+    return float(m.group(1)) if m else None
+
+
+# ------------------------------------------------------------------------------------------------ timing helpers
+def time_steps(fn, steps, warmup, torch):
+    """W untimed calls, then K calls bracketed by synchronize; HIP events on the current (launch) stream."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(steps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return e0.elapsed_time(e1) / steps, wall * 1e3 / steps
+
+
+def time_flushed(fn, reps, torch, flush):
+    """Median single-call latency after zeroing a 512 MiB buffer (clears L2 and the 256 MiB MALL)."""
+    ts = []
+    for _ in range(reps):
+        flush.zero_()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        fn()
+        b.record()
+        torch.cuda.synchronize()
+        ts.append(a.elapsed_time(b))
+    ts.sort()
+    return ts[len(ts) // 2]
+
+
+# ------------------------------------------------------------------------------------------------ inputs
+def c1_lens():
+    import numpy as np
+    rng = np.random.default_rng(C1_LENS_SEED)
+    return [int(x) for x in rng.integers(256, 8193, size=8)]
+
+
+def synth(T, H, dev, seed, torch):
+    """q, k: fp32 N(0,1) L2-normalized per (token, head) then bf16; v bf16 N(0,1); g = -softplus(N(0,1)) fp32;
+    beta = sigmoid(N(0,1)) fp32 (generated on the device)."""
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    out = []
+    for _ in range(2):
+        x = torch.randn(1, T, H, D, generator=gen, device=dev)
+        out.append(torch.nn.functional.normalize(x, dim=-1).bfloat16())
+        del x
+    out.append(torch.randn(1, T, H, D, generator=gen, device=dev).bfloat16())
+    g = torch.randn(1, T, H, D, generator=gen, device=dev)
+    out.append(-torch.nn.functional.softplus(g))
+    del g
+    out.append(torch.sigmoid(torch.randn(1, T, H, generator=gen, device=dev)))
+    return out
+
+
+# ------------------------------------------------------------------------------------------------ configurations
+def bench_c1(kda, torch, dev, steps, warmup, flush):
+    lens = c1_lens()
+    T, N, H = sum(lens), len(lens), 32
+    q, k, v, g, beta = synth(T, H, dev, 1, torch)
+    h0 = torch.randn(N, H, D, D, generator=torch.Generator(device=dev).manual_seed(2), device=dev) * 0.02
+    cu = torch.tensor([0] + list(__import__("itertools").accumulate(lens)), dtype=torch.int32)
+    meta = kda.plan(cu, H, device=dev)
+    ws = torch.empty(meta.workspace_bytes, dtype=torch.uint8, device=dev)
+    out = torch.empty(1, T, H, D, dtype=torch.bfloat16, device=dev)
+
+    def step():
+        return kda.chunk_kda(q, k, v, g, beta, initial_state=h0, output_final_state=True, meta=meta, out=out,
+                             workspace=ws)
+
+    ms, wall_ms = time_steps(step, steps, warmup, torch)
+    flushed = time_flushed(step, 10, torch, flush)
+    flops = prefill_flops(lens) * H
+    nbytes = prefill_bytes(T, H, N)
+    res = dict(lens=lens, T=T, N=N, H=H, ms=ms, wall_ms=wall_ms, flushed_ms=flushed, flops=flops, bytes=nbytes,
+               workspace_bytes=meta.workspace_bytes)
+    cpu_inputs = (q, k, v, g, beta, h0, cu)
+    return res, cpu_inputs
+
+
+def bench_decode(kda, torch, dev, steps, warmup):
+    B, H, slots = 256, 32, 4096
+    gen = torch.Generator(device=dev).manual_seed(3)
+    q, k, v, g, beta = synth(B, H, dev, 3, torch)
+    pool = torch.empty(slots, H, D, D, device=dev)
+    pool.normal_(0.0, 0.05, generator=gen)
+    idx = (torch.randperm(slots - 1, generator=torch.Generator().manual_seed(3))[:B] + 1).to(torch.int32).to(dev)
+    cu = torch.arange(0, B + 1, dtype=torch.int32, device=dev)
+    out = torch.empty(1, B, H, D, dtype=torch.bfloat16, device=dev)
+
+    def call():
+        kda.fused_recurrent_kda(q, k, v, g, beta, initial_state=pool, cu_seqlens=cu, ssm_state_indices=idx, out=out)
+
+    call()
+    torch.cuda.synchronize()
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr):
+        call()
+    ms, wall_ms = time_steps(gr.replay, steps * 5, warmup * 5, torch)
+    state_bytes = B * H * D * D * 4 * 2
+    other = B * H * (3 * D * 2 + D * 4 + 4 + D * 2)
+    del pool
+    return dict(B=B, H=H, slots=slots, us=ms * 1e3, wall_us=wall_ms * 1e3, state_bytes=state_bytes,
+                other_bytes=other)
+
+
+def bench_spec(kda, torch, dev, steps, warmup, H):
+    B, S, slots = 64, 4, 1024
+    T = B * S
+    gen = torch.Generator(device=dev).manual_seed(4 + H)
+    q, k, v, g, beta = synth(T, H, dev, 4 + H, torch)
+    pool = torch.empty(slots, H, D, D, device=dev)
+    pool.normal_(0.0, 0.05, generator=gen)
+    cpu = torch.Generator().manual_seed(4 + H)
+    slot = torch.randperm(slots - 1, generator=cpu)[:B] + 1
+    acc = torch.randint(1, S + 1, (B,), generator=cpu)
+    read_idx = slot.view(B, 1).expand(B, S).contiguous().to(torch.int32).to(dev)   # every entry = the sequence's slot
+    scratch = torch.empty(T, H, D, D, device=dev)                                  # [64, 4, H, 128, 128] as rows
+    scratch_idx = torch.arange(T, dtype=torch.int32, device=dev).view(B, S)
+    pool_idx = slot.to(torch.int32).to(dev)
+    accd = acc.to(torch.int32).to(dev)
+    cu = torch.arange(0, T + 1, S, dtype=torch.int32, device=dev)
+    out = torch.empty(1, T, H, D, dtype=torch.bfloat16, device=dev)
+
+    def verify():
+        kda.fused_recurrent_kda(q, k, v, g, beta, initial_state=pool, cu_seqlens=cu, ssm_state_indices=read_idx,
+                                num_accepted_tokens=accd, out=out, write_pool=scratch, write_indices=scratch_idx)
+
+    def commit():
+        kda.spec_commit(scratch, scratch_idx, pool, pool_idx, accd)
+
+    verify()
+    commit()
+    torch.cuda.synchronize()
+    g1, g2 = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g1):
+        verify()
+    with torch.cuda.graph(g2):
+        verify()
+        commit()
+    ms_v, _ = time_steps(g1.replay, steps * 5, warmup * 5, torch)
+    ms_vc, _ = time_steps(g2.replay, steps * 5, warmup * 5, torch)
+    vb = B * H * D * D * 4 * (1 + S)
+    cb = B * H * D * D * 4 * 2
+    del pool, scratch
+    return dict(B=B, S=S, H=H, slots=slots, verify_us=ms_v * 1e3, verify_commit_us=ms_vc * 1e3, verify_bytes=vb,
+                commit_bytes=cb)
+
+
+def bench_c2(kda, torch, dev, steps, warmup):
+    T, H, slots, every, nck = 131072, 32, 64, 4096, 32
+    q, k, v, g, beta = synth(T, H, dev, 5, torch)
+    cpu = torch.Generator().manual_seed(5)
+    perm = torch.randperm(slots, generator=cpu)
+    slot = perm[:1].to(torch.int32).to(dev)
+    pool = torch.empty(slots, H, D, D, device=dev)
+    pool.normal_(0.0, 0.02, generator=torch.Generator(device=dev).manual_seed(5))
+    ck_rows = (torch.randperm(64, generator=cpu)[:nck]).to(torch.int32).to(dev)
+    ck = torch.empty(64, H, D, D, dtype=torch.bfloat16, device=dev)
+    cu = torch.tensor([0, T], dtype=torch.int64)
+    meta = kda.plan(cu, H, ck_every=every, device=dev)
+    ws = torch.empty(meta.workspace_bytes, dtype=torch.uint8, device=dev)
+    out = torch.empty(1, T, H, D, dtype=torch.bfloat16, device=dev)
+
+    def step():
+        kda.chunk_kda(q, k, v, g, beta, initial_state=pool, meta=meta, out=out, workspace=ws, ssm_state_indices=slot,
+                      state_checkpoints=ck, checkpoint_every_n_tokens=every, checkpoint_state_indices=ck_rows)
+
+    ms, wall_ms = time_steps(step, max(1, steps // 4), max(1, warmup), torch)
+    flops = prefill_flops([T]) * H
+    nbytes = prefill_bytes(T, H, 1, ck_rows=nck, ck_row_bytes=D * D * 2)
+    del pool, ws, q, k, v, g, beta
+    return dict(T=T, H=H, ms=ms, wall_ms=wall_ms, flops=flops, bytes=nbytes, tok_s=T / (ms * 1e-3),
+                hbm_frac=nbytes / (ms * 1e-3) / (HBM_PEAK_GBS * 1e9),
+                mfma_frac=flops / (ms * 1e-3) / (MFMA_PEAK_TFLOPS * 1e12))
+
+
+# ------------------------------------------------------------------------------------------------ CPU baseline
+def cpu_baseline(inputs, lens, seconds, torch):
+    """The oracle's fp32 token recurrence (OpenMP over (sequence, head) chains) on the whole configuration-1
+    workload, repeated for about `seconds`; tokens/s of one pass."""
+    import numpy as np
+
+    from oracle import oracle as O
+    q, k, v, g, beta, h0, cu = inputs
+    f = lambda t: np.ascontiguousarray(t[0].float().cpu().numpy()) if t.dim() >= 3 and t.shape[0] == 1 else \
+        np.ascontiguousarray(t.float().cpu().numpy())  # noqa: E731
+    qn, kn, vv, gg, bb = f(q), f(k), f(v), f(g), f(beta)
+    S0 = np.ascontiguousarray(h0.cpu().numpy())
+    cun = cu.numpy().astype(np.int64)
+    T = int(cun[-1])
+    threads = O.max_threads()
+    passes = []
+    t_end = time.perf_counter() + seconds
+    while True:
+        t0 = time.perf_counter()
+        qq, kk = O.l2norm_clamp(qn), O.l2norm_clamp(kn)
+        O.chains(qq, kk, vv, gg, bb, cun, D ** -0.5, S0, precision=32, nthreads=threads)
+        passes.append(time.perf_counter() - t0)
+        if time.perf_counter() >= t_end or len(passes) >= 50:
+            break
+    med = sorted(passes)[len(passes) // 2]
+    model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": T / med, "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"the whole configuration-1 workload ({T} tokens x 32 heads, fp32 token recurrence of "
+                      f"kda/mi350x/reference.py:85-91 restated in C, OpenMP over the 256 (sequence, head) chains), "
+                      f"{len(passes)} passes, median {med:.3f} s; host: {model}, nproc {os.cpu_count()}"}
+
+
+# ------------------------------------------------------------------------------------------------ main
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--configs", default="c1,c3,c4,c2")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="also run a 1 GiB device-to-device copy 5x (the known-size kernel for HBM counter scaling)")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE {world}); the "
+              "multi-GPU split of the path is a design note, not a measured configuration", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import kda355
+    kda355.lib()  # fails loudly without the HIP library
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    cfgs = set(args.configs.split(","))
+    flush = torch.empty(512 * 1024 * 1024 // 4, dtype=torch.float32, device=dev)
+
+    if args.calib_copy:
+        a = torch.empty(1 << 28, dtype=torch.float32, device=dev)
+        b = torch.empty_like(a)
+        a.fill_(1.0)
+        for _ in range(5):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        log("calibration copy: 5 x 1 GiB read + 1 GiB write")
+        del a, b
+
+    log(f"c1 prefill: steps {args.steps} warmup {args.warmup}")
+    c1, cpu_inputs = bench_c1(kda355, torch, dev, args.steps, args.warmup, flush)
+    log(f"c1: {c1['ms']:.3f} ms/step (flushed median {c1['flushed_ms']:.3f} ms)")
+    extra = {}
+    if "c3" in cfgs:
+        d = bench_decode(kda355, torch, dev, args.steps, args.warmup)
+        gbs = d["state_bytes"] / (d["us"] * 1e-6) / 1e9
+        extra["decode"] = {"config": "configs[3]: B=256 x 1 token, H=32, fp32 pool 4096 slots, HIP graph replay",
+                           "us_per_step": round(d["us"], 2), "state_bytes": d["state_bytes"],
+                           "other_bytes": d["other_bytes"], "achieved_GBs": round(gbs, 1),
+                           "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+        log(f"decode: {d['us']:.1f} us/step, {gbs:.0f} GB/s state traffic")
+    if "c4" in cfgs:
+        rows = []
+        for H in (64, 96):
+            s = bench_spec(kda355, torch, dev, args.steps, args.warmup, H)
+            gbs = s["verify_bytes"] / (s["verify_us"] * 1e-6) / 1e9
+            gbs2 = (s["verify_bytes"] + s["commit_bytes"]) / (s["verify_commit_us"] * 1e-6) / 1e9
+            rows.append({"H": H, "B": s["B"], "S": s["S"], "verify_us": round(s["verify_us"], 2),
+                         "verify_GBs": round(gbs, 1), "verify_hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+                         "verify_commit_us": round(s["verify_commit_us"], 2),
+                         "verify_commit_GBs": round(gbs2, 1)})
+            log(f"spec H={H}: verify {s['verify_us']:.1f} us ({gbs:.0f} GB/s), +commit {s['verify_commit_us']:.1f} us")
+        extra["spec_verify"] = rows
+    if "c2" in cfgs:
+        c2 = bench_c2(kda355, torch, dev, args.steps, args.warmup)
+        extra["long_prefill"] = {"config": "configs[2]: T=131072, H=32, pool slot, bf16 checkpoints every 4096 tokens",
+                                 "ms_per_step": round(c2["ms"], 3), "tok_s": round(c2["tok_s"], 1),
+                                 "hbm_frac": round(c2["hbm_frac"], 4), "mfma_frac": round(c2["mfma_frac"], 4)}
+        log(f"c2: {c2['ms']:.3f} ms/step")
+
+    cpu = None
+    if args.cpu_seconds > 0:
+        log("cpu baseline")
+        cpu = cpu_baseline(cpu_inputs, c1["lens"], args.cpu_seconds, torch)
+
+    s = c1["ms"] * 1e-3
+    achieved = c1["bytes"] / s / 1e9
+    tflops = c1["flops"] / s / 1e12
+    traffic = read_traffic("prefill_c1_traffic.md")
+    line = {
+        "metric": METRIC, "value": round(c1["T"] / s, 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(c1["ms"], 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "fp16-mfma/fp32-state (bf16 io)", "data": "synthetic",
+        "config": {"workload": "configs[1]: chunk_kda plain call, 8 varlen sequences (lengths U[256,8192] seed 1: "
+                               f"{c1['lens']}), T={c1['T']}, H=32, D=128, bf16 q/k/v, fp32 g/beta, fp32 initial "
+                               "states, final states returned",
+                   "global_batch": c1["N"], "seq_len": c1["T"], "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "algorithmic_bytes": c1["bytes"],
+                     "kernel": "prefill launch (chunk prologue + chain walk kernels)",
+                     "mfma": {"achieved": round(tflops, 2), "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                              "frac": round(tflops / MFMA_PEAK_TFLOPS, 4), "flops": c1["flops"]}},
+        "cpu_baseline": cpu,
+        "prefill_flushed_median_ms": round(c1["flushed_ms"], 4),
+        "wall_ms_per_step": round(c1["wall_ms"], 4),
+    }
+    line.update(extra)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

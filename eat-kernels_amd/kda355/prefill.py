@@ -180,104 +180,80 @@ def _check_qkv(q, k, v):
     return dev, T, H
 
 
-def chunk_kda(q, k, v, g, beta, scale=None, initial_state=None, output_final_state=True, cu_seqlens=None,
-              use_qk_l2norm_in_kernel=True, use_gate_in_kernel=False, use_beta_sigmoid_in_kernel=False,
-              A_log=None, dt_bias=None, lower_bound=-5.0, state_v_first=True, meta=None, out=None, workspace=None,
-              **unused):
-    """fla chunk_kda plain call. q, k, v [1, T, H, 128] bf16; g [1, T, H, 128] (fp32 log-decay, or the raw gate with
-    use_gate_in_kernel); beta [1, T, H] (fp32 activated, or logits with use_beta_sigmoid_in_kernel); initial_state
-    [N, H, 128(V), 128(K)] fp32 or None; cu_seqlens [N+1] (None: one sequence).  meta: a plan(...) result for this
-    layout (skips the host read of cu_seqlens).  Returns (o [1, T, H, 128] bf16, final_state [N, H, 128, 128] fp32
-    or None)."""
-    if not state_v_first:
-        raise ValueError("kda355: only the value-first state layout [N, H, V, K] is supported (state_v_first=True)")
-    dev, T, H = _check_qkv(q, k, v)
-    if scale is None:
-        scale = D ** -0.5
-    flags = PF_NORMALIZE_QK if use_qk_l2norm_in_kernel else 0
-    if use_gate_in_kernel:
-        _need("g", g, torch.bfloat16 if g.dtype == torch.bfloat16 else torch.float32, dev)
+def _gates(dev, T, H, g, beta, raw_gate, raw_beta, A_log, dt_bias):
+    """Validates the gate / beta inputs; returns (g, beta, A_log, dt_bias, flags)."""
+    flags = 0
+    if raw_gate:
+        if not isinstance(g, torch.Tensor):
+            raise TypeError("kda355: the gate must be a tensor")
         if g.dtype != torch.bfloat16:
             g = g.bfloat16()
+        _need("raw_g", g, torch.bfloat16, dev)
         flags |= PF_RAW_GATE
         if A_log is None or dt_bias is None:
-            raise ValueError("kda355: use_gate_in_kernel needs A_log and dt_bias")
+            raise ValueError("kda355: the in-kernel gate needs A_log and dt_bias")
         _need("A_log", A_log, torch.float32, dev)
         _need("dt_bias", dt_bias, torch.float32, dev)
-        A_log, dt_bias = A_log.reshape(-1).contiguous(), dt_bias.reshape(-1).contiguous()
         if A_log.numel() != H or dt_bias.numel() != H * D:
             raise ValueError("kda355: A_log must be [H] and dt_bias [H*128]")
+        A_log, dt_bias = A_log.reshape(-1).contiguous(), dt_bias.reshape(-1).contiguous()
     else:
         _need("g", g, torch.float32, dev)
+        A_log = dt_bias = None
     _tok_rows("g", g, T, H, D)
-    if use_beta_sigmoid_in_kernel:
+    if raw_beta:
+        if not isinstance(beta, torch.Tensor):
+            raise TypeError("kda355: beta must be a tensor")
         if beta.dtype != torch.bfloat16:
             beta = beta.bfloat16()
+        _need("raw_beta", beta, torch.bfloat16, dev)
         flags |= PF_RAW_BETA
     else:
         _need("beta", beta, torch.float32, dev)
     _tok_rows("beta", beta, T, H, 0)
-    if meta is None:
+    return g, beta, A_log, dt_bias, flags
+
+
+def _run_plain(q, k, v, g, beta, scale, initial_state, cu_seqlens, lower_bound, meta, out, workspace, flags, A_log,
+               dt_bias, ssm_state_indices, state_checkpoints, checkpoint_cu_starts, checkpoint_every_n_tokens,
+               checkpoint_state_indices):
+    """The plain call with the B200 serving keywords (kda/b200/kda_b200.py:15-24).  Returns (out, final, ck, meta)."""
+    dev, T, H = q.device, q.shape[1], q.shape[2]
+    every = int(checkpoint_every_n_tokens or 0)
+    if every:
+        if every % CHUNK:
+            raise ValueError("kda355: checkpoint_every_n_tokens must be a multiple of 64")
+        if state_checkpoints is None or (checkpoint_cu_starts is None) == (checkpoint_state_indices is None):
+            raise ValueError("kda355: every-n checkpoints need state_checkpoints and exactly one of "
+                             "checkpoint_cu_starts / checkpoint_state_indices")
+    if meta is None or meta.ck_every != every:
+        if meta is not None and cu_seqlens is None:
+            cu_seqlens = torch.as_tensor(np.concatenate([[0], np.cumsum(meta.lens)]))
         cu = torch.tensor([0, T], dtype=torch.int64) if cu_seqlens is None else cu_seqlens
-        meta = plan(cu, H, device=dev)
+        meta = plan(cu, H, ck_every=every, device=dev)
     N = meta.N
-    if initial_state is not None:
-        _need("initial_state", initial_state, torch.float32, dev)
-        if tuple(initial_state.shape) != (N, H, D, D):
-            raise ValueError(f"kda355: initial_state must be [{N}, {H}, 128, 128], got {list(initial_state.shape)}")
-        initial_state = initial_state.contiguous()
     if out is None:
         out = torch.empty(1, T, H, D, dtype=torch.bfloat16, device=dev)
     else:
         _need("out", out, torch.bfloat16, dev)
         _tok_rows("out", out, T, H, D)
-    final = torch.empty(N, H, D, D, dtype=torch.float32, device=dev)
-    _launch(meta, q, k, v, g, beta, out, flags, scale, lower_bound, A_log, dt_bias, init=initial_state, final=final,
-            workspace=workspace)
-    return out, (final if output_final_state else None)
-
-
-def kda_prefill(q, k, v, raw_g, raw_beta, A_log, dt_bias, initial_state, cu_seqlens=None, scale=None,
-                lower_bound=-5.0, meta=None, *, ssm_state_indices=None, state_checkpoints=None,
-                checkpoint_cu_starts=None, checkpoint_every_n_tokens=0):
-    """kda/mi350x_plain/kda_mi350x.py:37-46 (gates, beta sigmoid and q/k norm in the kernel) with the B200 serving
-    keywords (kda/b200/kda_b200.py:15-24):
-      ssm_state_indices int32 [N]: initial_state is a pool [P, H, 128, 128]; sequence i reads and updates slot
-          ssm_state_indices[i] in place and the returned final state is the pool itself;
-      state_checkpoints fp32 / bf16 [C, H, 128, 128] with checkpoint_cu_starts int64 [N+1] and
-          checkpoint_every_n_tokens n (multiple of 64): row checkpoint_cu_starts[i] + j = state before token j*n.
-    Returns (output, final_state) or (output, final_state, state_checkpoints)."""
-    dev, T, H = _check_qkv(q, k, v)
-    if scale is None:
-        scale = D ** -0.5
-    _need("raw_g", raw_g, torch.bfloat16, dev)
-    _tok_rows("raw_g", raw_g, T, H, D)
-    _need("raw_beta", raw_beta, torch.bfloat16, dev)
-    _tok_rows("raw_beta", raw_beta, T, H, 0)
-    _need("A_log", A_log, torch.float32, dev)
-    _need("dt_bias", dt_bias, torch.float32, dev)
-    if A_log.numel() != H or dt_bias.numel() != H * D:
-        raise ValueError("kda355: A_log must be [H] and dt_bias [H*128]")
-    A_log, dt_bias = A_log.reshape(-1).contiguous(), dt_bias.reshape(-1).contiguous()
-    every = int(checkpoint_every_n_tokens or 0)
-    if every and (every % CHUNK or state_checkpoints is None or checkpoint_cu_starts is None):
-        raise ValueError("kda355: checkpoints need state_checkpoints, checkpoint_cu_starts and n a multiple of 64")
-    if meta is None or (every and meta.ck_every != every):
-        cu = torch.tensor([0, T], dtype=torch.int64) if cu_seqlens is None else cu_seqlens
-        meta = plan(cu, H, ck_every=every, device=dev)
-    N = meta.N
-    flags = PF_NORMALIZE_QK | PF_RAW_GATE | PF_RAW_BETA
-    out = torch.empty(1, T, H, D, dtype=torch.bfloat16, device=dev)
-    ck_pool = ck_idx = None
-    ck_bf16 = False
+    ck = {}
     if every:
         if state_checkpoints.dtype not in (torch.float32, torch.bfloat16) or state_checkpoints.device != dev:
             raise TypeError("kda355: state_checkpoints must be fp32 or bf16 on the device")
-        ck_bf16 = state_checkpoints.dtype == torch.bfloat16
-        ck_pool = state_checkpoints
-        starts = checkpoint_cu_starts.to(device=dev, dtype=torch.int64)
-        counts = (meta.lens + every - 1) // every
-        ck_idx = _ck_row_table(starts[:-1], counts, dev)
+        if checkpoint_state_indices is not None:
+            # explicit row table: row checkpoint_state_indices[r] receives the r-th checkpoint (sequence-major)
+            _need("checkpoint_state_indices", checkpoint_state_indices, torch.int32, dev)
+            if checkpoint_state_indices.dim() != 1 or not checkpoint_state_indices.is_contiguous() or \
+                    checkpoint_state_indices.numel() < meta.ck_rows:
+                raise ValueError(f"kda355: checkpoint_state_indices must be a contiguous int32 tensor of >= "
+                                 f"{meta.ck_rows} rows")
+            ck_idx = checkpoint_state_indices
+        else:
+            starts = checkpoint_cu_starts.to(device=dev, dtype=torch.int64)
+            counts = (meta.lens + every - 1) // every
+            ck_idx = _ck_row_table(starts[:-1], counts, dev)
+        ck = dict(ck_pool=state_checkpoints, ck_idx=ck_idx, ck_bf16=state_checkpoints.dtype == torch.bfloat16)
         flags |= PF_CK_EVERY
     if ssm_state_indices is not None:
         pool = initial_state
@@ -286,20 +262,74 @@ def kda_prefill(q, k, v, raw_g, raw_beta, A_log, dt_bias, initial_state, cu_seql
         if ssm_state_indices.dim() != 1 or ssm_state_indices.numel() != N or not ssm_state_indices.is_contiguous():
             raise ValueError("kda355: ssm_state_indices must be a contiguous int32 [N] tensor")
         has_init = torch.ones(N, dtype=torch.bool, device=dev)
-        _launch(meta, q, k, v, raw_g, raw_beta, out, flags, scale, lower_bound, A_log, dt_bias, pool=pool,
-                idx=ssm_state_indices, has_init=has_init, ck_pool=ck_pool, ck_idx=ck_idx, ck_bf16=ck_bf16)
+        _launch(meta, q, k, v, g, beta, out, flags, scale, lower_bound, A_log, dt_bias, pool=pool,
+                idx=ssm_state_indices, has_init=has_init, workspace=workspace, **ck)
         final = pool
     else:
         init = None
         if initial_state is not None and initial_state.numel():
             _need("initial_state", initial_state, torch.float32, dev)
             if tuple(initial_state.shape) != (N, H, D, D):
-                raise ValueError(f"kda355: initial_state must be [{N}, {H}, 128, 128]")
+                raise ValueError(f"kda355: initial_state must be [{N}, {H}, 128, 128], got {list(initial_state.shape)}")
             init = initial_state.contiguous()
         final = torch.empty(N, H, D, D, dtype=torch.float32, device=dev)
-        _launch(meta, q, k, v, raw_g, raw_beta, out, flags, scale, lower_bound, A_log, dt_bias, init=init, final=final,
-                ck_pool=ck_pool, ck_idx=ck_idx, ck_bf16=ck_bf16)
-    return (out, final, state_checkpoints) if every else (out, final)
+        _launch(meta, q, k, v, g, beta, out, flags, scale, lower_bound, A_log, dt_bias, init=init, final=final,
+                workspace=workspace, **ck)
+    return out, final, (state_checkpoints if every else None), meta
+
+
+def chunk_kda(q, k, v, g, beta, scale=None, initial_state=None, output_final_state=True, cu_seqlens=None,
+              use_qk_l2norm_in_kernel=True, use_gate_in_kernel=False, use_beta_sigmoid_in_kernel=False,
+              A_log=None, dt_bias=None, lower_bound=-5.0, state_v_first=True, meta=None, out=None, workspace=None,
+              *, ssm_state_indices=None, state_checkpoints=None, checkpoint_cu_starts=None,
+              checkpoint_every_n_tokens=0, checkpoint_state_indices=None, **unused):
+    """fla chunk_kda plain call. q, k, v [1, T, H, 128] bf16; g [1, T, H, 128] (fp32 log-decay, or the raw gate with
+    use_gate_in_kernel); beta [1, T, H] (fp32 activated, or logits with use_beta_sigmoid_in_kernel); initial_state
+    [N, H, 128(V), 128(K)] fp32 or None; cu_seqlens [N+1] (None: one sequence).  meta: a plan(...) result for this
+    layout (skips the host read of cu_seqlens).  Returns (o [1, T, H, 128] bf16, final_state [N, H, 128, 128] fp32
+    or None).
+
+    Serving keywords (the B200 contract, kda/b200/kda_b200.py:15-24):
+      ssm_state_indices int32 [N]: initial_state is a pool [P, H, 128, 128]; sequence i reads and updates slot
+          ssm_state_indices[i] in place (every other slot is untouched) and the returned final state is the pool;
+      state_checkpoints fp32 / bf16 [C, H, 128, 128] with checkpoint_every_n_tokens n (a multiple of 64) and either
+          checkpoint_cu_starts int64 [N+1] (row checkpoint_cu_starts[i] + j = state before token j*n of sequence i,
+          j < ceil(len_i / n)) or checkpoint_state_indices int32 [>= rows] (the r-th such state, sequence-major, goes to
+          row checkpoint_state_indices[r]); bf16 rows are the fp32 states rounded to nearest even.
+    With checkpoints the call returns (o, final_state, state_checkpoints)."""
+    if not state_v_first:
+        raise ValueError("kda355: only the value-first state layout [N, H, V, K] is supported (state_v_first=True)")
+    dev, T, H = _check_qkv(q, k, v)
+    if scale is None:
+        scale = D ** -0.5
+    g, beta, A_log, dt_bias, flags = _gates(dev, T, H, g, beta, use_gate_in_kernel, use_beta_sigmoid_in_kernel,
+                                            A_log, dt_bias)
+    if use_qk_l2norm_in_kernel:
+        flags |= PF_NORMALIZE_QK
+    out, final, ck, _ = _run_plain(q, k, v, g, beta, scale, initial_state, cu_seqlens, lower_bound, meta, out,
+                                   workspace, flags, A_log, dt_bias, ssm_state_indices, state_checkpoints,
+                                   checkpoint_cu_starts, checkpoint_every_n_tokens, checkpoint_state_indices)
+    if ck is not None:
+        return out, final, ck
+    return out, (final if output_final_state else None)
+
+
+def kda_prefill(q, k, v, raw_g, raw_beta, A_log, dt_bias, initial_state, cu_seqlens=None, scale=None,
+                lower_bound=-5.0, meta=None, *, ssm_state_indices=None, state_checkpoints=None,
+                checkpoint_cu_starts=None, checkpoint_every_n_tokens=0, checkpoint_state_indices=None):
+    """kda/mi350x_plain/kda_mi350x.py:37-46 (gates, beta sigmoid and q/k norm in the kernel) with the B200 serving
+    keywords of chunk_kda (kda/b200/kda_b200.py:15-24).  raw_g [1, T, H, 128] bf16, raw_beta [1, T, H] bf16 logits,
+    A_log [H], dt_bias [H*128] fp32.  Returns (output, final_state) or (output, final_state, state_checkpoints)."""
+    dev, T, H = _check_qkv(q, k, v)
+    if scale is None:
+        scale = D ** -0.5
+    _need("raw_g", raw_g, torch.bfloat16, dev)
+    _need("raw_beta", raw_beta, torch.bfloat16, dev)
+    g, beta, A_log, dt_bias, flags = _gates(dev, T, H, raw_g, raw_beta, True, True, A_log, dt_bias)
+    out, final, ck, _ = _run_plain(q, k, v, g, beta, scale, initial_state, cu_seqlens, lower_bound, meta, None, None,
+                                   flags | PF_NORMALIZE_QK, A_log, dt_bias, ssm_state_indices, state_checkpoints,
+                                   checkpoint_cu_starts, checkpoint_every_n_tokens, checkpoint_state_indices)
+    return (out, final, ck) if ck is not None else (out, final)
 
 
 def _ck_row_table(starts, counts, dev):
