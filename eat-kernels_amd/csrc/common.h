@@ -24,11 +24,10 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 // bf16 bits <-> fp32 (the bf16 value widened exactly)
 __device__ __forceinline__ float bf2f(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
-// fp32 -> bf16 bits, round to nearest even (finite inputs; NaN stays NaN)
+// fp32 -> bf16 bits, round to nearest even (gfx950 converts in hardware: v_cvt_pk_bf16_f32)
 __device__ __forceinline__ uint32_t f2bf(float x) {
-    const uint32_t u = __float_as_uint(x);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
-    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+    const __bf16 b = (__bf16)x;
+    return (uint32_t)__builtin_bit_cast(uint16_t, b);
 }
 
 // DPP lane moves inside a row of 16 lanes (quad_perm / row_half_mirror / row_mirror).

@@ -1,35 +1,36 @@
-// Chunked KDA prefill on gfx950 (chunk 64, head dim 128): host plan, chunk prologue kernel, chain walk kernel.
+// Chunked KDA prefill on gfx950 (chunk 64, head dim 128): host plan and one fused chunk kernel.
 //
 // Math (per sequence n, head h, chunk of c <= 64 tokens; Gamma = inclusive cumsum of the log-decay g over the chunk,
-// per key channel; S the fp32 state, K-major in the formulas, V-major in memory):
+// per key channel; S the fp32 state, K-major [k][v] in the formulas, V-major [v][k] in memory):
 //     A_kk = strict_tril(diag(beta) (K e^{Gamma}) (K e^{-Gamma})^T),   A_qk = tril((Q e^{Gamma}) (K e^{-Gamma})^T)
-//     T    = (I + A_kk)^-1
-//     W    = T diag(beta) (K e^{Gamma}),   U = T diag(beta) V
-//     Qp   = Q e^{Gamma} - A_qk W,          Oi = A_qk U                  (so that O = scale (Qp S + Oi))
-//     Kd   = K e^{Gamma_c - Gamma},         decay = e^{Gamma_c}
-//   per chunk, serially:  V' = U - W S;   O = scale (Qp S + Oi);   S <- diag(decay) S + Kd^T V'
+//     W = (I + A_kk)^-1 diag(beta) K e^{Gamma},   U = (I + A_kk)^-1 diag(beta) V
+//     V' = U - W S;   O = scale (Q e^{Gamma} S + A_qk V');   S <- diag(e^{Gamma_c}) S + (K e^{Gamma_c - Gamma})^T V'
 // This is the token recurrence of kda/mi350x/reference.py:85-91 regrouped per chunk (the chunked WY form; the same
 // operator as kda/b200/csrc/w3/base/tiny/kda_tiny.cu:5-10 and vLLM's qg / w / u / kg_t / decay decomposition,
-// kda/mi350x/benchmark/baselines/prefill/vllm_reference/kda_chunk.py:73-76, 97-108).  Folding A_qk W into Qp takes
-// the A_qk V' product off the serial path.
+// kda/mi350x/benchmark/baselines/prefill/vllm_reference/kda_chunk.py:73-76, 97-108).
 //
-// Precision plan (from a numerical model of this exact form): every MFMA operand is fp16 (11-bit significand; bf16
-// operands miss the 1e-3 state bar) with fp32 accumulation, except the diagonal 16 x 16 blocks of A_kk / A_qk, whose
-// gated operands span e^{+-8|g|} and are taken as bf16 hi + lo pairs (3 MFMAs: hi.hi + hi.lo + lo.hi).  Off-diagonal
-// blocks use the last row of the previous block as the reference point, so both gated operands are <= 1 (no overflow,
-// only harmless underflow).  T is solved in fp32 (16 x 16 forward substitution + fp32 block products).  The state is
-// fp32 throughout and is rounded to fp16 only as the B operand of W S / Qp S.
-// Range note: fp16 operands hold |values| < 65504: the state, v and U must stay below that (the reference's relay has
-// the same window, kda/mi350x/kda/kernel.py:113-128).  The diagonal blocks need |Gamma_i - Gamma_m| < 88 over 8
-// tokens, i.e. a per-token log-decay above ~ -11 (always true for gate-in-kernel calls with lower_bound >= -11).
-//
-// Kernel 1, prologue: one workgroup (256 threads) per (chunk, head); writes the chunk's operands to the workspace.
-// Kernel 2, walk: one workgroup (4 wave64) per (sequence, head); wave w owns value columns [32w, 32w + 32) and keeps
-//   its 128 x 32 slice of S in MFMA accumulator registers for the whole sequence.  MFMA v_mfma_f32_16x16x32_f16:
-//   A lane l holds row l%16, k-slots 8(l/16)..+7; B lane l holds column l%16, the same k-slots; C lane l holds rows
-//   4(l/16)..+3 of column l%16.  Using the C layout of one product as the B operand of the next (no LDS round trip)
-//   makes a lane's 8 k-slots the rows {4g..4g+3, 16+4g..16+4g+3} of a 32-row block (g = l/16); the workspace stores
-//   W / Qp (channels) and Kd^T (tokens) in that permuted order so each A fragment is one 16-byte load.
+// One workgroup of 512 threads (8 wave64) walks the chunks of one (sequence, head) and keeps everything of a chunk
+// on chip: the only HBM traffic is q, k, v, g, beta in, o out, and the state in / out / checkpoints.  The next
+// chunk's inputs are prefetched into registers while the current chunk is processed.  Per chunk:
+//   P0  raw rows -> LDS (gate), row norms (DPP)          thread (r = tid / 8, channels 16 (tid % 8) .. + 15)
+//   P1  in-chunk gate cumsum, 4 segments of 16 rows      thread (channel tid % 128, segment tid / 128)
+//   P2  per-element factors fi = e^{Gamma_i - Gamma_m}, fj = 1 / fi with m the middle row of the 16-row block,
+//       and the per-channel block factors (a, b, x, y, decay) -- two exponentials per element
+//   P4  Gram tiles on MFMA: the four diagonal 16 x 16 blocks from bf16 hi + lo operands (3 MFMAs: hi.hi + hi.lo +
+//       lo.hi; their gated operands span e^{+-8|g|}), the six off-diagonal blocks from fp16 operands <= 1 (the
+//       reference point is the last row before the row block)
+//   P5  diagonal-block inverses (I + L_II)^-1 by forward substitution (fp32); Q e^Gamma, K e^{Gamma_c - Gamma}
+//       and beta V to LDS in the walk's operand layouts
+//   P6  W and U by block forward substitution on MFMA: X_I = T_II (B_I - sum_{J<I} A_IJ X_J); wave w owns key
+//       channels [16w, 16w+16) of W and value columns [16w, 16w+16) of U, so no wave waits for another
+//   P7  the walk: wave w keeps the 128 x 16 slice S[:, 16w:16w+16] in fp32 registers (MFMA C layout) for the whole
+//       sequence; V' = U - W S, O = scale (Q~ S + A_qk V'), S = diag(decay) S + Kd^T V' (16x16x32 f16 MFMAs whose B
+//       operands come straight from the accumulators: the LDS operands are stored with the matching permutation of
+//       each 32-block, position 8g + 4h + e <-> index 16h + 4g + e)
+// Precision: MFMA operands are fp16 (11-bit significand) except the diagonal Gram blocks (bf16 hi/lo); fp32
+// accumulation; the state is fp32 and is rounded to fp16 only as the B operand of W S and Q~ S.  Range: fp16 holds
+// |x| < 65504 (state, U, T entries); the diagonal blocks need |Gamma_i - Gamma_m| < 88 over 8 tokens, i.e. a
+// per-token log-decay above ~ -11 (gate-in-kernel calls with lower_bound >= -11 always satisfy it).
 #include <algorithm>
 #include <numeric>
 #include <vector>
@@ -39,30 +40,68 @@
 namespace kda355 {
 namespace {
 
-constexpr int PF_THREADS = 256;
-// workspace per (chunk, head), fp16 element offsets
-constexpr int WS_W = 0;          // [64 tokens][128 channels], channels permuted within 32-blocks
-constexpr int WS_QP = 8192;      // [64][128], channels permuted
-constexpr int WS_KDT = 16384;    // [128 channels][64 tokens], tokens permuted within 32-blocks
-constexpr int WS_UT = 24576;     // [128 values][64 tokens]
-constexpr int WS_OIT = 32768;    // [128 values][64 tokens]
-constexpr int WS_DEC_BYTES = 81920;  // fp32 [128] = e^{Gamma_c}
-constexpr int64_t WS_BYTES = 82432;  // multiple of 256
+constexpr int PF_THREADS = 512;
+
+// LDS layout (bytes).  Region A: gate / Gamma fp32 [64][132], then k^ fi fp32 [64][132].  Region B: q^ fi fp32
+// [64][132], then Q~ fp16 [64][136] and beta v fp16 [64][136].  Region C: k^ fj fp32 [64][132], then Kd^T fp16
+// [128][72].  Row paddings keep the 16-lane MFMA fragment reads and the column reads free of bank conflicts.
+constexpr int RS32 = 132;   // fp32 rows of 128
+constexpr int RS16 = 136;   // fp16 rows of 128
+constexpr int RS16S = 72;   // fp16 rows of 64
+constexpr int LDS_A = 0;
+constexpr int LDS_B = 33792;
+constexpr int LDS_BV = LDS_B + 17408;
+constexpr int LDS_C = 68608;
+constexpr int LDS_W = 102400;
+constexpr int LDS_AQ = 119808;
+constexpr int LDS_AK = 129024;
+constexpr int LDS_L = 138240;
+constexpr int LDS_F = 142592;
+constexpr int LDS_WT = 151808;
+constexpr int LDS_BETA = 153856;
+constexpr int LDS_DT = 154112;    // dt_bias of the head (gate-in-kernel) fp32 [128]
+constexpr int LDS_TOTAL = 154624;
+// per-channel factor rows of LDS_F
+constexpr int F_A = 0;      // a_I = e^{Gamma_m(I) - Gamma_{16I-1}}, I = 1..3          (rows 0..2)
+constexpr int F_B = 3;      // b_IJ = e^{Gamma_{16I-1} - Gamma_m(J)}, row 3 + I(I-1)/2 + J (rows 3..8)
+constexpr int F_X = 9;      // x_I = e^{Gamma_m(I)}                                    (rows 9..12)
+constexpr int F_Y = 13;     // y_I = e^{Gamma_c - Gamma_m(I)}                          (rows 13..16)
+constexpr int F_DEC = 17;   // e^{Gamma_c}
+constexpr int F_ROWS = 18;
 
 constexpr uint32_t PLAN_MAGIC = 0x4b443535u;  // "KD55"
 // table header words
-enum { H_MAGIC = 0, H_N, H_T, H_NCHUNK, H_EVERY, H_OFF_CHUNK, H_OFF_CHAIN, H_OFF_SEQ, H_CKROWS, H_WORDS = 16 };
+enum { H_MAGIC = 0, H_N, H_T, H_NCHUNK, H_EVERY, H_OFF_CHAIN, H_NCHAIN, H_CKROWS, H_WORDS = 16 };
+// one chain entry: the chunks [0, nch) of sequence n, tokens [t_start, t_start + len)
+enum { C_SEQ = 0, C_NCH, C_TSTART, C_LEN, C_CKSINGLE, C_CKROW0, C_WORDS = 8 };
 
 typedef _Float16 half_t;
 
-__device__ __forceinline__ f32x4 mfma_f16(f16x8 a, f16x8 b, f32x4 c) {
+__device__ __forceinline__ f32x4 mfma32(f16x8 a, f16x8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
-__device__ __forceinline__ f32x4 mfma_bf16(bf16x8 a, bf16x8 b, f32x4 c) {
+__device__ __forceinline__ f32x4 mfma32bf(bf16x8 a, bf16x8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
-// position p (0..31) inside a 32-block for k-slot e (0..7) of lane group g
-__device__ __forceinline__ int perm32(int g, int e) { return e < 4 ? 4 * g + e : 16 + 4 * g + (e - 4); }
+__device__ __forceinline__ f32x4 mfma16(f16x4 a, f16x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+}
+// storage position of index q (0..31) inside a permuted 32-block: q = 16h + 4g + e  ->  8g + 4h + e
+__device__ __forceinline__ int pos32(int q) { return ((q >> 2) & 3) * 8 + ((q >> 4) << 2) + (q & 3); }
+__device__ __forceinline__ int pos64(int q) { return (q & 32) + pos32(q & 31); }
+
+// Workgroup barrier for LDS traffic only.  __syncthreads() also fences global memory (s_waitcnt vmcnt(0)), which
+// would wait for the next chunk's prefetched loads and for the output stores at every phase boundary; the waves of
+// this kernel exchange data through LDS alone, so completing the LDS operations (lgkmcnt(0)) is sufficient.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// Sum over each group of 8 consecutive lanes (quad swaps, then the mirrored quad).
+__device__ __forceinline__ float sum8(float x) {
+    x += dpp<0xB1>(x);
+    x += dpp<0x4E>(x);
+    x += dpp<0x141>(x);
+    return x;
+}
 
 struct PfParams {
     const uint16_t* q;
@@ -81,7 +120,6 @@ struct PfParams {
     void* ck_pool;
     const int32_t* ck_idx;
     const int32_t* tab;
-    uint8_t* ws;
     int64_t qkv_rs, g_rs, beta_rs, out_rs;
     int64_t state_ss, state_slots, ck_ss, ck_slots;
     int N, H;
@@ -90,406 +128,118 @@ struct PfParams {
     int ck_bf16;
 };
 
-// ------------------------------------------------------------------------------------------------ prologue
-struct PrologueSmem {
-    uint16_t q[64][128];    // raw bf16 rows (pad rows zero)
-    uint16_t k[64][128];
-    uint16_t v[64][128];
-    float G[64][128];       // log-decay, then Gamma (inclusive cumsum) in place
-    float rq[64], rk[64];   // 1 / max(|x|, 1e-6)
-    float beta[64];
-    float Akk[64][68];
-    float Aqk[64][68];
-    float T[64][68];
-    float X[3][16][17];
+// Raw inputs of one chunk row slice: row r, channels 16 cb .. 16 cb + 15.
+struct RawRow {
+    u32x4 q[2], k[2], v[2];
+    u32x4 g[4];  // fp32 log-decay (4 x 4 floats), or bf16 raw gate in g[0..1]
+    uint32_t beta;  // fp32 bits, or the bf16 raw beta in the low half (converted when the chunk is consumed)
 };
 
-template <bool RAW_GATE, bool RAW_BETA, bool NORM>
-__global__ void __launch_bounds__(PF_THREADS) prologue_kernel(PfParams p) {
-    extern __shared__ __align__(16) unsigned char smem_raw[];
-    PrologueSmem& sm = *reinterpret_cast<PrologueSmem*>(smem_raw);
-    const int H = p.H;
-    const int cg = blockIdx.x / H;
-    const int h = blockIdx.x - cg * H;
-    const int tid = threadIdx.x;
-    const int wv = tid >> 6;
-    const int lane = tid & 63;
-    const int m = lane & 15;
-    const int gq = lane >> 4;
-    const int* chunk = p.tab + p.tab[H_OFF_CHUNK] + 2 * cg;
-    const int t0 = chunk[0];
-    const int L = chunk[1];
-
-    // ---------------- load q, k, v (bf16), g, beta
-    for (int i = tid; i < 64 * 16; i += PF_THREADS) {  // 16-byte pieces: row = i / 16, col8 = (i % 16) * 8
-        const int r = i >> 4, c8 = (i & 15) * 8;
-        u32x4 zq = {0, 0, 0, 0}, zk = zq, zv = zq;
-        if (r < L) {
-            const int64_t off = (int64_t)(t0 + r) * p.qkv_rs + (int64_t)h * D + c8;
-            zq = *reinterpret_cast<const u32x4*>(p.q + off);
-            zk = *reinterpret_cast<const u32x4*>(p.k + off);
-            zv = *reinterpret_cast<const u32x4*>(p.v + off);
+template <bool RG>
+__device__ __forceinline__ void load_row(const PfParams& p, int h, int t0, int L, int r, int cb, bool RB, RawRow& x) {
+    const u32x4 z = {0u, 0u, 0u, 0u};
+    if (r < L) {
+        const int64_t tok = (int64_t)t0 + r;
+        const int64_t o = tok * p.qkv_rs + (int64_t)h * D + 16 * cb;
+        const u32x4* q4 = reinterpret_cast<const u32x4*>(p.q + o);
+        const u32x4* k4 = reinterpret_cast<const u32x4*>(p.k + o);
+        const u32x4* v4 = reinterpret_cast<const u32x4*>(p.v + o);
+        x.q[0] = q4[0]; x.q[1] = q4[1];
+        x.k[0] = k4[0]; x.k[1] = k4[1];
+        x.v[0] = v4[0]; x.v[1] = v4[1];
+        if (RG) {
+            const u32x4* g4 = reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(p.g) + tok * p.g_rs +
+                                                             (int64_t)h * D + 16 * cb);
+            x.g[0] = g4[0]; x.g[1] = g4[1];
+            x.g[2] = z; x.g[3] = z;
+        } else {
+            const u32x4* g4 = reinterpret_cast<const u32x4*>(reinterpret_cast<const float*>(p.g) + tok * p.g_rs +
+                                                             (int64_t)h * D + 16 * cb);
+            x.g[0] = g4[0]; x.g[1] = g4[1]; x.g[2] = g4[2]; x.g[3] = g4[3];
         }
-        *reinterpret_cast<u32x4*>(&sm.q[r][c8]) = zq;
-        *reinterpret_cast<u32x4*>(&sm.k[r][c8]) = zk;
-        *reinterpret_cast<u32x4*>(&sm.v[r][c8]) = zv;
-    }
-    for (int i = tid; i < 64 * 32; i += PF_THREADS) {  // 4-float pieces
-        const int r = i >> 5, c4 = (i & 31) * 4;
-        f32x4 gv = {0.f, 0.f, 0.f, 0.f};
-        if (r < L) {
-            if (RAW_GATE) {
-                const uint16_t* gb = reinterpret_cast<const uint16_t*>(p.g) + (int64_t)(t0 + r) * p.g_rs + h * D + c4;
-                const u32x2 raw = *reinterpret_cast<const u32x2*>(gb);
-                const float A = __expf(p.A_log[h]);
-                const f32x4 db = *reinterpret_cast<const f32x4*>(p.dt_bias + h * D + c4);
-                gv.x = p.lb * sigmoidf_(A * (bf2f(raw.x & 0xffffu) + db.x));
-                gv.y = p.lb * sigmoidf_(A * (bf2f(raw.x >> 16) + db.y));
-                gv.z = p.lb * sigmoidf_(A * (bf2f(raw.y & 0xffffu) + db.z));
-                gv.w = p.lb * sigmoidf_(A * (bf2f(raw.y >> 16) + db.w));
-            } else {
-                gv = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(p.g) + (int64_t)(t0 + r) * p.g_rs +
-                                                     h * D + c4);
-            }
-        }
-        *reinterpret_cast<f32x4*>(&sm.G[r][c4]) = gv;
-    }
-    if (tid < 64) {
-        float b = 0.f;
-        if (tid < L) {
-            if (RAW_BETA)
-                b = sigmoidf_(bf2f(reinterpret_cast<const uint16_t*>(p.beta)[(int64_t)(t0 + tid) * p.beta_rs + h]));
-            else
-                b = reinterpret_cast<const float*>(p.beta)[(int64_t)(t0 + tid) * p.beta_rs + h];
-        }
-        sm.beta[tid] = b;
-    }
-    // zero T (upper blocks stay zero)
-    for (int i = tid; i < 64 * 68; i += PF_THREADS) (&sm.T[0][0])[i] = 0.f;
-    __syncthreads();
-
-    // ---------------- row norms (threads 0..127) and the gate cumsum (threads 128..255)
-    if (tid < 128) {
-        const int r = tid & 63;
-        const uint16_t* row = (tid < 64) ? sm.q[r] : sm.k[r];
-        float ss = 0.f;
-        for (int c = 0; c < 128; c += 2) {
-            const uint32_t w2 = *reinterpret_cast<const uint32_t*>(row + c);
-            const float a = bf2f(w2 & 0xffffu), b = bf2f(w2 >> 16);
-            ss += a * a + b * b;
-        }
-        float inv = 1.f;
-        if (NORM) inv = 1.f / fmaxf(sqrtf(ss), 1e-6f);  // F.normalize (kda/mi350x/reference.py:59-60)
-        if (tid < 64) sm.rq[r] = inv; else sm.rk[r] = inv;
+        x.beta = RB ? (uint32_t)reinterpret_cast<const uint16_t*>(p.beta)[tok * p.beta_rs + h]
+                    : reinterpret_cast<const uint32_t*>(p.beta)[tok * p.beta_rs + h];
     } else {
-        const int c = tid - 128;
-        float acc = 0.f;
-        for (int r = 0; r < 64; ++r) {
-            acc += sm.G[r][c];
-            sm.G[r][c] = acc;
-        }
-    }
-    __syncthreads();
-
-    // ---------------- A_kk, A_qk: wave wv owns row block I = wv
-    {
-        const int I = wv;
-        const int i = 16 * I + m;  // A-operand row of this lane
-        const float rki = sm.rk[i], rqi = sm.rq[i];
-        // diagonal block, reference row mr, bf16 hi/lo operands
-        {
-            const int mr = 16 * I + 7;
-            f32x4 akk = {0.f, 0.f, 0.f, 0.f}, aqk = akk;
-#pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                bf16x8 ka_hi, ka_lo, qa_hi, qa_lo, kb_hi, kb_lo;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const int c = 32 * s + 8 * gq + e;
-                    const float gi = sm.G[i][c], gm = sm.G[mr][c];
-                    const float fi = __expf(gi - gm), fj = __expf(gm - gi);  // row i as A, column i as B
-                    const float kv = bf2f(sm.k[i][c]) * rki;
-                    const float ka = kv * fi, qa = bf2f(sm.q[i][c]) * rqi * fi, kb = kv * fj;
-                    const __bf16 kah = (__bf16)ka, qah = (__bf16)qa, kbh = (__bf16)kb;
-                    ka_hi[e] = kah; ka_lo[e] = (__bf16)(ka - (float)kah);
-                    qa_hi[e] = qah; qa_lo[e] = (__bf16)(qa - (float)qah);
-                    kb_hi[e] = kbh; kb_lo[e] = (__bf16)(kb - (float)kbh);
-                }
-                akk = mfma_bf16(ka_hi, kb_hi, akk);
-                akk = mfma_bf16(ka_hi, kb_lo, akk);
-                akk = mfma_bf16(ka_lo, kb_hi, akk);
-                aqk = mfma_bf16(qa_hi, kb_hi, aqk);
-                aqk = mfma_bf16(qa_hi, kb_lo, aqk);
-                aqk = mfma_bf16(qa_lo, kb_hi, aqk);
-            }
-#pragma unroll
-            for (int rr = 0; rr < 4; ++rr) {
-                const int row = 16 * I + 4 * gq + rr, col = 16 * I + m;
-                sm.Akk[row][col] = (col < row) ? sm.beta[row] * akk[rr] : 0.f;
-                sm.Aqk[row][col] = (col <= row) ? aqk[rr] : 0.f;
-            }
-        }
-        // off-diagonal blocks (I, J < I), reference row r = 16 I - 1, fp16 operands <= 1
-        if (I > 0) {
-            const int r = 16 * I - 1;
-            f16x8 kA[4], qA[4];
-#pragma unroll
-            for (int s = 0; s < 4; ++s)
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const int c = 32 * s + 8 * gq + e;
-                    const float f = __expf(sm.G[i][c] - sm.G[r][c]);
-                    kA[s][e] = (half_t)(bf2f(sm.k[i][c]) * rki * f);
-                    qA[s][e] = (half_t)(bf2f(sm.q[i][c]) * rqi * f);
-                }
-            for (int J = 0; J < I; ++J) {
-                const int j = 16 * J + m;  // B-operand column of this lane
-                const float rkj = sm.rk[j];
-                f32x4 akk = {0.f, 0.f, 0.f, 0.f}, aqk = akk;
-#pragma unroll
-                for (int s = 0; s < 4; ++s) {
-                    f16x8 kB;
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        const int c = 32 * s + 8 * gq + e;
-                        kB[e] = (half_t)(bf2f(sm.k[j][c]) * rkj * __expf(sm.G[r][c] - sm.G[j][c]));
-                    }
-                    akk = mfma_f16(kA[s], kB, akk);
-                    aqk = mfma_f16(qA[s], kB, aqk);
-                }
-#pragma unroll
-                for (int rr = 0; rr < 4; ++rr) {
-                    const int row = 16 * I + 4 * gq + rr, col = 16 * J + m;
-                    sm.Akk[row][col] = sm.beta[row] * akk[rr];
-                    sm.Aqk[row][col] = aqk[rr];
-                }
-            }
-        }
-        // zero the strictly-upper blocks of Aqk (read by the Qp / Oi products)
-        for (int J = I + 1; J < 4; ++J)
-#pragma unroll
-            for (int rr = 0; rr < 4; ++rr) sm.Aqk[16 * I + 4 * gq + rr][16 * J + m] = 0.f;
-    }
-    __syncthreads();
-
-    // ---------------- T = (I + A_kk)^-1: diagonal blocks by forward substitution (wave 0: lane = (block, column))
-    if (wv == 0) {
-        const int I = lane >> 4, j = lane & 15;
-        float x[16];
-#pragma unroll
-        for (int ii = 0; ii < 16; ++ii) {
-            float acc = 0.f;
-#pragma unroll
-            for (int mm = 0; mm < ii; ++mm) acc += sm.Akk[16 * I + ii][16 * I + mm] * x[mm];
-            x[ii] = (ii < j) ? 0.f : ((ii == j) ? 1.f : -acc);
-        }
-#pragma unroll
-        for (int ii = 0; ii < 16; ++ii) sm.T[16 * I + ii][16 * I + j] = x[ii];
-    }
-    __syncthreads();
-    // off-diagonal blocks, by distance d = I - J: T_IJ = -T_II sum_{K=J}^{I-1} A_IK T_KJ
-    for (int d = 1; d < 4; ++d) {
-        const int cnt = 4 - d;
-        for (int e = tid; e < cnt * 256; e += PF_THREADS) {
-            const int b = e >> 8, ii = (e >> 4) & 15, jj = e & 15;
-            const int I = d + b, J = b;
-            float acc = 0.f;
-            for (int K = J; K < I; ++K)
-#pragma unroll
-                for (int mm = 0; mm < 16; ++mm) acc += sm.Akk[16 * I + ii][16 * K + mm] * sm.T[16 * K + mm][16 * J + jj];
-            sm.X[b][ii][jj] = acc;
-        }
-        __syncthreads();
-        for (int e = tid; e < cnt * 256; e += PF_THREADS) {
-            const int b = e >> 8, ii = (e >> 4) & 15, jj = e & 15;
-            const int I = d + b, J = b;
-            float acc = 0.f;
-#pragma unroll
-            for (int mm = 0; mm < 16; ++mm) acc += sm.T[16 * I + ii][16 * I + mm] * sm.X[b][mm][jj];
-            sm.T[16 * I + ii][16 * J + jj] = -acc;
-        }
-        __syncthreads();
-    }
-
-    // ---------------- W = T diag(beta) K e^Gamma, U = T diag(beta) V: wave wv owns channels [32 wv, 32 wv + 32)
-    uint8_t* ws = p.ws + ((int64_t)cg * H + h) * WS_BYTES;
-    half_t* wsh = reinterpret_cast<half_t*>(ws);
-    f32x4 Wacc[4][2], Uacc[4][2];
-#pragma unroll
-    for (int it = 0; it < 4; ++it)
-#pragma unroll
-        for (int ct = 0; ct < 2; ++ct) {
-            Wacc[it][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
-            Uacc[it][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
-        }
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {  // tokens 32 s .. 32 s + 31, natural k order: slot e of group gq = token 32 s + 8 gq + e
-        f16x8 BW[2], BU[2];
-#pragma unroll
-        for (int ct = 0; ct < 2; ++ct) {
-            const int c = 32 * wv + 16 * ct + m;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int j = 32 * s + 8 * gq + e;
-                const float bj = sm.beta[j];
-                BW[ct][e] = (half_t)(bj * bf2f(sm.k[j][c]) * sm.rk[j] * __expf(sm.G[j][c]));
-                BU[ct][e] = (half_t)(bj * bf2f(sm.v[j][c]));
-            }
-        }
-#pragma unroll
-        for (int it = 0; it < 4; ++it) {
-            if (2 * s > it) continue;  // T[it block][tokens of k-step s] is zero
-            f16x8 A;
-            const float* trow = &sm.T[16 * it + m][32 * s + 8 * gq];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) A[e] = (half_t)trow[e];
-#pragma unroll
-            for (int ct = 0; ct < 2; ++ct) {
-                Wacc[it][ct] = mfma_f16(A, BW[ct], Wacc[it][ct]);
-                Uacc[it][ct] = mfma_f16(A, BU[ct], Uacc[it][ct]);
-            }
-        }
-    }
-    // W -> workspace (channels permuted), U -> U^T (natural tokens)
-#pragma unroll
-    for (int it = 0; it < 4; ++it)
-#pragma unroll
-        for (int ct = 0; ct < 2; ++ct) {
-            const int pos = 16 * ct + m;  // natural position inside the 32-block of channels
-            const int slot = pos < 16 ? 8 * (pos >> 2) + (pos & 3) : 8 * ((pos - 16) >> 2) + 4 + (pos & 3);
-            const int cperm = 32 * wv + slot;
-            const int c = 32 * wv + pos;
-#pragma unroll
-            for (int rr = 0; rr < 4; ++rr) {
-                const int row = 16 * it + 4 * gq + rr;
-                wsh[WS_W + row * 128 + cperm] = (half_t)Wacc[it][ct][rr];
-            }
-            f16x4 u4;
-#pragma unroll
-            for (int rr = 0; rr < 4; ++rr) u4[rr] = (half_t)Uacc[it][ct][rr];
-            *reinterpret_cast<f16x4*>(&wsh[WS_UT + c * 64 + 16 * it + 4 * gq]) = u4;
-        }
-
-    // ---------------- Qp = Q e^Gamma - A_qk W, Oi = A_qk U (B operands straight from the W / U accumulators)
-    f32x4 Pacc[4][2], Oacc[4][2];
-#pragma unroll
-    for (int it = 0; it < 4; ++it)
-#pragma unroll
-        for (int ct = 0; ct < 2; ++ct) {
-            Pacc[it][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
-            Oacc[it][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
-        }
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {  // tokens of k-step s in permuted order: slot e of group gq = token 32 s + perm32(gq, e)
-        f16x8 BW[2], BU[2];
-#pragma unroll
-        for (int ct = 0; ct < 2; ++ct)
-#pragma unroll
-            for (int rr = 0; rr < 4; ++rr) {
-                BW[ct][rr] = (half_t)Wacc[2 * s][ct][rr];
-                BW[ct][4 + rr] = (half_t)Wacc[2 * s + 1][ct][rr];
-                BU[ct][rr] = (half_t)Uacc[2 * s][ct][rr];
-                BU[ct][4 + rr] = (half_t)Uacc[2 * s + 1][ct][rr];
-            }
-#pragma unroll
-        for (int it = 0; it < 4; ++it) {
-            if (2 * s > it) continue;
-            f16x8 A;
-            const float* arow = &sm.Aqk[16 * it + m][32 * s];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) A[e] = (half_t)arow[perm32(gq, e)];
-#pragma unroll
-            for (int ct = 0; ct < 2; ++ct) {
-                Pacc[it][ct] = mfma_f16(A, BW[ct], Pacc[it][ct]);
-                Oacc[it][ct] = mfma_f16(A, BU[ct], Oacc[it][ct]);
-            }
-        }
-    }
-#pragma unroll
-    for (int it = 0; it < 4; ++it)
-#pragma unroll
-        for (int ct = 0; ct < 2; ++ct) {
-            const int pos = 16 * ct + m;
-            const int slot = pos < 16 ? 8 * (pos >> 2) + (pos & 3) : 8 * ((pos - 16) >> 2) + 4 + (pos & 3);
-            const int cperm = 32 * wv + slot;
-            const int c = 32 * wv + pos;
-#pragma unroll
-            for (int rr = 0; rr < 4; ++rr) {
-                const int row = 16 * it + 4 * gq + rr;
-                const float qt = bf2f(sm.q[row][c]) * sm.rq[row] * __expf(sm.G[row][c]);
-                wsh[WS_QP + row * 128 + cperm] = (half_t)(qt - Pacc[it][ct][rr]);
-            }
-            f16x4 o4;
-#pragma unroll
-            for (int rr = 0; rr < 4; ++rr) o4[rr] = (half_t)Oacc[it][ct][rr];
-            *reinterpret_cast<f16x4*>(&wsh[WS_OIT + c * 64 + 16 * it + 4 * gq]) = o4;
-        }
-
-    // ---------------- Kd^T (tokens permuted) and the chunk decay
-    for (int e = tid; e < 128 * 8; e += PF_THREADS) {
-        const int c = e >> 3, grp8 = e & 7;  // 8 slots: block s = grp8 / 4, group g = grp8 % 4
-        const int s = grp8 >> 2, g = grp8 & 3;
-        const float gl = sm.G[63][c];
-        f16x8 val;
-#pragma unroll
-        for (int ee = 0; ee < 8; ++ee) {
-            const int t = 32 * s + perm32(g, ee);
-            val[ee] = (half_t)(bf2f(sm.k[t][c]) * sm.rk[t] * __expf(gl - sm.G[t][c]));
-        }
-        *reinterpret_cast<f16x8*>(&wsh[WS_KDT + c * 64 + 8 * grp8]) = val;
-    }
-    if (tid < 128) reinterpret_cast<float*>(ws + WS_DEC_BYTES)[tid] = __expf(sm.G[63][tid]);
-}
-
-// ------------------------------------------------------------------------------------------------ walk
-struct WalkSmem {
-    half_t W[64][128];
-    half_t Qp[64][128];
-    half_t KdT[128][64];
-};
-
-__device__ __forceinline__ void store_state_rows(float* dst, const f32x4 (&S)[8][2], int wv, int gq, int m) {
-    // dst: V-major [128 v][128 d]
-#pragma unroll
-    for (int vt = 0; vt < 2; ++vt) {
-        const int v = 32 * wv + 16 * vt + m;
-#pragma unroll
-        for (int dt = 0; dt < 8; ++dt) *reinterpret_cast<f32x4*>(dst + v * 128 + 16 * dt + 4 * gq) = S[dt][vt];
-    }
-}
-__device__ __forceinline__ void store_state_rows_bf16(uint16_t* dst, const f32x4 (&S)[8][2], int wv, int gq, int m) {
-#pragma unroll
-    for (int vt = 0; vt < 2; ++vt) {
-        const int v = 32 * wv + 16 * vt + m;
-#pragma unroll
-        for (int dt = 0; dt < 8; ++dt) {
-            u32x2 w;
-            w.x = f2bf(S[dt][vt][0]) | (f2bf(S[dt][vt][1]) << 16);
-            w.y = f2bf(S[dt][vt][2]) | (f2bf(S[dt][vt][3]) << 16);
-            *reinterpret_cast<u32x2*>(dst + v * 128 + 16 * dt + 4 * gq) = w;
-        }
+        x.q[0] = z; x.q[1] = z; x.k[0] = z; x.k[1] = z; x.v[0] = z; x.v[1] = z;
+        x.g[0] = z; x.g[1] = z; x.g[2] = z; x.g[3] = z;
+        x.beta = 0u;  // padded rows get beta = 0 when the chunk is consumed
     }
 }
 
-__global__ void __launch_bounds__(PF_THREADS) walk_kernel(PfParams p) {
-    extern __shared__ __align__(16) unsigned char smem_raw[];
-    WalkSmem& sm = *reinterpret_cast<WalkSmem*>(smem_raw);
+__device__ __forceinline__ void unpack16(const u32x4 (&w)[2], float (&f)[16]) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            f[8 * i + 2 * j] = bf2f(w[i][j] & 0xffffu);
+            f[8 * i + 2 * j + 1] = bf2f(w[i][j] >> 16);
+        }
+}
+
+// The staged output row slice of raw thread (r, cb): 16 bf16 values in the first half of its 64-byte slot of region A.
+__device__ __forceinline__ void store_out_slot(const PfParams& p, int h, int t0, int L, int r, int cb,
+                                               const unsigned char* lds) {
+    if (r < L) {
+        const u32x4* so = reinterpret_cast<const u32x4*>(lds + r * 528 + 64 * cb);
+        u32x4* dst = reinterpret_cast<u32x4*>(p.out + ((int64_t)t0 + r) * p.out_rs + (int64_t)h * D + 16 * cb);
+        dst[0] = so[0];
+        dst[1] = so[1];
+    }
+}
+
+// V-major state rows of this lane: v = 16w + m, k = 16dt + 4g .. + 3
+__device__ __forceinline__ void store_state(float* dst, const f32x4 (&S)[8], int w, int g, int m) {
+    float* row = dst + (16 * w + m) * D + 4 * g;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) *reinterpret_cast<f32x4*>(row + 16 * dt) = S[dt];
+}
+__device__ __forceinline__ void store_state_bf16(uint16_t* dst, const f32x4 (&S)[8], int w, int g, int m) {
+    uint16_t* row = dst + (16 * w + m) * D + 4 * g;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+        u32x2 o;
+        o.x = f2bf(S[dt][0]) | (f2bf(S[dt][1]) << 16);
+        o.y = f2bf(S[dt][2]) | (f2bf(S[dt][3]) << 16);
+        *reinterpret_cast<u32x2*>(row + 16 * dt) = o;
+    }
+}
+
+template <bool RG>
+__global__ void __launch_bounds__(PF_THREADS, 1)
+    chunk_kernel(PfParams p, const int32_t* __restrict__ tab, const int32_t* __restrict__ ck_idx) {
+    extern __shared__ __align__(16) unsigned char lds[];
+    float* sG = reinterpret_cast<float*>(lds + LDS_A);       // gate / Gamma, then k^ fi
+    float* sKA = sG;
+    float* sQA = reinterpret_cast<float*>(lds + LDS_B);      // q^ fi
+    half_t* sQt = reinterpret_cast<half_t*>(lds + LDS_B);    // Q~ (channels permuted)
+    half_t* sBV = reinterpret_cast<half_t*>(lds + LDS_BV);   // beta v
+    float* sKB = reinterpret_cast<float*>(lds + LDS_C);      // k^ fj
+    half_t* sKd = reinterpret_cast<half_t*>(lds + LDS_C);    // Kd^T (tokens permuted)
+    half_t* sW = reinterpret_cast<half_t*>(lds + LDS_W);     // W (channels permuted)
+    half_t* sAq = reinterpret_cast<half_t*>(lds + LDS_AQ);   // A_qk (columns permuted)
+    half_t* sAk = reinterpret_cast<half_t*>(lds + LDS_AK);   // -A_kk off-diagonal blocks, T_II diagonal blocks
+    float* sL = reinterpret_cast<float*>(lds + LDS_L);       // A_kk diagonal blocks [4][16][17]
+    float* sF = reinterpret_cast<float*>(lds + LDS_F);       // per-channel factors [18][128]
+    float* sWt = reinterpret_cast<float*>(lds + LDS_WT);     // segment totals of the gate cumsum [4][128]
+    float* sBeta = reinterpret_cast<float*>(lds + LDS_BETA);
+    float* sDT = reinterpret_cast<float*>(lds + LDS_DT);
+
     const int H = p.H;
     const int ci = blockIdx.x / H;
     const int h = blockIdx.x - ci * H;
-    const int tid = threadIdx.x;
-    const int wv = tid >> 6;
-    const int lane = tid & 63;
-    const int m = lane & 15;
-    const int gq = lane >> 4;
-    const int* chain = p.tab + p.tab[H_OFF_CHAIN] + 4 * ci;
-    const int n = chain[0], first = chain[1], nch = chain[2];
-    const int* seqinfo = p.tab + p.tab[H_OFF_SEQ] + 2 * n;
-    const int every = p.tab[H_EVERY];  // every-n checkpoint interval in chunks (0 = off)
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+    // uniform table reads through a __restrict__ pointer: scalar loads, which never join the vector-memory counter that
+    // the prefetched rows are waited on with
+    const int32_t* chain = tab + H_WORDS + C_WORDS * ci;
+    const int n = chain[C_SEQ], nch = chain[C_NCH], tstart = chain[C_TSTART], len = chain[C_LEN];
+    const int every = tab[H_EVERY];
     const bool pool = (p.flags & KDA355_PF_POOL) != 0;
+    const bool RB = (p.flags & KDA355_PF_RAW_BETA) != 0;
+    const bool NORM = (p.flags & KDA355_PF_NORMALIZE_QK) != 0;
 
-    // ---- initial state
-    f32x4 S[8][2];
+    // ---- initial state (lane: v = 16w + m, k = 16dt + 4g + e)
+    int tid = threadIdx.x, lane = tid & 63, m = lane & 15, g = lane >> 4, r = tid >> 3, cb = tid & 7;
+    f32x4 S[8];
     const float* src = nullptr;
     int64_t row = -1;
     if (pool) {
@@ -499,140 +249,455 @@ __global__ void __launch_bounds__(PF_THREADS) walk_kernel(PfParams p) {
         src = p.init_state + ((int64_t)n * H + h) * D * D;
     }
 #pragma unroll
-    for (int vt = 0; vt < 2; ++vt) {
-        const int v = 32 * wv + 16 * vt + m;
-#pragma unroll
-        for (int dt = 0; dt < 8; ++dt)
-            S[dt][vt] = src ? *reinterpret_cast<const f32x4*>(src + v * 128 + 16 * dt + 4 * gq) : f32x4{0.f, 0.f, 0.f, 0.f};
-    }
-    // every-n checkpoint rows: row j = state before token j * every * 64 (j = 0: the initial state)
-    const int ck_mode = (p.flags & KDA355_PF_CK_EVERY) ? 2 : ((p.flags & KDA355_PF_CK_SINGLE) ? 1 : 0);
-    auto ck_store = [&](int64_t r) {
-        if (r < 0 || r >= p.ck_slots) return;
-        if (p.ck_bf16)
-            store_state_rows_bf16(reinterpret_cast<uint16_t*>(p.ck_pool) + r * p.ck_ss + (int64_t)h * D * D, S, wv, gq, m);
-        else
-            store_state_rows(reinterpret_cast<float*>(p.ck_pool) + r * p.ck_ss + (int64_t)h * D * D, S, wv, gq, m);
-    };
-    if (ck_mode == 2 && every > 0 && nch > 0) ck_store(p.ck_idx[seqinfo[1]]);
-    const int ck_single = (ck_mode == 1) ? seqinfo[0] : 0;  // chunk count after which the single checkpoint is taken
+    for (int dt = 0; dt < 8; ++dt)
+        S[dt] = src ? *reinterpret_cast<const f32x4*>(src + (16 * w + m) * D + 16 * dt + 4 * g) : f32x4{0.f, 0.f, 0.f, 0.f};
 
-    const int* chunks = p.tab + p.tab[H_OFF_CHUNK];
-    for (int cl = 0; cl < nch; ++cl) {
-        const int cgl = first + cl;
-        const int t0 = chunks[2 * cgl], L = chunks[2 * cgl + 1];
-        const uint8_t* ws = p.ws + ((int64_t)cgl * H + h) * WS_BYTES;
-        const half_t* wsh = reinterpret_cast<const half_t*>(ws);
-        __syncthreads();  // previous chunk's LDS reads done
-        {
-            const u32x4* s4 = reinterpret_cast<const u32x4*>(wsh);  // W, Qp, KdT are the first 3 x 16 KiB
-            u32x4* d4 = reinterpret_cast<u32x4*>(&sm.W[0][0]);
-#pragma unroll
-            for (int i = 0; i < 12; ++i) d4[i * PF_THREADS + tid] = s4[i * PF_THREADS + tid];
-        }
-        __syncthreads();
-        // S -> fp16 B fragments (k = d in permuted order)
-        f16x8 SB[4][2];
-#pragma unroll
-        for (int s = 0; s < 4; ++s)
-#pragma unroll
-            for (int vt = 0; vt < 2; ++vt)
-#pragma unroll
-                for (int rr = 0; rr < 4; ++rr) {
-                    SB[s][vt][rr] = (half_t)S[2 * s][vt][rr];
-                    SB[s][vt][4 + rr] = (half_t)S[2 * s + 1][vt][rr];
-                }
-        // V' = U - W S  (row tiles 0..3)
-        f16x8 VB[2][2];
-        f32x4 Vp[4][2];
-#pragma unroll
-        for (int it = 0; it < 4; ++it) {
-            f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-#pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                const f16x8 A = *reinterpret_cast<const f16x8*>(&sm.W[16 * it + m][32 * s + 8 * gq]);
-                acc[0] = mfma_f16(A, SB[s][0], acc[0]);
-                acc[1] = mfma_f16(A, SB[s][1], acc[1]);
-            }
-#pragma unroll
-            for (int vt = 0; vt < 2; ++vt) {
-                const int v = 32 * wv + 16 * vt + m;
-                const f16x4 u4 = *reinterpret_cast<const f16x4*>(&wsh[WS_UT + v * 64 + 16 * it + 4 * gq]);
-#pragma unroll
-                for (int rr = 0; rr < 4; ++rr) Vp[it][vt][rr] = (float)u4[rr] - acc[vt][rr];
-            }
-        }
-        // O = scale (Qp S + Oi)  (row tiles 4..7)
-#pragma unroll
-        for (int it = 0; it < 4; ++it) {
-            f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-#pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                const f16x8 A = *reinterpret_cast<const f16x8*>(&sm.Qp[16 * it + m][32 * s + 8 * gq]);
-                acc[0] = mfma_f16(A, SB[s][0], acc[0]);
-                acc[1] = mfma_f16(A, SB[s][1], acc[1]);
-            }
-#pragma unroll
-            for (int vt = 0; vt < 2; ++vt) {
-                const int v = 32 * wv + 16 * vt + m;
-                const f16x4 o4 = *reinterpret_cast<const f16x4*>(&wsh[WS_OIT + v * 64 + 16 * it + 4 * gq]);
-#pragma unroll
-                for (int rr = 0; rr < 4; ++rr) {
-                    const int i = 16 * it + 4 * gq + rr;
-                    if (i < L)
-                        p.out[(int64_t)(t0 + i) * p.out_rs + (int64_t)h * D + v] =
-                            (uint16_t)f2bf(p.scale * (acc[vt][rr] + (float)o4[rr]));
-                }
-            }
-        }
-        // S <- diag(decay) S + Kd^T V'
-#pragma unroll
-        for (int s = 0; s < 2; ++s)
-#pragma unroll
-            for (int vt = 0; vt < 2; ++vt)
-#pragma unroll
-                for (int rr = 0; rr < 4; ++rr) {
-                    VB[s][vt][rr] = (half_t)Vp[2 * s][vt][rr];
-                    VB[s][vt][4 + rr] = (half_t)Vp[2 * s + 1][vt][rr];
-                }
-        const float* dec = reinterpret_cast<const float*>(ws + WS_DEC_BYTES);
-#pragma unroll
-        for (int dt = 0; dt < 8; ++dt) {
-            const f32x4 d4 = *reinterpret_cast<const f32x4*>(dec + 16 * dt + 4 * gq);
-#pragma unroll
-            for (int vt = 0; vt < 2; ++vt) {
-                S[dt][vt][0] *= d4[0]; S[dt][vt][1] *= d4[1]; S[dt][vt][2] *= d4[2]; S[dt][vt][3] *= d4[3];
-            }
-#pragma unroll
-            for (int s = 0; s < 2; ++s) {
-                const f16x8 A = *reinterpret_cast<const f16x8*>(&sm.KdT[16 * dt + m][32 * s + 8 * gq]);
-                S[dt][0] = mfma_f16(A, VB[s][0], S[dt][0]);
-                S[dt][1] = mfma_f16(A, VB[s][1], S[dt][1]);
-            }
-        }
-        // checkpoints at chunk boundaries
-        if (ck_mode == 1 && cl + 1 == ck_single) ck_store(p.ck_idx[n]);
-        if (ck_mode == 2 && every > 0 && (cl + 1) % every == 0 && cl + 1 < nch) ck_store(p.ck_idx[seqinfo[1] + (cl + 1) / every]);
+    const int ck_mode = (p.flags & KDA355_PF_CK_EVERY) ? 2 : ((p.flags & KDA355_PF_CK_SINGLE) ? 1 : 0);
+    auto ck_store = [&](int64_t rr) {
+        if (rr < 0 || rr >= p.ck_slots) return;
+        if (p.ck_bf16)
+            store_state_bf16(reinterpret_cast<uint16_t*>(p.ck_pool) + rr * p.ck_ss + (int64_t)h * D * D, S, w, g, m);
+        else
+            store_state(reinterpret_cast<float*>(p.ck_pool) + rr * p.ck_ss + (int64_t)h * D * D, S, w, g, m);
+    };
+    const int ck_row0 = chain[C_CKROW0];
+    if (ck_mode == 2 && every > 0 && nch > 0) ck_store(ck_idx[ck_row0]);
+    const int ck_single = (ck_mode == 1) ? chain[C_CKSINGLE] : 0;
+
+    // gate-in-kernel constants for this thread's 16 channels
+    float Aexp = 0.f;
+    if (RG) {
+        Aexp = __expf(p.A_log[h]);
+        if (tid < D) sDT[tid] = p.dt_bias[h * D + tid];
     }
+    // A_qk blocks (0,1) and (2,3) are read by the walk and never written by the Gram phase
+    for (int e = tid; e < 2 * 16 * 16; e += PF_THREADS) {
+        const int b = e >> 8, ii = (e >> 4) & 15, jj = e & 15;
+        sAq[(32 * b + ii) * RS16S + 32 * b + pos32(16 + jj)] = (half_t)0.f;
+    }
+
+    RawRow nx;
+    if (nch > 0) load_row<RG>(p, h, tstart, min(64, len), r, cb, RB, nx);
+
+    for (int cl = 0; cl < nch; ++cl) {
+        // Lane indices are re-derived every chunk from an opaque copy so that the per-lane LDS addresses of all phases
+        // are recomputed where they are used instead of being kept live (and spilled) across the whole loop.
+        tid = threadIdx.x;
+        asm volatile("" : "+v"(tid));
+        lane = tid & 63;
+        m = lane & 15;
+        g = lane >> 4;
+        r = tid >> 3;
+        cb = tid & 7;
+        const int t0 = tstart + 64 * cl, L = min(64, len - 64 * cl);
+        // ================= P0: this chunk's raw rows; prefetch the next chunk
+        // The raw q, k, v go to LDS slots that only this thread reads back and later overwrites (q: first half of its
+        // q^ fi slot in region B, k: of its k^ fj slot in region C, v: the W area, which is free until P6), so the
+        // registers die here and the next chunk's loads reuse them without a loop-carried copy.
+        *reinterpret_cast<u32x4*>(lds + LDS_B + r * (4 * RS32) + 64 * cb) = nx.q[0];
+        *reinterpret_cast<u32x4*>(lds + LDS_B + r * (4 * RS32) + 64 * cb + 16) = nx.q[1];
+        *reinterpret_cast<u32x4*>(lds + LDS_C + r * (4 * RS32) + 64 * cb) = nx.k[0];
+        *reinterpret_cast<u32x4*>(lds + LDS_C + r * (4 * RS32) + 64 * cb + 16) = nx.k[1];
+        *reinterpret_cast<u32x4*>(lds + LDS_W + r * (2 * RS16) + 32 * cb) = nx.v[0];
+        *reinterpret_cast<u32x4*>(lds + LDS_W + r * (2 * RS16) + 32 * cb + 16) = nx.v[1];
+        float gv[16];
+        if (RG) {
+            float rg[16];
+            const u32x4 gg[2] = {nx.g[0], nx.g[1]};
+            unpack16(gg, rg);
+#pragma unroll
+            for (int c = 0; c < 16; ++c) gv[c] = (r < L) ? p.lb * sigmoidf_(Aexp * (rg[c] + sDT[16 * cb + c])) : 0.f;
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) gv[4 * i + j] = __uint_as_float(nx.g[i][j]);
+        }
+        const float bt = (r >= L) ? 0.f : (RB ? sigmoidf_(bf2f(nx.beta)) : __uint_as_float(nx.beta));
+        float rq = 1.f, rk = 1.f;
+        if (NORM) {  // F.normalize(x, eps=1e-6) = x / max(|x|, 1e-6)  (kda/mi350x/reference.py:59-60)
+            float qf[16], kf[16];
+            {
+                const u32x4 a[2] = {nx.q[0], nx.q[1]}, b[2] = {nx.k[0], nx.k[1]};
+                unpack16(a, qf);
+                unpack16(b, kf);
+            }
+            float sq = 0.f, sk = 0.f;
+#pragma unroll
+            for (int c = 0; c < 16; ++c) { sq += qf[c] * qf[c]; sk += kf[c] * kf[c]; }
+            sq = sum8(sq);
+            sk = sum8(sk);
+            rq = 1.f / fmaxf(sqrtf(sq), 1e-6f);
+            rk = 1.f / fmaxf(sqrtf(sk), 1e-6f);
+        }
+        // The previous chunk's staged output is read from this thread's slot before the gate overwrites it and is
+        // stored after every prefetched register was consumed and before the next loads are issued, so no wait for
+        // the prefetch ever covers the stores.
+        const u32x4 o0 = *reinterpret_cast<const u32x4*>(lds + r * 528 + 64 * cb);
+        const u32x4 o1 = *reinterpret_cast<const u32x4*>(lds + r * 528 + 64 * cb + 16);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            *reinterpret_cast<f32x4*>(&sG[r * RS32 + 16 * cb + 4 * i]) =
+                f32x4{gv[4 * i], gv[4 * i + 1], gv[4 * i + 2], gv[4 * i + 3]};
+        if (cb == 0) sBeta[r] = bt;
+        if (cl > 0 && r < 64) {  // the previous chunk was a full one
+            u32x4* dst = reinterpret_cast<u32x4*>(p.out + ((int64_t)t0 - 64 + r) * p.out_rs + (int64_t)h * D + 16 * cb);
+            dst[0] = o0;
+            dst[1] = o1;
+        }
+        if (cl + 1 < nch) load_row<RG>(p, h, t0 + 64, min(64, len - 64 * (cl + 1)), r, cb, RB, nx);
+        lds_barrier();
+        // ================= P1: gate cumsum inside 16-row segments
+        {
+            const int c = tid & 127, s = tid >> 7;
+            float x[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) x[i] = sG[(16 * s + i) * RS32 + c];
+#pragma unroll
+            for (int i = 1; i < 16; ++i) x[i] += x[i - 1];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) sG[(16 * s + i) * RS32 + c] = x[i];
+            sWt[s * 128 + c] = x[15];
+        }
+        lds_barrier();
+        // ================= P2: element factors (raw threads) and block factors (channel threads)
+        float kfi[16];
+        {
+            float qf[16], kf[16], qfi[16], kfj[16];
+            {
+                const u32x4* qs = reinterpret_cast<const u32x4*>(lds + LDS_B + r * (4 * RS32) + 64 * cb);
+                const u32x4* ks = reinterpret_cast<const u32x4*>(lds + LDS_C + r * (4 * RS32) + 64 * cb);
+                const u32x4 a[2] = {qs[0], qs[1]}, b[2] = {ks[0], ks[1]};
+                unpack16(a, qf);
+                unpack16(b, kf);
+            }
+            const int I = r >> 4, mr = 16 * I + 7;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const f32x4 a = *reinterpret_cast<const f32x4*>(&sG[r * RS32 + 16 * cb + 4 * i]);
+                const f32x4 b = *reinterpret_cast<const f32x4*>(&sG[mr * RS32 + 16 * cb + 4 * i]);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int c = 4 * i + j;
+                    const float d = a[j] - b[j];  // Gamma_r - Gamma_m (the segment offset cancels)
+                    const float fi = __expf(d), fj = __expf(-d);
+                    const float kh = kf[c] * rk;
+                    kfi[c] = kh * fi;
+                    kfj[c] = kh * fj;
+                    qfi[c] = qf[c] * rq * fi;
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                *reinterpret_cast<f32x4*>(&sQA[r * RS32 + 16 * cb + 4 * i]) =
+                    f32x4{qfi[4 * i], qfi[4 * i + 1], qfi[4 * i + 2], qfi[4 * i + 3]};
+                *reinterpret_cast<f32x4*>(&sKB[r * RS32 + 16 * cb + 4 * i]) =
+                    f32x4{kfj[4 * i], kfj[4 * i + 1], kfj[4 * i + 2], kfj[4 * i + 3]};
+            }
+        }
+        {
+            const int c = tid & 127, qd = tid >> 7;
+            const float o1 = sWt[c], o2 = o1 + sWt[128 + c], o3 = o2 + sWt[256 + c];
+            float gr[8];  // Gamma at rows 8w' + 7
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float off = (i < 2) ? 0.f : (i < 4) ? o1 : (i < 6) ? o2 : o3;
+                gr[i] = sG[(8 * i + 7) * RS32 + c] + off;
+            }
+#pragma unroll
+            for (int f = 0; f < F_ROWS; ++f) {  // unrolled: gr[] is indexed by constants only (stays in registers)
+                if ((f & 3) != qd) continue;
+                float x;
+                if (f < F_B) {                       // a_I, I = f + 1: Gamma_m(I) - Gamma_{16I-1}
+                    const int I = f + 1;
+                    x = gr[2 * I] - gr[2 * I - 1];
+                } else if (f < F_X) {                // b_IJ
+                    const int t = f - F_B;
+                    const int I = t < 1 ? 1 : (t < 3 ? 2 : 3);
+                    const int J = t - (I * (I - 1)) / 2;
+                    x = gr[2 * I - 1] - gr[2 * J];
+                } else if (f < F_Y) {
+                    x = gr[2 * (f - F_X)];
+                } else if (f < F_DEC) {
+                    x = gr[7] - gr[2 * (f - F_Y)];
+                } else {
+                    x = gr[7];
+                }
+                sF[f * 128 + c] = __expf(x);
+            }
+        }
+        lds_barrier();
+        // ================= P3: k^ fi over the (now unused) gate rows
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            *reinterpret_cast<f32x4*>(&sKA[r * RS32 + 16 * cb + 4 * i]) =
+                f32x4{kfi[4 * i], kfi[4 * i + 1], kfi[4 * i + 2], kfi[4 * i + 3]};
+        lds_barrier();
+        // ================= P4: Gram tiles
+        if (w < 4) {
+            const int I = w, i = 16 * I + m;
+            f32x4 akk = {0.f, 0.f, 0.f, 0.f}, aqk = akk;
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                const int c0 = 32 * s + 8 * g;
+                bf16x8 kah, kal, qah, qal, kbh, kbl;
+#pragma unroll
+                for (int hf = 0; hf < 2; ++hf) {
+                    const f32x4 ka = *reinterpret_cast<const f32x4*>(&sKA[i * RS32 + c0 + 4 * hf]);
+                    const f32x4 qa = *reinterpret_cast<const f32x4*>(&sQA[i * RS32 + c0 + 4 * hf]);
+                    const f32x4 kb = *reinterpret_cast<const f32x4*>(&sKB[i * RS32 + c0 + 4 * hf]);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const int e = 4 * hf + j;
+                        const __bf16 a1 = (__bf16)ka[j], a2 = (__bf16)qa[j], a3 = (__bf16)kb[j];
+                        kah[e] = a1; kal[e] = (__bf16)(ka[j] - (float)a1);
+                        qah[e] = a2; qal[e] = (__bf16)(qa[j] - (float)a2);
+                        kbh[e] = a3; kbl[e] = (__bf16)(kb[j] - (float)a3);
+                    }
+                }
+                akk = mfma32bf(kah, kbh, akk);
+                akk = mfma32bf(kah, kbl, akk);
+                akk = mfma32bf(kal, kbh, akk);
+                aqk = mfma32bf(qah, kbh, aqk);
+                aqk = mfma32bf(qah, kbl, aqk);
+                aqk = mfma32bf(qal, kbh, aqk);
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int rr = 4 * g + e, rw = 16 * I + rr;
+                sL[(I * 16 + rr) * 17 + m] = (m < rr) ? sBeta[rw] * akk[e] : 0.f;
+                sAq[rw * RS16S + pos64(16 * I + m)] = (half_t)((m <= rr) ? aqk[e] : 0.f);
+            }
+        } else {
+            const int I = (w == 4) ? 1 : ((w == 5) ? 2 : 3);
+            const int J0 = (w == 7) ? 2 : 0;
+            const int nJ = (w == 4 || w == 7) ? 1 : 2;
+            const int i = 16 * I + m;
+            f32x4 akk[2], aqk[2];
+#pragma unroll
+            for (int t = 0; t < 2; ++t) { akk[t] = f32x4{0.f, 0.f, 0.f, 0.f}; aqk[t] = akk[t]; }
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                const int c0 = 32 * s + 8 * g;
+                f16x8 ka, qa;
+#pragma unroll
+                for (int hf = 0; hf < 2; ++hf) {
+                    const f32x4 a = *reinterpret_cast<const f32x4*>(&sKA[i * RS32 + c0 + 4 * hf]);
+                    const f32x4 q4 = *reinterpret_cast<const f32x4*>(&sQA[i * RS32 + c0 + 4 * hf]);
+                    const f32x4 fa = *reinterpret_cast<const f32x4*>(&sF[(F_A + I - 1) * 128 + c0 + 4 * hf]);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        ka[4 * hf + j] = (half_t)(a[j] * fa[j]);
+                        qa[4 * hf + j] = (half_t)(q4[j] * fa[j]);
+                    }
+                }
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    if (t < nJ) {
+                        const int J = J0 + t, jr = 16 * J + m;
+                        const int fb = F_B + (I * (I - 1)) / 2 + J;
+                        f16x8 kb;
+#pragma unroll
+                        for (int hf = 0; hf < 2; ++hf) {
+                            const f32x4 b = *reinterpret_cast<const f32x4*>(&sKB[jr * RS32 + c0 + 4 * hf]);
+                            const f32x4 fbv = *reinterpret_cast<const f32x4*>(&sF[fb * 128 + c0 + 4 * hf]);
+#pragma unroll
+                            for (int j = 0; j < 4; ++j) kb[4 * hf + j] = (half_t)(b[j] * fbv[j]);
+                        }
+                        akk[t] = mfma32(ka, kb, akk[t]);
+                        aqk[t] = mfma32(qa, kb, aqk[t]);
+                    }
+                }
+            }
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                if (t < nJ) {
+                    const int J = J0 + t;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int rw = 16 * I + 4 * g + e, col = 16 * J + m;
+                        sAk[rw * RS16S + col] = (half_t)(-sBeta[rw] * akk[t][e]);
+                        sAq[rw * RS16S + pos64(col)] = (half_t)aqk[t][e];
+                    }
+                }
+            }
+        }
+        lds_barrier();
+        // ================= P5: T_II (wave 0); Q~, Kd^T, beta v into their walk layouts (raw threads)
+        float qfi[16], kfj[16], vf[16];
+        {
+            const u32x4* vs = reinterpret_cast<const u32x4*>(lds + LDS_W + r * (2 * RS16) + 32 * cb);
+            const u32x4 a[2] = {vs[0], vs[1]};
+            unpack16(a, vf);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const f32x4 a = *reinterpret_cast<const f32x4*>(&sQA[r * RS32 + 16 * cb + 4 * i]);
+            const f32x4 b = *reinterpret_cast<const f32x4*>(&sKB[r * RS32 + 16 * cb + 4 * i]);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) { qfi[4 * i + j] = a[j]; kfj[4 * i + j] = b[j]; }
+        }
+        lds_barrier();  // regions B and C are rewritten below
+        if (w == 0) {  // T_II = (I + L_II)^-1, lane (block I, column j); overlaps the layout writes of the other waves
+            const int I = lane >> 4, j = lane & 15;
+            const float* Lb = sL + I * 16 * 17;
+            float x[16];
+#pragma unroll
+            for (int ii = 0; ii < 16; ++ii) x[ii] = (ii == j) ? 1.f : 0.f;
+#pragma unroll
+            for (int k = 0; k < 15; ++k)  // right-looking: x[k] is final, push it into the rows below
+#pragma unroll
+                for (int ii = k + 1; ii < 16; ++ii) x[ii] -= Lb[ii * 17 + k] * x[k];
+#pragma unroll
+            for (int ii = 0; ii < 16; ++ii) sAk[(16 * I + ii) * RS16S + 16 * I + j] = (half_t)x[ii];
+        }
+        {
+            const int I = r >> 4;
+            const int hb = cb & 1, blk = cb >> 1;
+#pragma unroll
+            for (int gq = 0; gq < 4; ++gq) {
+                const f32x4 xf = *reinterpret_cast<const f32x4*>(&sF[(F_X + I) * 128 + 16 * cb + 4 * gq]);
+                f16x4 o;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) o[e] = (half_t)(qfi[4 * gq + e] * xf[e]);
+                *reinterpret_cast<f16x4*>(&sQt[r * RS16 + 32 * blk + 8 * gq + 4 * hb]) = o;
+            }
+            // Kd^T row of key channel k is stored at row 16 (k / 16) + (k % 16 ^ k / 16): the 8 channel blocks of a
+            // column write then land on 8 different banks
+            const int pr = pos64(r);
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const float y = sF[(F_Y + I) * 128 + 16 * cb + e];
+                sKd[(16 * cb + (e ^ cb)) * RS16S + pr] = (half_t)(kfj[e] * y);
+            }
+            const float b = sBeta[r];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                f16x8 o;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) o[e] = (half_t)(b * vf[8 * i + e]);
+                *reinterpret_cast<f16x8*>(&sBV[r * RS16 + 16 * cb + 8 * i]) = o;
+            }
+        }
+        lds_barrier();
+        // ================= P6: W and U by block forward substitution (wave w: channel / value tile w)
+        f32x4 Ur[4];
+        {
+            const int c = 16 * w + m;
+            f32x4 Xw[4];
+#pragma unroll
+            for (int I = 0; I < 4; ++I) {
+                const float xI = sF[(F_X + I) * 128 + c];
+                f32x4 aw, au;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int rw = 16 * I + 4 * g + e;
+                    aw[e] = sBeta[rw] * sKA[rw * RS32 + c] * xI;
+                    au[e] = (float)sBV[rw * RS16 + c];
+                }
+#pragma unroll
+                for (int J = 0; J < I; ++J) {
+                    const f16x4 A = *reinterpret_cast<const f16x4*>(&sAk[(16 * I + m) * RS16S + 16 * J + 4 * g]);
+                    f16x4 bw, bu;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) { bw[e] = (half_t)Xw[J][e]; bu[e] = (half_t)Ur[J][e]; }
+                    aw = mfma16(A, bw, aw);
+                    au = mfma16(A, bu, au);
+                }
+                const f16x4 T = *reinterpret_cast<const f16x4*>(&sAk[(16 * I + m) * RS16S + 16 * I + 4 * g]);
+                f16x4 bw, bu;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) { bw[e] = (half_t)aw[e]; bu[e] = (half_t)au[e]; }
+                const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+                Xw[I] = mfma16(T, bw, z);
+                Ur[I] = mfma16(T, bu, z);
+            }
+            const int pc = 32 * (c >> 5) + pos32(c & 31);
+#pragma unroll
+            for (int I = 0; I < 4; ++I)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) sW[(16 * I + 4 * g + e) * RS16 + pc] = (half_t)Xw[I][e];
+        }
+        lds_barrier();
+        // ================= P7: the walk
+        {
+            f16x8 SB[4];
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    SB[s][e] = (half_t)S[2 * s][e];
+                    SB[s][4 + e] = (half_t)S[2 * s + 1][e];
+                }
+            f32x4 Vp[4];
+#pragma unroll
+            for (int it = 0; it < 4; ++it) {
+                f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int s = 0; s < 4; ++s)
+                    acc = mfma32(*reinterpret_cast<const f16x8*>(&sW[(16 * it + m) * RS16 + 32 * s + 8 * g]), SB[s], acc);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) Vp[it][e] = Ur[it][e] - acc[e];
+            }
+            f16x8 VB[2];
+#pragma unroll
+            for (int s = 0; s < 2; ++s)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    VB[s][e] = (half_t)Vp[2 * s][e];
+                    VB[s][4 + e] = (half_t)Vp[2 * s + 1][e];
+                }
+            // O is staged in region A: token tk, value v at byte tk * 528 + 64 (v / 16) + 2 (v % 16) -- the first half of
+            // the 64-byte slot the raw thread (tk, v / 16) later fills with its gate values
+            uint16_t* sO = reinterpret_cast<uint16_t*>(lds + LDS_A) + 32 * w + m;
+#pragma unroll
+            for (int it = 0; it < 4; ++it) {
+                f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int s = 0; s < 4; ++s)
+                    acc = mfma32(*reinterpret_cast<const f16x8*>(&sQt[(16 * it + m) * RS16 + 32 * s + 8 * g]), SB[s], acc);
+#pragma unroll
+                for (int s = 0; s < 2; ++s)
+                    if (s <= (it >> 1))
+                        acc = mfma32(*reinterpret_cast<const f16x8*>(&sAq[(16 * it + m) * RS16S + 32 * s + 8 * g]), VB[s],
+                                     acc);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) sO[(16 * it + 4 * g + e) * (2 * RS32)] = (uint16_t)f2bf(p.scale * acc[e]);
+            }
+#pragma unroll
+            for (int dt = 0; dt < 8; ++dt) {
+                const f32x4 d4 = *reinterpret_cast<const f32x4*>(&sF[F_DEC * 128 + 16 * dt + 4 * g]);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) S[dt][e] *= d4[e];
+#pragma unroll
+                for (int s = 0; s < 2; ++s)
+                    S[dt] = mfma32(*reinterpret_cast<const f16x8*>(&sKd[(16 * dt + (m ^ dt)) * RS16S + 32 * s + 8 * g]), VB[s],
+                                   S[dt]);
+            }
+        }
+        if (ck_mode == 1 && cl + 1 == ck_single) ck_store(ck_idx[n]);
+        if (ck_mode == 2 && every > 0 && (cl + 1) % every == 0 && cl + 1 < nch) ck_store(ck_idx[ck_row0 + (cl + 1) / every]);
+        lds_barrier();
+    }
+    if (nch > 0) store_out_slot(p, h, tstart + 64 * (nch - 1), min(64, len - 64 * (nch - 1)), r, cb, lds);
     // ---- final state
     if (pool) {
-        if (row >= 0 && row < p.state_slots) store_state_rows(p.state_pool + row * p.state_ss + (int64_t)h * D * D, S, wv, gq, m);
+        if (row >= 0 && row < p.state_slots) store_state(p.state_pool + row * p.state_ss + (int64_t)h * D * D, S, w, g, m);
     } else {
-        store_state_rows(p.final_state + ((int64_t)n * H + h) * D * D, S, wv, gq, m);
+        store_state(p.final_state + ((int64_t)n * H + h) * D * D, S, w, g, m);
     }
 }
 
-template <bool RG, bool RB, bool NM>
-hipError_t launch_prologue(const PfParams& p, int nchunks, hipStream_t s) {
-    const size_t smem = sizeof(PrologueSmem);
+template <bool RG>
+hipError_t launch_chunk(const PfParams& p, int grid, hipStream_t s) {
     static bool attr_set = false;  // idempotent; a race only repeats the call
     if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&prologue_kernel<RG, RB, NM>),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&chunk_kernel<RG>),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, LDS_TOTAL);
         if (e != hipSuccess) return e;
         attr_set = true;
     }
-    hipLaunchKernelGGL((prologue_kernel<RG, RB, NM>), dim3(nchunks * p.H), dim3(PF_THREADS), smem, s, p);
+    hipLaunchKernelGGL((chunk_kernel<RG>), dim3(grid), dim3(PF_THREADS), LDS_TOTAL, s, p, p.tab, p.ck_idx);
     return hipGetLastError();
 }
 
@@ -658,10 +723,7 @@ extern "C" int kda355_prefill_plan(const KdaPrefillPlanIn* in, KdaPrefillPlan* p
     const int every_chunks = in->ck_every / KDA355_CHUNK;
     int64_t nchunks = 0;
     for (int n = 0; n < N; ++n) nchunks += (cu[n + 1] - cu[n] + 63) / 64;
-    const int64_t off_chunk = H_WORDS;
-    const int64_t off_chain = off_chunk + 2 * nchunks;
-    const int64_t off_seq = off_chain + 4 * (int64_t)N;
-    const int64_t words = off_seq + 2 * (int64_t)N;
+    const int64_t words = H_WORDS + (int64_t)C_WORDS * N;
     plan->T = T;
     plan->N = N;
     plan->H = in->H;
@@ -676,7 +738,7 @@ extern "C" int kda355_prefill_plan(const KdaPrefillPlanIn* in, KdaPrefillPlan* p
     }
     plan->max_chain_chunks = maxc;
     plan->table_words = words;
-    plan->workspace_bytes = nchunks * (int64_t)in->H * WS_BYTES;
+    plan->workspace_bytes = 0;  // the fused kernel keeps every per-chunk operand on chip
     plan->ck_rows = ckrows;
     plan->magic = PLAN_MAGIC;
     plan->flags = in->flags;
@@ -685,49 +747,43 @@ extern "C" int kda355_prefill_plan(const KdaPrefillPlanIn* in, KdaPrefillPlan* p
     if (!tables) return 0;
     KDA_CHECK_ARG(capacity >= words, "prefill_plan: table capacity %lld < %lld words", (long long)capacity, (long long)words);
     int32_t* t = tables;
-    std::fill(t, t + H_WORDS, 0);
+    std::fill(t, t + words, 0);
     t[H_MAGIC] = (int32_t)PLAN_MAGIC;
     t[H_N] = N;
     t[H_T] = (int32_t)T;
     t[H_NCHUNK] = (int32_t)nchunks;
     t[H_EVERY] = every_chunks;
-    t[H_OFF_CHUNK] = (int32_t)off_chunk;
-    t[H_OFF_CHAIN] = (int32_t)off_chain;
-    t[H_OFF_SEQ] = (int32_t)off_seq;
+    t[H_OFF_CHAIN] = H_WORDS;
+    t[H_NCHAIN] = N;
     t[H_CKROWS] = (int32_t)ckrows;
-    std::vector<int> first(N);
-    int64_t c = 0;
+    std::vector<int> ck_chunk(N, 0), ck_row0(N, 0);
     int64_t ckstart = 0;
     for (int n = 0; n < N; ++n) {
-        first[n] = (int)c;
-        for (int64_t s0 = cu[n]; s0 < cu[n + 1]; s0 += 64, ++c) {
-            t[off_chunk + 2 * c] = (int32_t)s0;
-            t[off_chunk + 2 * c + 1] = (int32_t)std::min<int64_t>(64, cu[n + 1] - s0);
-        }
-        int ck_chunk = 0;
         if (in->ck_offsets) {
             const int32_t o = in->ck_offsets[n];
             // kda/mi350x/kda/prefill/main.cpp:110-118: offsets that are not positive multiples of 64 within the sequence
             // write nothing
-            if (o > 0 && o % 64 == 0 && o <= cu[n + 1] - cu[n]) ck_chunk = o / 64;
+            if (o > 0 && o % 64 == 0 && o <= cu[n + 1] - cu[n]) ck_chunk[n] = o / 64;
         }
-        t[off_seq + 2 * n] = ck_chunk;
-        t[off_seq + 2 * n + 1] = (int32_t)ckstart;
+        ck_row0[n] = (int)ckstart;
         if (every_chunks) {
             const int cn = (int)((cu[n + 1] - cu[n] + 63) / 64);
             ckstart += (cn + every_chunks - 1) / every_chunks;
         }
     }
-    // chains longest first (the walk's critical path starts earliest)
+    // chains longest first (the longest critical paths start earliest when the grid runs in several waves)
     std::vector<int> order(N);
     std::iota(order.begin(), order.end(), 0);
     std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return cu[a + 1] - cu[a] > cu[b + 1] - cu[b]; });
     for (int i = 0; i < N; ++i) {
         const int n = order[i];
-        t[off_chain + 4 * i] = n;
-        t[off_chain + 4 * i + 1] = first[n];
-        t[off_chain + 4 * i + 2] = (int)((cu[n + 1] - cu[n] + 63) / 64);
-        t[off_chain + 4 * i + 3] = (int32_t)cu[n];
+        int32_t* e = t + H_WORDS + (int64_t)C_WORDS * i;
+        e[C_SEQ] = n;
+        e[C_NCH] = (int)((cu[n + 1] - cu[n] + 63) / 64);
+        e[C_TSTART] = (int32_t)cu[n];
+        e[C_LEN] = (int32_t)(cu[n + 1] - cu[n]);
+        e[C_CKSINGLE] = ck_chunk[n];
+        e[C_CKROW0] = ck_row0[n];
     }
     return 0;
 }
@@ -746,7 +802,6 @@ extern "C" int kda355_prefill_launch(const KdaPrefillArgs* a, kda355_stream_t st
                   pl->H, a->N, (long long)a->T, a->H);
     const uint32_t f = a->flags;
     KDA_CHECK_ARG(a->q && a->k && a->v && a->g && a->beta && a->out && a->tables, "prefill: a required pointer is null");
-    KDA_CHECK_ARG(pl->num_chunks == 0 || a->workspace, "prefill: workspace is null");
     KDA_CHECK_ARG(!(f & KDA355_PF_RAW_GATE) || (a->A_log && a->dt_bias), "prefill: raw gate needs A_log and dt_bias");
     const bool pool = f & KDA355_PF_POOL;
     KDA_CHECK_ARG(pool ? (a->state_pool && a->state_idx && a->has_initial_state) : (a->final_state != nullptr),
@@ -757,15 +812,15 @@ extern "C" int kda355_prefill_launch(const KdaPrefillArgs* a, kda355_stream_t st
     KDA_CHECK_ARG(!(f & KDA355_PF_CK_EVERY) || pl->ck_every > 0, "prefill: every-n checkpoints need a plan with ck_every");
     KDA_CHECK_ARG(aligned(a->q, 16) && aligned(a->k, 16) && aligned(a->v, 16) && a->qkv_row_stride % 8 == 0,
                   "prefill: q/k/v rows must be 16-byte aligned");
-    KDA_CHECK_ARG((f & KDA355_PF_RAW_GATE) ? (aligned(a->g, 8) && a->g_row_stride % 4 == 0)
+    // every row piece is moved as 16-byte vectors: 16-byte aligned bases and row strides
+    KDA_CHECK_ARG((f & KDA355_PF_RAW_GATE) ? (aligned(a->g, 16) && a->g_row_stride % 8 == 0)
                                            : (aligned(a->g, 16) && a->g_row_stride % 4 == 0),
-                  "prefill: g rows misaligned");
-    KDA_CHECK_ARG(aligned(a->out, 2), "prefill: out misaligned");
+                  "prefill: g rows must be 16-byte aligned");
+    KDA_CHECK_ARG(aligned(a->out, 16) && a->out_row_stride % 8 == 0, "prefill: out rows must be 16-byte aligned");
     KDA_CHECK_ARG(!pool || (aligned(a->state_pool, 16) && a->state_slot_stride % 4 == 0), "prefill: state pool misaligned");
     KDA_CHECK_ARG(pool || (aligned(a->final_state, 16) && (!a->initial_state || aligned(a->initial_state, 16))),
                   "prefill: states misaligned");
     KDA_CHECK_ARG(!a->ck_pool || (aligned(a->ck_pool, 16) && a->ck_slot_stride % 8 == 0), "prefill: ck pool misaligned");
-    KDA_CHECK_ARG(aligned(a->workspace, 256), "prefill: workspace must be 256-byte aligned");
     if (a->N == 0) return 0;
     PfParams p;
     p.q = static_cast<const uint16_t*>(a->q);
@@ -784,7 +839,6 @@ extern "C" int kda355_prefill_launch(const KdaPrefillArgs* a, kda355_stream_t st
     p.ck_pool = a->ck_pool;
     p.ck_idx = a->ck_idx;
     p.tab = a->tables;
-    p.ws = static_cast<uint8_t*>(a->workspace);
     p.qkv_rs = a->qkv_row_stride;
     p.g_rs = a->g_row_stride;
     p.beta_rs = a->beta_row_stride;
@@ -800,26 +854,10 @@ extern "C" int kda355_prefill_launch(const KdaPrefillArgs* a, kda355_stream_t st
     p.flags = f;
     p.ck_bf16 = a->ck_dtype == 1;
     const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    hipError_t e = hipSuccess;
-    if (pl->num_chunks > 0) {
-        const bool rg = f & KDA355_PF_RAW_GATE, rb = f & KDA355_PF_RAW_BETA, nm = f & KDA355_PF_NORMALIZE_QK;
-        if (rg) {
-            e = rb ? (nm ? launch_prologue<true, true, true>(p, pl->num_chunks, s) : launch_prologue<true, true, false>(p, pl->num_chunks, s))
-                   : (nm ? launch_prologue<true, false, true>(p, pl->num_chunks, s) : launch_prologue<true, false, false>(p, pl->num_chunks, s));
-        } else {
-            e = rb ? (nm ? launch_prologue<false, true, true>(p, pl->num_chunks, s) : launch_prologue<false, true, false>(p, pl->num_chunks, s))
-                   : (nm ? launch_prologue<false, false, true>(p, pl->num_chunks, s) : launch_prologue<false, false, false>(p, pl->num_chunks, s));
-        }
-        if (e != hipSuccess) {
-            set_error("prefill: prologue launch failed: %s", hipGetErrorString(e));
-            return KDA355_ELAUNCH;
-        }
-    }
-    const size_t wsm = sizeof(WalkSmem);
-    hipLaunchKernelGGL(walk_kernel, dim3(pl->num_chains * p.H), dim3(PF_THREADS), wsm, s, p);
-    e = hipGetLastError();
+    const hipError_t e = (f & KDA355_PF_RAW_GATE) ? launch_chunk<true>(p, pl->num_chains * p.H, s)
+                                                  : launch_chunk<false>(p, pl->num_chains * p.H, s);
     if (e != hipSuccess) {
-        set_error("prefill: walk launch failed: %s", hipGetErrorString(e));
+        set_error("prefill: launch failed: %s", hipGetErrorString(e));
         return KDA355_ELAUNCH;
     }
     return 0;

@@ -69,7 +69,7 @@ def test_prefill_plan_host_only():
     pl = _lib.KdaPrefillPlan()
     assert L.kda355_prefill_plan(ctypes.byref(pin), ctypes.byref(pl), None, 0) == 0
     assert pl.num_chunks == 2 + 0 + 4 + 64 and pl.T == 4396 and pl.ck_rows == 1 + 0 + 2 + 32
-    assert L.kda355_prefill_workspace_bytes(ctypes.byref(pl)) == pl.num_chunks * 8 * 82432
+    assert L.kda355_prefill_workspace_bytes(ctypes.byref(pl)) == 0   # the fused kernel keeps chunk operands on chip
     tab = np.zeros(pl.table_words, np.int32)
     assert L.kda355_prefill_plan(ctypes.byref(pin), ctypes.byref(pl), ctypes.c_void_p(tab.ctypes.data), tab.size) == 0
     assert L.kda355_prefill_plan(ctypes.byref(pin), ctypes.byref(pl), ctypes.c_void_p(tab.ctypes.data), 3) == _lib.EINVAL
