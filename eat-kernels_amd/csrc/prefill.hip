@@ -55,12 +55,13 @@ constexpr int LDS_C = 68608;
 constexpr int LDS_W = 102400;
 constexpr int LDS_AQ = 119808;
 constexpr int LDS_AK = 129024;
-constexpr int LDS_L = 138240;
+constexpr int LDS_UNUSED = 138240;  // 4352 bytes
 constexpr int LDS_F = 142592;
 constexpr int LDS_WT = 151808;
 constexpr int LDS_BETA = 153856;
 constexpr int LDS_DT = 154112;    // dt_bias of the head (gate-in-kernel) fp32 [128]
-constexpr int LDS_TOTAL = 154624;
+constexpr int LDS_L = 154624;     // A_kk diagonal blocks, transposed: [block][column][row], rows padded to 20
+constexpr int LDS_TOTAL = 159744;
 // per-channel factor rows of LDS_F
 constexpr int F_A = 0;      // a_I = e^{Gamma_m(I) - Gamma_{16I-1}}, I = 1..3          (rows 0..2)
 constexpr int F_B = 3;      // b_IJ = e^{Gamma_{16I-1} - Gamma_m(J)}, row 3 + I(I-1)/2 + J (rows 3..8)
@@ -89,6 +90,8 @@ __device__ __forceinline__ f32x4 mfma16(f16x4 a, f16x4 b, f32x4 c) {
 // storage position of index q (0..31) inside a permuted 32-block: q = 16h + 4g + e  ->  8g + 4h + e
 __device__ __forceinline__ int pos32(int q) { return ((q >> 2) & 3) * 8 + ((q >> 4) << 2) + (q & 3); }
 __device__ __forceinline__ int pos64(int q) { return (q & 32) + pos32(q & 31); }
+// 2^x (v_exp_f32)
+__device__ __forceinline__ float exp2_(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // Workgroup barrier for LDS traffic only.  __syncthreads() also fences global memory (s_waitcnt vmcnt(0)), which
 // would wait for the next chunk's prefetched loads and for the output stores at every phase boundary; the waves of
@@ -218,7 +221,7 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
     half_t* sW = reinterpret_cast<half_t*>(lds + LDS_W);     // W (channels permuted)
     half_t* sAq = reinterpret_cast<half_t*>(lds + LDS_AQ);   // A_qk (columns permuted)
     half_t* sAk = reinterpret_cast<half_t*>(lds + LDS_AK);   // -A_kk off-diagonal blocks, T_II diagonal blocks
-    float* sL = reinterpret_cast<float*>(lds + LDS_L);       // A_kk diagonal blocks [4][16][17]
+    float* sL = reinterpret_cast<float*>(lds + LDS_L);       // A_kk diagonal blocks, column-major [4][16][20]
     float* sF = reinterpret_cast<float*>(lds + LDS_F);       // per-channel factors [18][128]
     float* sWt = reinterpret_cast<float*>(lds + LDS_WT);     // segment totals of the gate cumsum [4][128]
     float* sBeta = reinterpret_cast<float*>(lds + LDS_BETA);
@@ -314,6 +317,8 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
                 for (int j = 0; j < 4; ++j) gv[4 * i + j] = __uint_as_float(nx.g[i][j]);
         }
         const float bt = (r >= L) ? 0.f : (RB ? sigmoidf_(bf2f(nx.beta)) : __uint_as_float(nx.beta));
+#pragma unroll
+        for (int c = 0; c < 16; ++c) gv[c] *= 1.4426950408889634f;  // log2(e): the cumsum runs in log2 units
         float rq = 1.f, rk = 1.f;
         if (NORM) {  // F.normalize(x, eps=1e-6) = x / max(|x|, 1e-6)  (kda/mi350x/reference.py:59-60)
             float qf[16], kf[16];
@@ -327,8 +332,8 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
             for (int c = 0; c < 16; ++c) { sq += qf[c] * qf[c]; sk += kf[c] * kf[c]; }
             sq = sum8(sq);
             sk = sum8(sk);
-            rq = 1.f / fmaxf(sqrtf(sq), 1e-6f);
-            rk = 1.f / fmaxf(sqrtf(sk), 1e-6f);
+            rq = __builtin_amdgcn_rcpf(fmaxf(sqrtf(sq), 1e-6f));
+            rk = __builtin_amdgcn_rcpf(fmaxf(sqrtf(sk), 1e-6f));
         }
         // The previous chunk's staged output is read from this thread's slot before the gate overwrites it and is
         // stored after every prefetched register was consumed and before the next loads are issued, so no wait for
@@ -380,7 +385,7 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
                 for (int j = 0; j < 4; ++j) {
                     const int c = 4 * i + j;
                     const float d = a[j] - b[j];  // Gamma_r - Gamma_m (the segment offset cancels)
-                    const float fi = __expf(d), fj = __expf(-d);
+                    const float fi = exp2_(d), fj = exp2_(-d);
                     const float kh = kf[c] * rk;
                     kfi[c] = kh * fi;
                     kfj[c] = kh * fj;
@@ -423,7 +428,7 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
                 } else {
                     x = gr[7];
                 }
-                sF[f * 128 + c] = __expf(x);
+                sF[f * 128 + c] = exp2_(x);
             }
         }
         lds_barrier();
@@ -462,12 +467,14 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
                 aqk = mfma32bf(qah, kbl, aqk);
                 aqk = mfma32bf(qal, kbh, aqk);
             }
+            f32x4 lt;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int rr = 4 * g + e, rw = 16 * I + rr;
-                sL[(I * 16 + rr) * 17 + m] = (m < rr) ? sBeta[rw] * akk[e] : 0.f;
+                lt[e] = (m < rr) ? sBeta[rw] * akk[e] : 0.f;
                 sAq[rw * RS16S + pos64(16 * I + m)] = (half_t)((m <= rr) ? aqk[e] : 0.f);
             }
+            *reinterpret_cast<f32x4*>(&sL[(I * 16 + m) * 20 + 4 * g]) = lt;
         } else {
             const int I = (w == 4) ? 1 : ((w == 5) ? 2 : 3);
             const int J0 = (w == 7) ? 2 : 0;
@@ -540,14 +547,21 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
         lds_barrier();  // regions B and C are rewritten below
         if (w == 0) {  // T_II = (I + L_II)^-1, lane (block I, column j); overlaps the layout writes of the other waves
             const int I = lane >> 4, j = lane & 15;
-            const float* Lb = sL + I * 16 * 17;
+            const float* Lb = sL + I * 16 * 20;  // column k of L_II is the contiguous row k
             float x[16];
 #pragma unroll
             for (int ii = 0; ii < 16; ++ii) x[ii] = (ii == j) ? 1.f : 0.f;
 #pragma unroll
-            for (int k = 0; k < 15; ++k)  // right-looking: x[k] is final, push it into the rows below
+            for (int k = 0; k < 15; ++k) {  // right-looking: x[k] is final, push it into the rows below
+                float col[16];
 #pragma unroll
-                for (int ii = k + 1; ii < 16; ++ii) x[ii] -= Lb[ii * 17 + k] * x[k];
+                for (int q4 = 0; q4 < 4; ++q4) {
+                    const f32x4 c4 = *reinterpret_cast<const f32x4*>(&Lb[k * 20 + 4 * q4]);
+                    col[4 * q4] = c4[0]; col[4 * q4 + 1] = c4[1]; col[4 * q4 + 2] = c4[2]; col[4 * q4 + 3] = c4[3];
+                }
+#pragma unroll
+                for (int ii = k + 1; ii < 16; ++ii) x[ii] -= col[ii] * x[k];
+            }
 #pragma unroll
             for (int ii = 0; ii < 16; ++ii) sAk[(16 * I + ii) * RS16S + 16 * I + j] = (half_t)x[ii];
         }
