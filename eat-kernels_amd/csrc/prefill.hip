@@ -138,35 +138,48 @@ struct RawRow {
     uint32_t beta;  // fp32 bits, or the bf16 raw beta in the low half (converted when the chunk is consumed)
 };
 
+// Raw buffer descriptor over the rows [t0, t0 + L) of one token-major stream (row pitch `pitch` bytes, `bytes` bytes
+// per row used): a row past the chunk end lies outside num_records, and the buffer load returns zeros for it.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const void* base, int L, int64_t pitch, int bytes) {
+    const int num = L > 0 ? (int)((int64_t)(L - 1) * pitch + bytes) : 0;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, num, 0x00020000);
+}
+__device__ __forceinline__ u32x4 bload16(__amdgpu_buffer_rsrc_t rs, int off) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
+}
+
+// One chunk's raw row slice for this thread (row r, channels 16 cb .. 16 cb + 15); rows >= L read as zeros.
 template <bool RG>
 __device__ __forceinline__ void load_row(const PfParams& p, int h, int t0, int L, int r, int cb, bool RB, RawRow& x) {
-    const u32x4 z = {0u, 0u, 0u, 0u};
-    if (r < L) {
-        const int64_t tok = (int64_t)t0 + r;
-        const int64_t o = tok * p.qkv_rs + (int64_t)h * D + 16 * cb;
-        const u32x4* q4 = reinterpret_cast<const u32x4*>(p.q + o);
-        const u32x4* k4 = reinterpret_cast<const u32x4*>(p.k + o);
-        const u32x4* v4 = reinterpret_cast<const u32x4*>(p.v + o);
-        x.q[0] = q4[0]; x.q[1] = q4[1];
-        x.k[0] = k4[0]; x.k[1] = k4[1];
-        x.v[0] = v4[0]; x.v[1] = v4[1];
-        if (RG) {
-            const u32x4* g4 = reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(p.g) + tok * p.g_rs +
-                                                             (int64_t)h * D + 16 * cb);
-            x.g[0] = g4[0]; x.g[1] = g4[1];
-            x.g[2] = z; x.g[3] = z;
-        } else {
-            const u32x4* g4 = reinterpret_cast<const u32x4*>(reinterpret_cast<const float*>(p.g) + tok * p.g_rs +
-                                                             (int64_t)h * D + 16 * cb);
-            x.g[0] = g4[0]; x.g[1] = g4[1]; x.g[2] = g4[2]; x.g[3] = g4[3];
-        }
-        x.beta = RB ? (uint32_t)reinterpret_cast<const uint16_t*>(p.beta)[tok * p.beta_rs + h]
-                    : reinterpret_cast<const uint32_t*>(p.beta)[tok * p.beta_rs + h];
+    const int64_t o = (int64_t)t0 * p.qkv_rs + (int64_t)h * D;
+    const int64_t qp = p.qkv_rs * 2;
+    const int qo = r * (int)qp + 32 * cb;
+    const __amdgpu_buffer_rsrc_t rq = rows_rsrc(p.q + o, L, qp, 256);
+    const __amdgpu_buffer_rsrc_t rk = rows_rsrc(p.k + o, L, qp, 256);
+    const __amdgpu_buffer_rsrc_t rv = rows_rsrc(p.v + o, L, qp, 256);
+    x.q[0] = bload16(rq, qo); x.q[1] = bload16(rq, qo + 16);
+    x.k[0] = bload16(rk, qo); x.k[1] = bload16(rk, qo + 16);
+    x.v[0] = bload16(rv, qo); x.v[1] = bload16(rv, qo + 16);
+    const int64_t go = (int64_t)t0 * p.g_rs + (int64_t)h * D;
+    if (RG) {
+        const int64_t gp = p.g_rs * 2;
+        const __amdgpu_buffer_rsrc_t rg = rows_rsrc(reinterpret_cast<const uint16_t*>(p.g) + go, L, gp, 256);
+        const int off = r * (int)gp + 32 * cb;
+        x.g[0] = bload16(rg, off); x.g[1] = bload16(rg, off + 16);
+        x.g[2] = u32x4{0u, 0u, 0u, 0u}; x.g[3] = x.g[2];
     } else {
-        x.q[0] = z; x.q[1] = z; x.k[0] = z; x.k[1] = z; x.v[0] = z; x.v[1] = z;
-        x.g[0] = z; x.g[1] = z; x.g[2] = z; x.g[3] = z;
-        x.beta = 0u;  // padded rows get beta = 0 when the chunk is consumed
+        const int64_t gp = p.g_rs * 4;
+        const __amdgpu_buffer_rsrc_t rg = rows_rsrc(reinterpret_cast<const float*>(p.g) + go, L, gp, 512);
+        const int off = r * (int)gp + 64 * cb;
+        x.g[0] = bload16(rg, off); x.g[1] = bload16(rg, off + 16);
+        x.g[2] = bload16(rg, off + 32); x.g[3] = bload16(rg, off + 48);
     }
+    const int es = RB ? 2 : 4;
+    const int64_t bp = p.beta_rs * es;
+    const __amdgpu_buffer_rsrc_t rb =
+        rows_rsrc(reinterpret_cast<const unsigned char*>(p.beta) + ((int64_t)t0 * p.beta_rs + h) * es, L, bp, es);
+    x.beta = RB ? (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rb, r * (int)bp, 0, 0)
+                : __builtin_amdgcn_raw_buffer_load_b32(rb, r * (int)bp, 0, 0);
 }
 
 __device__ __forceinline__ void unpack16(const u32x4 (&w)[2], float (&f)[16]) {
@@ -293,7 +306,7 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
         r = tid >> 3;
         cb = tid & 7;
         const int t0 = tstart + 64 * cl, L = min(64, len - 64 * cl);
-        // ================= P0: this chunk's raw rows; prefetch the next chunk
+        // ================= P0: this chunk's raw rows (prefetched during the previous chunk)
         // The raw q, k, v go to LDS slots that only this thread reads back and later overwrites (q: first half of its
         // q^ fi slot in region B, k: of its k^ fj slot in region C, v: the W area, which is free until P6), so the
         // registers die here and the next chunk's loads reuse them without a loop-carried copy.
@@ -345,12 +358,11 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
             *reinterpret_cast<f32x4*>(&sG[r * RS32 + 16 * cb + 4 * i]) =
                 f32x4{gv[4 * i], gv[4 * i + 1], gv[4 * i + 2], gv[4 * i + 3]};
         if (cb == 0) sBeta[r] = bt;
-        if (cl > 0 && r < 64) {  // the previous chunk was a full one
+        if (cl > 0) {  // the previous chunk was a full one
             u32x4* dst = reinterpret_cast<u32x4*>(p.out + ((int64_t)t0 - 64 + r) * p.out_rs + (int64_t)h * D + 16 * cb);
             dst[0] = o0;
             dst[1] = o1;
         }
-        if (cl + 1 < nch) load_row<RG>(p, h, t0 + 64, min(64, len - 64 * (cl + 1)), r, cb, RB, nx);
         lds_barrier();
         // ================= P1: gate cumsum inside 16-row segments
         {
@@ -531,6 +543,8 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
         }
         lds_barrier();
         // ================= P5: T_II (wave 0); Q~, Kd^T, beta v into their walk layouts (raw threads)
+        // the next chunk's rows: issued here, consumed at the next P0 (their registers are free during P1..P4)
+        if (cl + 1 < nch) load_row<RG>(p, h, t0 + 64, min(64, len - 64 * (cl + 1)), r, cb, RB, nx);
         float qfi[16], kfj[16], vf[16];
         {
             const u32x4* vs = reinterpret_cast<const u32x4*>(lds + LDS_W + r * (2 * RS16) + 32 * cb);
