@@ -72,9 +72,16 @@ constexpr int F_ROWS = 18;
 
 constexpr uint32_t PLAN_MAGIC = 0x4b443535u;  // "KD55"
 // table header words
-enum { H_MAGIC = 0, H_N, H_T, H_NCHUNK, H_EVERY, H_OFF_CHAIN, H_NCHAIN, H_CKROWS, H_WORDS = 16 };
-// one chain entry: the chunks [0, nch) of sequence n, tokens [t_start, t_start + len)
-enum { C_SEQ = 0, C_NCH, C_TSTART, C_LEN, C_CKSINGLE, C_CKROW0, C_WORDS = 8 };
+// Table: header, then three lists of entries.  The final list holds every piece that produces outputs (a whole
+// sequence, or one piece of a split sequence); the transition list holds every piece of a split sequence (run first,
+// from a zero state, recording its local end state and its state transition); the scan list holds the split
+// sequences (their pieces' start states are composed between the two).
+enum { H_MAGIC = 0, H_N, H_T, H_NCHUNK, H_EVERY, H_CKROWS, H_OFF_FINAL, H_NFINAL, H_OFF_TRANS, H_NTRANS, H_OFF_SCAN,
+       H_NSCAN, H_NSLOTS, H_WORDS = 16 };
+// one piece entry: chunks [0, nch) starting at sequence chunk `first` of sequence n, tokens [t_start, t_start + len)
+enum { C_SEQ = 0, C_NCH, C_TSTART, C_LEN, C_CKSINGLE, C_CKROW0, C_FIRST, C_FLAGS, C_SLOT, C_SEQCH, C_WORDS = 12 };
+enum { PIECE_READ_WS = 1, PIECE_LAST = 2 };  // C_FLAGS: start state from the workspace; the piece ends the sequence
+enum { S_SEQ = 0, S_NP, S_SLOT0, S_WORDS = 4 };  // scan entry: sequence, pieces, slot of piece 0
 
 typedef _Float16 half_t;
 
@@ -129,6 +136,7 @@ struct PfParams {
     float scale, lb;
     uint32_t flags;
     int ck_bf16;
+    float* ws;   // split sequences: [3][slots][H][128][128] fp32 = local end states, transitions, start states
 };
 
 // Raw inputs of one chunk row slice: row r, channels 16 cb .. 16 cb + 15.
@@ -220,9 +228,11 @@ __device__ __forceinline__ void store_state_bf16(uint16_t* dst, const f32x4 (&S)
     }
 }
 
-template <bool RG>
+// P1 = false: the chunk walk with outputs, checkpoints and states.  P1 = true: a piece of a split sequence from a
+// zero state, also carrying the piece's state transition P (S_end = P S_start + S_loc); no outputs, no checkpoints.
+template <bool RG, bool P1>
 __global__ void __launch_bounds__(PF_THREADS, 1)
-    chunk_kernel(PfParams p, const int32_t* __restrict__ tab, const int32_t* __restrict__ ck_idx) {
+    chunk_kernel(PfParams p, const int32_t* __restrict__ tab, const int32_t* __restrict__ ck_idx, int list_off) {
     extern __shared__ __align__(16) unsigned char lds[];
     float* sG = reinterpret_cast<float*>(lds + LDS_A);       // gate / Gamma, then k^ fi
     float* sKA = sG;
@@ -246,9 +256,12 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     // uniform table reads through a __restrict__ pointer: scalar loads, which never join the vector-memory counter that
     // the prefetched rows are waited on with
-    const int32_t* chain = tab + H_WORDS + C_WORDS * ci;
+    const int32_t* chain = tab + list_off + C_WORDS * ci;
     const int n = chain[C_SEQ], nch = chain[C_NCH], tstart = chain[C_TSTART], len = chain[C_LEN];
+    const int first = chain[C_FIRST], pflags = chain[C_FLAGS], slot = chain[C_SLOT], seqch = chain[C_SEQCH];
     const int every = tab[H_EVERY];
+    const int64_t ws_arr = (int64_t)tab[H_NSLOTS] * H * D * D;  // floats per workspace array
+    float* ws_h = p.ws + ((int64_t)slot * H + h) * D * D;        // this piece-head in array 0 (+ ws_arr: 1, 2)
     const bool pool = (p.flags & KDA355_PF_POOL) != 0;
     const bool RB = (p.flags & KDA355_PF_RAW_BETA) != 0;
     const bool NORM = (p.flags & KDA355_PF_NORMALIZE_QK) != 0;
@@ -258,8 +271,12 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
     f32x4 S[8];
     const float* src = nullptr;
     int64_t row = -1;
-    if (pool) {
-        row = p.state_idx[n];
+    if (pool) row = p.state_idx[n];
+    if (P1) {
+        // a piece's local run starts from zero
+    } else if (pflags & PIECE_READ_WS) {
+        src = ws_h + 2 * ws_arr;  // start state composed by the scan
+    } else if (pool) {
         if (row >= 0 && row < p.state_slots && p.has_init[n]) src = p.state_pool + row * p.state_ss + (int64_t)h * D * D;
     } else if (p.init_state) {
         src = p.init_state + ((int64_t)n * H + h) * D * D;
@@ -267,8 +284,15 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt)
         S[dt] = src ? *reinterpret_cast<const f32x4*>(src + (16 * w + m) * D + 16 * dt + 4 * g) : f32x4{0.f, 0.f, 0.f, 0.f};
+    f32x4 Pm[8];  // P1: the transition, P[k][k'] at (k = 16dt + 4g + e, k' = 16w + m); starts as the identity
+    if (P1) {
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) Pm[dt][e] = (16 * dt + 4 * g + e == 16 * w + m) ? 1.f : 0.f;
+    }
 
-    const int ck_mode = (p.flags & KDA355_PF_CK_EVERY) ? 2 : ((p.flags & KDA355_PF_CK_SINGLE) ? 1 : 0);
+    const int ck_mode = P1 ? 0 : (p.flags & KDA355_PF_CK_EVERY) ? 2 : ((p.flags & KDA355_PF_CK_SINGLE) ? 1 : 0);
     auto ck_store = [&](int64_t rr) {
         if (rr < 0 || rr >= p.ck_slots) return;
         if (p.ck_bf16)
@@ -277,7 +301,7 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
             store_state(reinterpret_cast<float*>(p.ck_pool) + rr * p.ck_ss + (int64_t)h * D * D, S, w, g, m);
     };
     const int ck_row0 = chain[C_CKROW0];
-    if (ck_mode == 2 && every > 0 && nch > 0) ck_store(ck_idx[ck_row0]);
+    if (ck_mode == 2 && every > 0 && nch > 0 && first == 0) ck_store(ck_idx[ck_row0]);
     const int ck_single = (ck_mode == 1) ? chain[C_CKSINGLE] : 0;
 
     // gate-in-kernel constants for this thread's 16 channels
@@ -358,7 +382,7 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
             *reinterpret_cast<f32x4*>(&sG[r * RS32 + 16 * cb + 4 * i]) =
                 f32x4{gv[4 * i], gv[4 * i + 1], gv[4 * i + 2], gv[4 * i + 3]};
         if (cb == 0) sBeta[r] = bt;
-        if (cl > 0) {  // the previous chunk was a full one
+        if (!P1 && cl > 0) {  // the previous chunk was a full one
             u32x4* dst = reinterpret_cast<u32x4*>(p.out + ((int64_t)t0 - 64 + r) * p.out_rs + (int64_t)h * D + 16 * cb);
             dst[0] = o0;
             dst[1] = o1;
@@ -648,7 +672,53 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
         }
         lds_barrier();
         // ================= P7: the walk
-        {
+        if (P1) {  // S <- (diag(d) - Kd^T W) S + Kd^T U and P <- (diag(d) - Kd^T W) P, sharing every A fragment
+            f16x8 SB[4], PB[4];
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    SB[s][e] = (half_t)S[2 * s][e];
+                    SB[s][4 + e] = (half_t)S[2 * s + 1][e];
+                    PB[s][e] = (half_t)Pm[2 * s][e];
+                    PB[s][4 + e] = (half_t)Pm[2 * s + 1][e];
+                }
+            f32x4 Vp[4], Wp[4];
+#pragma unroll
+            for (int it = 0; it < 4; ++it) {
+                f32x4 acc = {0.f, 0.f, 0.f, 0.f}, acp = acc;
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    const f16x8 A = *reinterpret_cast<const f16x8*>(&sW[(16 * it + m) * RS16 + 32 * s + 8 * g]);
+                    acc = mfma32(A, SB[s], acc);
+                    acp = mfma32(A, PB[s], acp);
+                }
+#pragma unroll
+                for (int e = 0; e < 4; ++e) { Vp[it][e] = Ur[it][e] - acc[e]; Wp[it][e] = -acp[e]; }
+            }
+            f16x8 VB[2], WB[2];
+#pragma unroll
+            for (int s = 0; s < 2; ++s)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    VB[s][e] = (half_t)Vp[2 * s][e];
+                    VB[s][4 + e] = (half_t)Vp[2 * s + 1][e];
+                    WB[s][e] = (half_t)Wp[2 * s][e];
+                    WB[s][4 + e] = (half_t)Wp[2 * s + 1][e];
+                }
+#pragma unroll
+            for (int dt = 0; dt < 8; ++dt) {
+                const f32x4 d4 = *reinterpret_cast<const f32x4*>(&sF[F_DEC * 128 + 16 * dt + 4 * g]);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) { S[dt][e] *= d4[e]; Pm[dt][e] *= d4[e]; }
+#pragma unroll
+                for (int s = 0; s < 2; ++s) {
+                    const f16x8 A = *reinterpret_cast<const f16x8*>(&sKd[(16 * dt + (m ^ dt)) * RS16S + 32 * s + 8 * g]);
+                    S[dt] = mfma32(A, VB[s], S[dt]);
+                    Pm[dt] = mfma32(A, WB[s], Pm[dt]);
+                }
+            }
+        } else {
             f16x8 SB[4];
 #pragma unroll
             for (int s = 0; s < 4; ++s)
@@ -703,12 +773,20 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
                                    S[dt]);
             }
         }
-        if (ck_mode == 1 && cl + 1 == ck_single) ck_store(ck_idx[n]);
-        if (ck_mode == 2 && every > 0 && (cl + 1) % every == 0 && cl + 1 < nch) ck_store(ck_idx[ck_row0 + (cl + 1) / every]);
+        // checkpoints at chunk boundaries, counted in chunks of the whole sequence
+        const int cs = first + cl + 1;
+        if (ck_mode == 1 && cs == ck_single) ck_store(ck_idx[n]);
+        if (ck_mode == 2 && every > 0 && cs % every == 0 && cs < seqch) ck_store(ck_idx[ck_row0 + cs / every]);
         lds_barrier();
     }
+    if (P1) {  // the piece's local end state and transition (stored [k'][k])
+        store_state(ws_h, S, w, g, m);
+        store_state(ws_h + ws_arr, Pm, w, g, m);
+        return;
+    }
     if (nch > 0) store_out_slot(p, h, tstart + 64 * (nch - 1), min(64, len - 64 * (nch - 1)), r, cb, lds);
-    // ---- final state
+    // ---- final state (the last piece of a sequence)
+    if (!(pflags & PIECE_LAST)) return;
     if (pool) {
         if (row >= 0 && row < p.state_slots) store_state(p.state_pool + row * p.state_ss + (int64_t)h * D * D, S, w, g, m);
     } else {
@@ -716,16 +794,87 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
     }
 }
 
-template <bool RG>
-hipError_t launch_chunk(const PfParams& p, int grid, hipStream_t s) {
+// Start states of the pieces of split sequences: S_start(0) = the sequence's initial state, S_start(p+1) =
+// P_p S_start(p) + S_loc(p), in fp32.  V-major storage makes each step the plain product S_vm[v][:] . P^T[:][k]
+// (P^T as stored by the transition pass).  One workgroup of 256 threads per (sequence, head); thread (v, half)
+// computes 64 outputs of row v.
+constexpr int SC_THREADS = 256;
+constexpr int SC_RS = 129;  // padded rows of the state copy (row v read along k by 64 different rows at once)
+__global__ void __launch_bounds__(SC_THREADS) scan_kernel(PfParams p, const int32_t* __restrict__ tab) {
+    extern __shared__ __align__(16) unsigned char lds[];
+    float* sS = reinterpret_cast<float*>(lds);                          // [128][129]
+    float* sP = reinterpret_cast<float*>(lds + 128 * SC_RS * 4 + 16);   // [128][128] P^T
+    const int H = p.H;
+    const int si = blockIdx.x / H;
+    const int h = blockIdx.x - si * H;
+    const int32_t* e = tab + tab[H_OFF_SCAN] + S_WORDS * si;
+    const int n = e[S_SEQ], np = e[S_NP], slot0 = e[S_SLOT0];
+    const int64_t ws_arr = (int64_t)tab[H_NSLOTS] * H * D * D;
+    const int t = threadIdx.x, v = t & 127, kh = t >> 7;
+    // the sequence's initial state (same rules as the chunk walk)
+    const float* src = nullptr;
+    if (p.flags & KDA355_PF_POOL) {
+        const int64_t row = p.state_idx[n];
+        if (row >= 0 && row < p.state_slots && p.has_init[n]) src = p.state_pool + row * p.state_ss + (int64_t)h * D * D;
+    } else if (p.init_state) {
+        src = p.init_state + ((int64_t)n * H + h) * D * D;
+    }
+    for (int i = t; i < D * D; i += SC_THREADS) sS[(i >> 7) * SC_RS + (i & 127)] = src ? src[i] : 0.f;
+    for (int pc = 0; pc + 1 < np; ++pc) {
+        const float* P = p.ws + ws_arr + ((int64_t)(slot0 + pc) * H + h) * D * D;
+        const float* L = p.ws + ((int64_t)(slot0 + pc) * H + h) * D * D;
+        for (int i = t; i < D * D / 4; i += SC_THREADS)
+            reinterpret_cast<f32x4*>(sP)[i] = reinterpret_cast<const f32x4*>(P)[i];
+        __syncthreads();
+        float acc[64];
+#pragma unroll
+        for (int j = 0; j < 64; ++j) acc[j] = L[v * D + 64 * kh + j];
+        for (int kk = 0; kk < D; ++kk) {
+            const float sv = sS[v * SC_RS + kk];
+            const f32x4* pr = reinterpret_cast<const f32x4*>(sP + kk * D + 64 * kh);
+#pragma unroll
+            for (int j4 = 0; j4 < 16; ++j4) {
+                const f32x4 pv = pr[j4];
+                acc[4 * j4] += sv * pv[0];
+                acc[4 * j4 + 1] += sv * pv[1];
+                acc[4 * j4 + 2] += sv * pv[2];
+                acc[4 * j4 + 3] += sv * pv[3];
+            }
+        }
+        __syncthreads();  // every thread has read sS and sP
+        float* dst = p.ws + 2 * ws_arr + ((int64_t)(slot0 + pc + 1) * H + h) * D * D;
+#pragma unroll
+        for (int j = 0; j < 64; ++j) {
+            sS[v * SC_RS + 64 * kh + j] = acc[j];
+            dst[v * D + 64 * kh + j] = acc[j];
+        }
+        __syncthreads();
+    }
+}
+
+template <bool RG, bool P1>
+hipError_t launch_chunk(const PfParams& p, int list_off, int entries, hipStream_t s) {
     static bool attr_set = false;  // idempotent; a race only repeats the call
     if (!attr_set) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&chunk_kernel<RG>),
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&chunk_kernel<RG, P1>),
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, LDS_TOTAL);
         if (e != hipSuccess) return e;
         attr_set = true;
     }
-    hipLaunchKernelGGL((chunk_kernel<RG>), dim3(grid), dim3(PF_THREADS), LDS_TOTAL, s, p, p.tab, p.ck_idx);
+    hipLaunchKernelGGL((chunk_kernel<RG, P1>), dim3(entries * p.H), dim3(PF_THREADS), LDS_TOTAL, s, p, p.tab, p.ck_idx,
+                       list_off);
+    return hipGetLastError();
+}
+hipError_t launch_scan(const PfParams& p, int entries, hipStream_t s) {
+    const int smem = 128 * SC_RS * 4 + 16 + D * D * 4;
+    static bool attr_set = false;
+    if (!attr_set) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&scan_kernel),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+        if (e != hipSuccess) return e;
+        attr_set = true;
+    }
+    hipLaunchKernelGGL(scan_kernel, dim3(entries * p.H), dim3(SC_THREADS), smem, s, p, p.tab);
     return hipGetLastError();
 }
 
@@ -749,29 +898,67 @@ extern "C" int kda355_prefill_plan(const KdaPrefillPlanIn* in, KdaPrefillPlan* p
     KDA_CHECK_ARG(T < (1ll << 31) - 64, "prefill_plan: too many tokens");
     KDA_CHECK_ARG(in->ck_every >= 0 && in->ck_every % KDA355_CHUNK == 0, "prefill_plan: ck_every must be a multiple of 64");
     const int every_chunks = in->ck_every / KDA355_CHUNK;
+    std::vector<int> nch(N);
     int64_t nchunks = 0;
-    for (int n = 0; n < N; ++n) nchunks += (cu[n + 1] - cu[n] + 63) / 64;
-    const int64_t words = H_WORDS + (int64_t)C_WORDS * N;
+    for (int n = 0; n < N; ++n) {
+        nch[n] = (int)((cu[n + 1] - cu[n] + 63) / 64);
+        nchunks += nch[n];
+    }
+    // Pieces: when the (sequence, head) chains alone would leave CUs idle, long sequences are cut into pieces of about
+    // the chunk count a CU would get at perfect balance (at least MIN_PIECE chunks each).  Split sequences run a
+    // transition pass and a scan before the final pass.
+    constexpr int MIN_PIECE = 16;
+    const int num_cus = in->num_cus > 0 ? in->num_cus : 256;
+    std::vector<int> npieces(N, 1);
+    if ((int64_t)N * in->H < num_cus && nchunks > 0) {
+        const int64_t target = std::max<int64_t>(MIN_PIECE, (nchunks * in->H + num_cus - 1) / num_cus);
+        for (int n = 0; n < N; ++n) {
+            const int most = nch[n] / MIN_PIECE;
+            const int np = (int)std::min<int64_t>(most, (nch[n] + target / 2) / target);
+            npieces[n] = std::max(1, np);
+        }
+    }
+    struct Piece { int n, first, count, slot; };
+    std::vector<Piece> pieces;
+    int nslots = 0, nsplit = 0, ntrans = 0;
+    for (int n = 0; n < N; ++n) {
+        const int np = npieces[n];
+        int f = 0;
+        for (int pc = 0; pc < np; ++pc) {
+            const int c = nch[n] / np + (pc < nch[n] % np ? 1 : 0);
+            pieces.push_back({n, f, c, np > 1 ? nslots + pc : 0});
+            f += c;
+        }
+        if (np > 1) {
+            nslots += np;
+            ++nsplit;
+            ntrans += np;
+        }
+    }
+    const int nfinal = (int)pieces.size();
+    const int64_t off_final = H_WORDS, off_trans = off_final + (int64_t)C_WORDS * nfinal;
+    const int64_t off_scan = off_trans + (int64_t)C_WORDS * ntrans;
+    const int64_t words = off_scan + (int64_t)S_WORDS * nsplit;
     plan->T = T;
     plan->N = N;
     plan->H = in->H;
     plan->num_chunks = (int32_t)nchunks;
-    plan->num_chains = N;
+    plan->num_chains = nfinal;
     int maxc = 0;
     int64_t ckrows = 0;
     for (int n = 0; n < N; ++n) {
-        const int c = (int)((cu[n + 1] - cu[n] + 63) / 64);
-        maxc = std::max(maxc, c);
-        if (every_chunks) ckrows += (c + every_chunks - 1) / every_chunks;
+        maxc = std::max(maxc, nch[n]);
+        if (every_chunks) ckrows += (nch[n] + every_chunks - 1) / every_chunks;
     }
     plan->max_chain_chunks = maxc;
     plan->table_words = words;
-    plan->workspace_bytes = 0;  // the fused kernel keeps every per-chunk operand on chip
+    plan->workspace_bytes = (int64_t)3 * nslots * in->H * KDA355_HEAD_DIM * KDA355_HEAD_DIM * 4;
     plan->ck_rows = ckrows;
     plan->magic = PLAN_MAGIC;
     plan->flags = in->flags;
     plan->ck_every = in->ck_every;
-    plan->reserved = 0;
+    plan->num_pieces = ntrans;
+    plan->num_split = nsplit;
     if (!tables) return 0;
     KDA_CHECK_ARG(capacity >= words, "prefill_plan: table capacity %lld < %lld words", (long long)capacity, (long long)words);
     int32_t* t = tables;
@@ -781,9 +968,14 @@ extern "C" int kda355_prefill_plan(const KdaPrefillPlanIn* in, KdaPrefillPlan* p
     t[H_T] = (int32_t)T;
     t[H_NCHUNK] = (int32_t)nchunks;
     t[H_EVERY] = every_chunks;
-    t[H_OFF_CHAIN] = H_WORDS;
-    t[H_NCHAIN] = N;
     t[H_CKROWS] = (int32_t)ckrows;
+    t[H_OFF_FINAL] = (int32_t)off_final;
+    t[H_NFINAL] = nfinal;
+    t[H_OFF_TRANS] = (int32_t)off_trans;
+    t[H_NTRANS] = ntrans;
+    t[H_OFF_SCAN] = (int32_t)off_scan;
+    t[H_NSCAN] = nsplit;
+    t[H_NSLOTS] = nslots;
     std::vector<int> ck_chunk(N, 0), ck_row0(N, 0);
     int64_t ckstart = 0;
     for (int n = 0; n < N; ++n) {
@@ -794,24 +986,41 @@ extern "C" int kda355_prefill_plan(const KdaPrefillPlanIn* in, KdaPrefillPlan* p
             if (o > 0 && o % 64 == 0 && o <= cu[n + 1] - cu[n]) ck_chunk[n] = o / 64;
         }
         ck_row0[n] = (int)ckstart;
-        if (every_chunks) {
-            const int cn = (int)((cu[n + 1] - cu[n] + 63) / 64);
-            ckstart += (cn + every_chunks - 1) / every_chunks;
-        }
+        if (every_chunks) ckstart += (nch[n] + every_chunks - 1) / every_chunks;
     }
-    // chains longest first (the longest critical paths start earliest when the grid runs in several waves)
-    std::vector<int> order(N);
+    auto fill = [&](int32_t* e, const Piece& pc, int flags) {
+        const int64_t len = cu[pc.n + 1] - cu[pc.n];
+        e[C_SEQ] = pc.n;
+        e[C_NCH] = pc.count;
+        e[C_TSTART] = (int32_t)(cu[pc.n] + 64 * (int64_t)pc.first);
+        e[C_LEN] = (int32_t)std::max<int64_t>(0, std::min<int64_t>(64 * (int64_t)pc.count, len - 64 * (int64_t)pc.first));
+        e[C_CKSINGLE] = ck_chunk[pc.n];
+        e[C_CKROW0] = ck_row0[pc.n];
+        e[C_FIRST] = pc.first;
+        e[C_FLAGS] = flags;
+        e[C_SLOT] = pc.slot;
+        e[C_SEQCH] = nch[pc.n];
+    };
+    // final pass: longest pieces first (they start earliest when the grid runs in several waves)
+    std::vector<int> order(nfinal);
     std::iota(order.begin(), order.end(), 0);
-    std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return cu[a + 1] - cu[a] > cu[b + 1] - cu[b]; });
-    for (int i = 0; i < N; ++i) {
-        const int n = order[i];
-        int32_t* e = t + H_WORDS + (int64_t)C_WORDS * i;
-        e[C_SEQ] = n;
-        e[C_NCH] = (int)((cu[n + 1] - cu[n] + 63) / 64);
-        e[C_TSTART] = (int32_t)cu[n];
-        e[C_LEN] = (int32_t)(cu[n + 1] - cu[n]);
-        e[C_CKSINGLE] = ck_chunk[n];
-        e[C_CKROW0] = ck_row0[n];
+    std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return pieces[a].count > pieces[b].count; });
+    for (int i = 0; i < nfinal; ++i) {
+        const Piece& pc = pieces[order[i]];
+        const bool last = pc.first + pc.count == nch[pc.n];
+        fill(t + off_final + (int64_t)C_WORDS * i, pc, (pc.first > 0 ? PIECE_READ_WS : 0) | (last ? PIECE_LAST : 0));
+    }
+    int ti = 0, si = 0;
+    for (int i = 0; i < nfinal; ++i) {
+        const Piece& pc = pieces[i];
+        if (npieces[pc.n] == 1) continue;
+        fill(t + off_trans + (int64_t)C_WORDS * ti++, pc, 0);
+        if (pc.first == 0) {
+            int32_t* e = t + off_scan + (int64_t)S_WORDS * si++;
+            e[S_SEQ] = pc.n;
+            e[S_NP] = npieces[pc.n];
+            e[S_SLOT0] = pc.slot;
+        }
     }
     return 0;
 }
@@ -849,6 +1058,9 @@ extern "C" int kda355_prefill_launch(const KdaPrefillArgs* a, kda355_stream_t st
     KDA_CHECK_ARG(pool || (aligned(a->final_state, 16) && (!a->initial_state || aligned(a->initial_state, 16))),
                   "prefill: states misaligned");
     KDA_CHECK_ARG(!a->ck_pool || (aligned(a->ck_pool, 16) && a->ck_slot_stride % 8 == 0), "prefill: ck pool misaligned");
+    KDA_CHECK_ARG(pl->workspace_bytes == 0 || (a->workspace && aligned(a->workspace, 256)),
+                  "prefill: this layout splits sequences and needs a 256-byte aligned workspace of %lld bytes",
+                  (long long)pl->workspace_bytes);
     if (a->N == 0) return 0;
     PfParams p;
     p.q = static_cast<const uint16_t*>(a->q);
@@ -881,9 +1093,17 @@ extern "C" int kda355_prefill_launch(const KdaPrefillArgs* a, kda355_stream_t st
     p.lb = a->lower_bound;
     p.flags = f;
     p.ck_bf16 = a->ck_dtype == 1;
+    p.ws = static_cast<float*>(a->workspace);
     const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    const hipError_t e = (f & KDA355_PF_RAW_GATE) ? launch_chunk<true>(p, pl->num_chains * p.H, s)
-                                                  : launch_chunk<false>(p, pl->num_chains * p.H, s);
+    const bool rg = (f & KDA355_PF_RAW_GATE) != 0;
+    const int off_final = H_WORDS, off_trans = off_final + C_WORDS * pl->num_chains;
+    hipError_t e = hipSuccess;
+    if (pl->num_pieces > 0) {  // split sequences: local runs with transitions, then the start states of their pieces
+        e = rg ? launch_chunk<true, true>(p, off_trans, pl->num_pieces, s) : launch_chunk<false, true>(p, off_trans, pl->num_pieces, s);
+        if (e == hipSuccess) e = launch_scan(p, pl->num_split, s);
+    }
+    if (e == hipSuccess)
+        e = rg ? launch_chunk<true, false>(p, off_final, pl->num_chains, s) : launch_chunk<false, false>(p, off_final, pl->num_chains, s);
     if (e != hipSuccess) {
         set_error("prefill: launch failed: %s", hipGetErrorString(e));
         return KDA355_ELAUNCH;

@@ -65,9 +65,16 @@ class PrefillMeta:
     def ck_rows(self):
         return int(self.plan.ck_rows)
 
+    @property
+    def split(self):
+        """(pieces, split sequences): 0 pieces when no sequence is split."""
+        return int(self.plan.num_pieces), int(self.plan.num_split)
 
-def plan(cu_seqlens, num_heads, checkpoint_offsets=None, ck_every=0, device=None):
-    """Host-only schedule from the layout (never the data); one H2D copy of the table when device is a GPU."""
+
+def plan(cu_seqlens, num_heads, checkpoint_offsets=None, ck_every=0, device=None, num_cus=None):
+    """Host-only schedule from the layout (never the data); one H2D copy of the table when device is a GPU.
+    num_cus: CUs to fill (default: the device's); when the (sequence, head) chains alone leave CUs idle, long sequences
+    are split into pieces (a transition pass and a scan run before the final pass, with a workspace)."""
     cu = np.ascontiguousarray(torch.as_tensor(cu_seqlens).detach().cpu().numpy(), dtype=np.int64)
     N = cu.size - 1
     if N < 1:
@@ -81,6 +88,9 @@ def plan(cu_seqlens, num_heads, checkpoint_offsets=None, ck_every=0, device=None
     pin.cu_seqlens = ctypes.c_void_p(cu.ctypes.data)
     pin.ck_offsets = ctypes.c_void_p(ck.ctypes.data) if ck is not None else None
     pin.N, pin.H, pin.ck_every = N, int(num_heads), int(ck_every)
+    if num_cus is None and device is not None and torch.device(device).type == "cuda":
+        num_cus = torch.cuda.get_device_properties(torch.device(device)).multi_processor_count
+    pin.num_cus = int(num_cus or 0)
     pl = _lib.KdaPrefillPlan()
     L = _lib.lib()
     _lib.check(L.kda355_prefill_plan(ctypes.byref(pin), ctypes.byref(pl), None, 0), "prefill_plan")

@@ -126,7 +126,8 @@ typedef struct KdaPrefillPlanIn {
     const int32_t* ck_offsets;  /* host [N] single-checkpoint offsets (tokens) or NULL */
     int32_t N, H;
     int32_t ck_every;           /* every-n interval in tokens (multiple of 64) or 0 */
-    int32_t num_cus;            /* 0: default */
+    int32_t num_cus;            /* CUs of the device (0: 256); sequences are split into pieces when the (sequence, head)
+                                   chains alone would leave CUs idle */
     uint32_t flags;
     int32_t reserved;
 } KdaPrefillPlanIn;
@@ -139,7 +140,8 @@ typedef struct KdaPrefillPlan {
     int64_t workspace_bytes;    /* device workspace the launch needs (256-byte aligned) */
     int64_t ck_rows;            /* every-n rows the layout writes (sum over n of ceil(len_n / ck_every)) */
     uint32_t magic, flags;
-    int32_t reserved, reserved2;
+    int32_t num_pieces;         /* pieces of split sequences (0: no sequence is split) */
+    int32_t num_split;          /* split sequences */
 } KdaPrefillPlan;
 
 /*

@@ -66,6 +66,7 @@ def test_prefill_plan_host_only():
     pin = _lib.KdaPrefillPlanIn()
     pin.cu_seqlens = ctypes.c_void_p(cu.ctypes.data)
     pin.N, pin.H, pin.ck_every = 4, 8, 128
+    pin.num_cus = 16                                     # 32 chains fill 16 CUs: no sequence is split
     pl = _lib.KdaPrefillPlan()
     assert L.kda355_prefill_plan(ctypes.byref(pin), ctypes.byref(pl), None, 0) == 0
     assert pl.num_chunks == 2 + 0 + 4 + 64 and pl.T == 4396 and pl.ck_rows == 1 + 0 + 2 + 32
@@ -79,3 +80,34 @@ def test_prefill_plan_host_only():
     assert b"non-decreasing" in L.kda355_last_error()
     pin.cu_seqlens, pin.N, pin.ck_every = ctypes.c_void_p(cu.ctypes.data), 4, 100
     assert L.kda355_prefill_plan(ctypes.byref(pin), ctypes.byref(pl), None, 0) == _lib.EINVAL
+
+
+def test_prefill_plan_splits_long_sequences():
+    """With idle CUs, long sequences are cut into pieces of >= 16 chunks; short ones and full chips are not split."""
+    import numpy as np
+    from kda355 import _lib
+    L = _lib.lib()
+
+    def plan(lens, H, cus):
+        cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+        pin = _lib.KdaPrefillPlanIn()
+        pin.cu_seqlens = ctypes.c_void_p(cu.ctypes.data)
+        pin.N, pin.H, pin.num_cus = len(lens), H, cus
+        pl = _lib.KdaPrefillPlan()
+        assert L.kda355_prefill_plan(ctypes.byref(pin), ctypes.byref(pl), None, 0) == 0
+        tab = np.zeros(pl.table_words, np.int32)
+        assert L.kda355_prefill_plan(ctypes.byref(pin), ctypes.byref(pl), ctypes.c_void_p(tab.ctypes.data), tab.size) == 0
+        return pl, tab
+
+    pl, tab = plan([131072], 32, 256)                    # configuration 2: 2048 chunks x 32 heads on 256 CUs
+    assert (pl.num_pieces, pl.num_split, pl.num_chains) == (8, 1, 8)
+    assert pl.workspace_bytes == 3 * 8 * 32 * 128 * 128 * 4
+    final = tab[16:16 + 12 * 8].reshape(8, 12)
+    assert sorted(final[:, 6]) == list(range(0, 2048, 256)) and set(final[:, 1]) == {256}   # first chunk, count
+    assert final[:, 7].tolist().count(2) + final[:, 7].tolist().count(3) == 1                # one last piece
+    pl, _ = plan([4011, 4318, 6249, 7799, 532, 1400, 6787, 7785], 32, 256)   # configuration 1 fills the chip
+    assert pl.num_pieces == 0 and pl.workspace_bytes == 0
+    pl, _ = plan([1000, 900], 2, 256)                    # 16 chunks: too short to split
+    assert pl.num_pieces == 0
+    pl, _ = plan([2048, 500], 2, 256)                    # 32 chunks -> 2 pieces of 16
+    assert (pl.num_pieces, pl.num_split) == (2, 1)

@@ -337,3 +337,89 @@ def test_prefill_errors():
         kda.chunk_kda(q[:, :5], q[:, :5], q[:, :5], g[:, :5], b[:, :5], meta=meta)
     with pytest.raises(TypeError):
         kda.chunk_kda(q.cpu(), q.cpu(), q.cpu(), g.cpu(), b.cpu())
+
+
+# ------------------------------------------------------------------------------------------------ long-sequence split
+def test_split_long_sequence_plain(oracle):
+    """A sequence long enough to leave CUs idle is cut into pieces (transition pass, scan, final pass); the short one
+    stays whole.  Output and final states against the fp64 oracle; the split is visible in the plan."""
+    kda = _kda()
+    H, lens = 2, [8192, 300]
+    meta = kda.plan(torch.tensor(_cu(lens)), H, device=DEV)
+    assert meta.split[0] >= 4, f"expected a split layout, got {meta.split}"
+    _say(f"split plain H={H} lens={lens} pieces={meta.split}")
+    g = gen(70)
+    T = sum(lens)
+    q, k, v, gg, beta = config_inputs(T, H, g)
+    h0 = torch.randn(len(lens), H, D, D, generator=g) * 0.02
+    o, fin = kda.chunk_kda(q[None].to(DEV), k[None].to(DEV), v[None].to(DEV), gg[None].to(DEV), beta[None].to(DEV),
+                           initial_state=h0.to(DEV), meta=meta)
+    torch.cuda.synchronize()
+    ro, rf = oracle.prefill_plain(f32(q), f32(k), f32(v), f32(gg), f32(beta), _cu(lens), initial_state=f32(h0),
+                                  precision=64)
+    _check_out(o[0], ro, "split plain")
+    for n in range(len(lens)):
+        assert rel_frob(f32(fin[n]), rf[n]) <= STATE_TOL, f"split plain seq {n}"
+
+
+def test_split_matches_whole_walk():
+    """The same call planned for a full chip (no split) and for 256 CUs (split) agrees to fp32/fp16 rounding."""
+    kda = _kda()
+    H, lens = 4, [4096, 1100]
+    g = gen(71)
+    T = sum(lens)
+    q, k, v, gg, beta = (x[None].to(DEV) for x in config_inputs(T, H, g))
+    h0 = (torch.randn(len(lens), H, D, D, generator=g) * 0.02).to(DEV)
+    cu = torch.tensor(_cu(lens))
+    whole = kda.plan(cu, H, device=DEV, num_cus=1)
+    split = kda.plan(cu, H, device=DEV, num_cus=256)
+    assert whole.split[0] == 0 and split.split[0] >= 2
+    _say(f"split vs whole pieces={split.split}")
+    o1, f1 = kda.chunk_kda(q, k, v, gg, beta, initial_state=h0, meta=whole)
+    o2, f2 = kda.chunk_kda(q, k, v, gg, beta, initial_state=h0, meta=split)
+    torch.cuda.synchronize()
+    ex, raw, rel = out_err(f32(o2), f32(o1))
+    assert ex <= OUT_TOL, f"split vs whole output excess {ex:.3e}"
+    assert rel_frob(f32(f2), f32(f1)) <= STATE_TOL
+
+
+@pytest.mark.parametrize("ckdt", [torch.float32, torch.bfloat16])
+def test_split_pool_every_n_checkpoints(oracle, ckdt):
+    """Split sequence with the B200 every-n rows into an explicit row table (configuration 2's form) on a paged pool:
+    rows that fall in later pieces are written by the final pass from the composed start states."""
+    kda = _kda()
+    H, lens, every = 4, [4096], 256
+    g = gen(72)
+    T = sum(lens)
+    q, k, v, gg, beta = config_inputs(T, H, g)
+    P = 6
+    pool0 = torch.randn(P, H, D, D, generator=g) * 0.05
+    slot = torch.tensor([3], dtype=torch.int32)
+    nck = T // every
+    rows = torch.randperm(nck + 4, generator=g)[:nck].to(torch.int32)
+    ck = torch.full((nck + 4, H, D, D), float("nan"), dtype=ckdt, device=DEV)
+    pool = pool0.clone().to(DEV)
+    meta = kda.plan(torch.tensor(_cu(lens)), H, ck_every=every, device=DEV)
+    assert meta.split[0] >= 2
+    _say(f"split pool every-n dtype={ckdt} pieces={meta.split}")
+    o, fin, ckr = kda.chunk_kda(q[None].to(DEV), k[None].to(DEV), v[None].to(DEV), gg[None].to(DEV), beta[None].to(DEV),
+                                initial_state=pool, meta=meta, ssm_state_indices=slot.to(DEV), state_checkpoints=ck,
+                                checkpoint_every_n_tokens=every, checkpoint_state_indices=rows.to(DEV))
+    torch.cuda.synchronize()
+    ro, rf, rrows, _ = oracle.checkpoints_every_n(f32(q), f32(k), f32(v), f32(gg), f32(beta), _cu(lens), every,
+                                                 initial_state=f32(pool0)[slot.numpy()], precision=64)
+    _check_out(o[0], ro, "split every-n")
+    assert rel_frob(f32(pool[3]), rf[0]) <= STATE_TOL
+    untouched = [i for i in range(P) if i != 3]
+    assert torch.equal(pool[untouched].cpu(), pool0[untouched]), "other pool slots changed"
+    got = f32(ck)
+    written = set(rows.tolist())
+    for j in range(nck):
+        ref = rrows[j]
+        if ckdt == torch.bfloat16:
+            assert rel_frob(got[rows[j]], ref) <= rel_frob(oracle.bf16_round(ref), ref) + STATE_TOL, f"row {j}"
+        else:
+            assert rel_frob(got[rows[j]], ref) <= STATE_TOL, f"row {j}"
+    for i in range(nck + 4):
+        if i not in written:
+            assert np.isnan(got[i]).all(), f"checkpoint row {i} should be untouched"
