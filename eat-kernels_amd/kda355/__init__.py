@@ -3,6 +3,7 @@
     from kda355 import chunk_kda, kda_prefill                      # plain prefill calls (fla / reference forms)
     from kda355 import prefill_prepare, prefill                    # vLLM-ROCm Kimi serving prefill (paged pool)
     from kda355 import fused_recurrent_kda, spec_commit           # decode / speculative verify on a state pool
+    from kda355 import decode                                      # vLLM-ROCm fused decode (conv + KDA + gated norm)
 
 Every entry point runs the hand-written HIP kernels of libkda355.so (include/kda355.h).  There is no CPU or PyTorch
 fallback: calling on CPU tensors raises TypeError, and a missing library raises RuntimeError.
@@ -10,6 +11,7 @@ fallback: calling on CPU tensors raises TypeError, and a missing library raises 
 from ._lib import LIB_PATH, lib  # noqa: F401
 from .prefill import chunk_kda, kda_prefill, plan, prefill, prefill_prepare  # noqa: F401
 from .recurrent import fused_recurrent_kda, spec_commit  # noqa: F401
+from .decode import decode  # noqa: F401
 
-__all__ = ["chunk_kda", "kda_prefill", "plan", "prefill", "prefill_prepare", "fused_recurrent_kda", "spec_commit",
+__all__ = ["chunk_kda", "kda_prefill", "plan", "prefill", "prefill_prepare", "fused_recurrent_kda", "spec_commit", "decode",
            "lib", "LIB_PATH"]

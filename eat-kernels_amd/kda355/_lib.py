@@ -45,6 +45,20 @@ class KdaSpecCommitArgs(ctypes.Structure):
     ]
 
 
+class KdaDecodeArgs(ctypes.Structure):
+    _fields_ = [
+        ("mixed_qkv", P), ("conv_state", P), ("conv_weight", P), ("gate", P), ("beta", P), ("out_gate", P),
+        ("A_log", P), ("dt_bias", P), ("norm_weight", P), ("ssm_state", P), ("state_indices", P),
+        ("num_accepted", P), ("out", P),
+        ("mixed_row_stride", I64), ("gate_row_stride", I64), ("beta_row_stride", I64), ("out_gate_row_stride", I64),
+        ("out_row_stride", I64),
+        ("conv_slot_stride", I64), ("conv_tap_stride", I64), ("conv_slots", I64), ("ssm_slot_stride", I64),
+        ("ssm_slots", I64),
+        ("B", I32), ("S", I32), ("H", I32), ("conv_taps", I32),
+        ("norm_eps", F32), ("lower_bound", F32), ("flags", U32), ("reserved", I32),
+    ]
+
+
 class KdaPrefillPlanIn(ctypes.Structure):
     _fields_ = [
         ("cu_seqlens", P), ("ck_offsets", P), ("N", I32), ("H", I32), ("ck_every", I32), ("num_cus", I32),
@@ -91,6 +105,8 @@ def lib():
         L.kda355_recurrent_launch.restype = ctypes.c_int
         L.kda355_spec_commit_launch.argtypes = [ctypes.POINTER(KdaSpecCommitArgs), P]
         L.kda355_spec_commit_launch.restype = ctypes.c_int
+        L.kda355_decode_launch.argtypes = [ctypes.POINTER(KdaDecodeArgs), P]
+        L.kda355_decode_launch.restype = ctypes.c_int
         L.kda355_prefill_plan.argtypes = [ctypes.POINTER(KdaPrefillPlanIn), ctypes.POINTER(KdaPrefillPlan), P, I64]
         L.kda355_prefill_plan.restype = ctypes.c_int
         L.kda355_prefill_workspace_bytes.argtypes = [ctypes.POINTER(KdaPrefillPlan)]
@@ -114,5 +130,5 @@ def check(rc: int, what: str):
 
 def exported_symbols():
     """Names declared in include/kda355.h that the library must export."""
-    return ["kda355_recurrent_launch", "kda355_spec_commit_launch", "kda355_prefill_plan",
+    return ["kda355_recurrent_launch", "kda355_spec_commit_launch", "kda355_decode_launch", "kda355_prefill_plan",
             "kda355_prefill_workspace_bytes", "kda355_prefill_launch", "kda355_last_error", "kda355_version"]

@@ -1,0 +1,115 @@
+"""Fused KDA decode / speculative verify step of the vLLM-ROCm Kimi layer (host side of kda355_decode_launch).
+
+    decode(mixed_qkv, conv_state, conv_weight, gate, beta, out_gate, A_log, dt_bias, norm_weight, ssm_state,
+           state_indices, num_accepted_tokens, cu_seqlens, norm_eps, lower_bound, out)
+
+Same signature and argument meaning as the reference's `kernel.decode` (kda/mi350x/kda/kernel.py:212-216; semantics
+kda/mi350x/reference.py:104-181): one call runs the width-4 causal conv + SiLU with the rolling bf16 conv cache, the
+q/k norms, the gate and beta activations, the gated delta rule on the fp32 state pool and the gated RMSNorm, for
+B sequences of S tokens (T = B * S rows; S = 1 plain decode, S > 1 spec verify with num_accepted_tokens).  conv_state
+and ssm_state are updated in place and may be strided views into one paged byte pool (the slot stride is honoured,
+rows must be dense).  Slot rows <= 0 are padding (zero output rows, nothing written).  `out` is written and returned.
+
+Errors follow the reference validator (kda/mi350x/kda/decode/kernel_v13_a.py:697-735): TypeError for a wrong dtype or
+device, ValueError for a wrong shape or stride.  Nothing data dependent is checked on the host, so the call is
+capturable in a HIP graph.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+
+D = 128
+MAX_S = 16
+
+
+def _chk(name, t, dtype, shape, device, rows_only=False):
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"kda355 decode: {name} must be a tensor")
+    if t.dtype != dtype or t.device != device:
+        raise TypeError(f"kda355 decode: {name} must be {dtype} on {device}, got {t.dtype} on {t.device}")
+    if shape is not None and tuple(t.shape) != tuple(shape):
+        raise ValueError(f"kda355 decode: {name} must have shape {tuple(shape)}, got {tuple(t.shape)}")
+    dense = t[0].is_contiguous() if (rows_only and t.shape[0]) else t.is_contiguous()
+    if not dense:
+        raise ValueError(f"kda355 decode: {name} must be contiguous" + (" within a row / slot" if rows_only else ""))
+
+
+def _slot_stride(t, per_slot):
+    return t.stride(0) if t.shape[0] > 1 else per_slot
+
+
+def decode(mixed_qkv, conv_state, conv_weight, gate, beta, out_gate, A_log, dt_bias, norm_weight, ssm_state,
+           state_indices, num_accepted_tokens, cu_seqlens, norm_eps, lower_bound, out):
+    if not isinstance(mixed_qkv, torch.Tensor) or mixed_qkv.dim() != 2:
+        raise ValueError("kda355 decode: mixed_qkv must be [T, 3 * H * 128]")
+    dev = mixed_qkv.device
+    if dev.type != "cuda":
+        raise TypeError("kda355 decode: tensors must be on a GPU")
+    T, C = mixed_qkv.shape
+    if C % (3 * D):
+        raise ValueError(f"kda355 decode: mixed_qkv width {C} is not 3 * H * 128")
+    dim = C // 3
+    H = dim // D
+    B = cu_seqlens.numel() - 1
+    spec = num_accepted_tokens is not None
+    if B < 1 or T % B:
+        raise ValueError(f"kda355 decode: T = {T} is not B x S for B = {B}")
+    S = T // B
+    if S > MAX_S:
+        raise ValueError(f"kda355 decode: S = {S} tokens per sequence exceeds {MAX_S}")
+    if not spec and S != 1:
+        raise ValueError(f"kda355 decode: plain decode takes one token per sequence (S = {S}); pass "
+                         "num_accepted_tokens for a spec verify")
+    taps = (2 + S) if spec else 3
+    _chk("mixed_qkv", mixed_qkv, torch.bfloat16, (T, 3 * dim), dev, True)
+    if conv_state.dim() != 3 or conv_state.shape[1] < taps or conv_state.shape[2] != 3 * dim:
+        raise ValueError(f"kda355 decode: conv_state must be [slots, >= {taps}, {3 * dim}], got {tuple(conv_state.shape)}")
+    _chk("conv_state", conv_state, torch.bfloat16, None, dev, True)
+    _chk("conv_weight", conv_weight, torch.float32, (3, 4, dim), dev)
+    if not gate.is_contiguous():
+        gate = gate.contiguous()  # the reference's kernel.decode makes the same copy
+    _chk("gate", gate, torch.bfloat16, (T, H, D), dev)
+    _chk("beta", beta, torch.bfloat16, (T, H), dev, True)
+    _chk("out_gate", out_gate, torch.bfloat16, (T, dim), dev, True)
+    _chk("A_log", A_log, torch.float32, (H,), dev)
+    _chk("dt_bias", dt_bias, torch.float32, (dim,), dev)
+    _chk("norm_weight", norm_weight, torch.float32, (D,), dev)
+    if ssm_state.dim() != 4 or tuple(ssm_state.shape[1:]) != (H, D, D):
+        raise ValueError(f"kda355 decode: ssm_state must be [slots, {H}, 128, 128], got {tuple(ssm_state.shape)}")
+    _chk("ssm_state", ssm_state, torch.float32, None, dev, True)
+    _chk("out", out, torch.bfloat16, (T, dim), dev)
+    for name, t in (("state_indices", state_indices), ("num_accepted_tokens", num_accepted_tokens)):
+        if t is not None and t.device != dev:
+            raise TypeError(f"kda355 decode: {name} must be on {dev}, got {t.device}")
+    if state_indices.dtype != torch.int32 or tuple(state_indices.shape) != ((B, S) if spec else (B,)):
+        raise ValueError(f"kda355 decode: state_indices must be int32 {(B, S) if spec else (B,)}, "
+                         f"got {state_indices.dtype} {tuple(state_indices.shape)}")
+    if spec and (num_accepted_tokens.dtype != torch.int32 or tuple(num_accepted_tokens.shape) != (B,)):
+        raise ValueError(f"kda355 decode: num_accepted_tokens must be int32 ({B},), "
+                         f"got {num_accepted_tokens.dtype} {tuple(num_accepted_tokens.shape)}")
+    idx = state_indices.contiguous()
+    acc = num_accepted_tokens.contiguous() if spec else None
+
+    a = _lib.KdaDecodeArgs()
+    a.mixed_qkv, a.conv_state, a.conv_weight = mixed_qkv.data_ptr(), conv_state.data_ptr(), conv_weight.data_ptr()
+    a.gate, a.beta, a.out_gate = gate.data_ptr(), beta.data_ptr(), out_gate.data_ptr()
+    a.A_log, a.dt_bias, a.norm_weight = A_log.data_ptr(), dt_bias.data_ptr(), norm_weight.data_ptr()
+    a.ssm_state, a.state_indices = ssm_state.data_ptr(), idx.data_ptr()
+    a.num_accepted = acc.data_ptr() if spec else None
+    a.out = out.data_ptr()
+    a.mixed_row_stride, a.gate_row_stride = mixed_qkv.stride(0), gate.stride(0)
+    a.beta_row_stride, a.out_gate_row_stride, a.out_row_stride = beta.stride(0), out_gate.stride(0), out.stride(0)
+    a.conv_slot_stride = _slot_stride(conv_state, conv_state.shape[1] * 3 * dim)
+    a.conv_tap_stride = conv_state.stride(1) if conv_state.shape[1] > 1 else 3 * dim
+    a.conv_slots, a.conv_taps = conv_state.shape[0], conv_state.shape[1]
+    a.ssm_slot_stride, a.ssm_slots = _slot_stride(ssm_state, H * D * D), ssm_state.shape[0]
+    a.B, a.S, a.H = B, S, H
+    a.norm_eps, a.lower_bound = float(norm_eps), float(lower_bound)
+    a.flags = 0
+    stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    _lib.check(_lib.lib().kda355_decode_launch(ctypes.byref(a), stream), "decode")
+    return out

@@ -17,6 +17,10 @@
  *                                 (kda/mi350x/benchmark/vllm_reference/kda.py:488-502, 560-575) and the recurrent
  *                                 core of the decode kernel's `run` binding (kda/mi350x/kda/decode/kda_v14_b.cu:
  *                                 3266-3312, slot rules `slots()` :1013-1042)
+ *   kda355_decode_launch          the fused decode / spec-verify step of the vLLM-ROCm Kimi layer, `decode(mixed_qkv,
+ *                                 conv_state, ...)` (kda/mi350x/kda/kernel.py:212-216; semantics
+ *                                 kda/mi350x/reference.py:104-181; input contract kda/mi350x/kda/decode/kernel_v13_a.py:
+ *                                 697-735; slot rules kda/mi350x/kda/decode/kda_v14_b.cu:1013-1042)
  *   kda355_spec_commit_launch     the commit of an accepted draft length (kda/mi350x/reference.py:117-121 reads the
  *                                 state after token a-1; this copies it to the sequence's pool slot)
  *   kda355_prefill_plan           kda_build_meta (kda/mi350x/kda/prefill/kernel.h:100-102) and prepare_prod
@@ -104,6 +108,50 @@ typedef struct KdaSpecCommitArgs {
 } KdaSpecCommitArgs;
 
 int kda355_spec_commit_launch(const KdaSpecCommitArgs* args, kda355_stream_t stream);
+
+/* ------------------------------------------------------------------------------------------------ fused decode */
+
+/*
+ * Fused decode / speculative verify of B sequences x S tokens (T = B*S rows, row n*S + t is token t of sequence n),
+ * H heads, dim = H * 128, per (n, h) and token t:
+ *     conv      x = SiLU(sum_j window[t + j] * conv_weight[:, j]) over the head's q | k | v channels, where window =
+ *               3 history taps of conv_state[cs] followed by the S rows of mixed_qkv (width-4 causal depthwise conv)
+ *     q, k      x * rsqrt(sum x^2 + 1e-6);  q *= 128^-1/2
+ *     gate      g = lower_bound * sigmoid(exp(A_log[h]) * (gate + dt_bias));  beta = sigmoid(beta)
+ *     rule      S *= exp(g) (key axis);  u = beta (v - S k);  S += u k^T;  o = S q
+ *     output    y = bf16(o) * rsqrt(mean(bf16(o)^2) + norm_eps) * norm_weight * sigmoid(out_gate)   (bf16)
+ * plain decode (num_accepted == NULL, state_indices [B]): rd = cs = state_indices[n]; the final state goes back to
+ *     ssm_state[rd]; conv_state[cs] taps [0, 3) <- the last 3 window rows (taps beyond 3 are untouched).
+ * spec verify (num_accepted [B], state_indices [B, S]): a = clamp(num_accepted[n], 1, S), rd = state_indices[n, a-1],
+ *     cs = state_indices[n, 0]; history taps [a-1, a+2); the state after token t goes to ssm_state[state_indices[n, t]]
+ *     (rows <= 0 skipped); conv_state[cs] taps [0, 2 + S) <- window rows [1, 3 + S).
+ * Rows <= 0 or outside the pool are padding: a sequence whose rd or cs is padding gets zero output rows and writes
+ * nothing.  The vLLM page layout (conv_state and ssm_state as strided views into one byte pool) is expressed by the
+ * slot strides.  S <= 16.
+ */
+typedef struct KdaDecodeArgs {
+    const void* mixed_qkv;      /* bf16 [T, 3 * dim], row stride mixed_row_stride elements (16-byte aligned rows) */
+    void* conv_state;           /* bf16 [conv_slots, conv_taps, 3 * dim]: slot / tap strides in elements */
+    const float* conv_weight;   /* [3, 4, dim] dense: (q | k | v, tap, channel) */
+    const void* gate;           /* bf16 [T, H, 128], row stride gate_row_stride elements */
+    const void* beta;           /* bf16 [T, H] logits, row stride beta_row_stride */
+    const void* out_gate;       /* bf16 [T, dim], row stride out_gate_row_stride */
+    const float* A_log;         /* [H] */
+    const float* dt_bias;       /* [dim] */
+    const float* norm_weight;   /* [128] */
+    float* ssm_state;           /* [ssm_slots, H, 128, 128] fp32 V-major, slot stride ssm_slot_stride floats */
+    const int32_t* state_indices;  /* [B] (plain) or [B, S] (spec), dense */
+    const int32_t* num_accepted;   /* [B] or NULL (plain decode) */
+    void* out;                  /* bf16 [T, dim], row stride out_row_stride */
+    int64_t mixed_row_stride, gate_row_stride, beta_row_stride, out_gate_row_stride, out_row_stride;
+    int64_t conv_slot_stride, conv_tap_stride, conv_slots, ssm_slot_stride, ssm_slots;
+    int32_t B, S, H, conv_taps;
+    float norm_eps, lower_bound;
+    uint32_t flags;             /* 0 */
+    int32_t reserved;
+} KdaDecodeArgs;
+
+int kda355_decode_launch(const KdaDecodeArgs* args, kda355_stream_t stream);
 
 /* ------------------------------------------------------------------------------------------------ prefill */
 

@@ -281,7 +281,9 @@ def decode_full(mixed_qkv, conv_state, conv_weight, gate_in, beta_in, out_gate, 
     mixed_qkv [T, 3*H*128] (bf16 values), conv_state [slots, taps, 3*H*128] (bf16 values), conv_weight
     [3, 4, H*128], gate_in [T, H, 128], beta_in [T, H], out_gate [T, H*128], A_log [H], dt_bias [H*128],
     norm_weight [128], ssm_state [slots, H, 128, 128].  Returns (out [T, H*128] bf16-rounded fp32, conv_new,
-    ssm_new).  Padding slots (<= 0) follow the same rule as recurrent()."""
+    ssm_new).  Rows <= 0 are padding: a sequence whose read row or conv row (idx[n, 0] in spec) is padding gets zero
+    output and writes nothing (the reference kernel's slot rule, kda/mi350x/kda/decode/kda_v14_b.cu:1013-1042);
+    spec writes skip padding rows (reference.py:168-171)."""
     W = 4
     T, C = mixed_qkv.shape
     dim = C // 3
@@ -318,7 +320,7 @@ def decode_full(mixed_qkv, conv_state, conv_weight, gate_in, beta_in, out_gate, 
     g = gate(_f32(gate_in).reshape(T, H, D), A_log, dt_bias, lower_bound)
     b = sigmoid(beta_in)
     S_in = np.zeros((B, H, D, D), np.float32)
-    live = read_slot > 0
+    live = (read_slot > 0) & (cslot > 0)                          # kda/mi350x/kda/decode/kda_v14_b.cu:1035
     for n in range(B):
         if live[n]:
             S_in[n] = ssm_state[read_slot[n]]
@@ -341,7 +343,8 @@ def decode_full(mixed_qkv, conv_state, conv_weight, gate_in, beta_in, out_gate, 
             conv_new[cslot[n], :W - 2 + S] = window[n, 1:]        # reference.py:176-177
         else:
             ssm_new[read_slot[n]] = steps[n, S - 1]
-            conv_new[cslot[n]] = window[n, -(W - 1):]             # reference.py:178-180
+            # reference.py:178-180 (taps [0, 3); more taps, which kernel_v13_a.py:711-712 accepts, stay as they are)
+            conv_new[cslot[n], :W - 1] = window[n, -(W - 1):]
     return out, conv_new, ssm_new
 
 

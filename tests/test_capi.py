@@ -37,6 +37,12 @@ def test_invalid_arguments_rejected_without_gpu():
     c = _lib.KdaSpecCommitArgs()
     c.B, c.S, c.H = 2, 2, 1
     assert L.kda355_spec_commit_launch(ctypes.byref(c), None) == _lib.EINVAL
+    d = _lib.KdaDecodeArgs()
+    d.B, d.S, d.H, d.conv_taps = 4, 1, 2, 3             # pointers left null
+    assert L.kda355_decode_launch(ctypes.byref(d), None) == _lib.EINVAL
+    assert b"null" in L.kda355_last_error()
+    d.S = 17                                            # beyond the 16-token verify window
+    assert L.kda355_decode_launch(ctypes.byref(d), None) == _lib.EINVAL
 
 
 def test_struct_layout_matches_header():
@@ -44,16 +50,16 @@ def test_struct_layout_matches_header():
     import subprocess
     import tempfile
     from kda355 import _lib
-    src = '#include "kda355.h"\n#include <stdio.h>\nint main(){printf("%zu %zu %zu %zu %zu\\n", ' \
+    src = '#include "kda355.h"\n#include <stdio.h>\nint main(){printf("%zu %zu %zu %zu %zu %zu\\n", ' \
           'sizeof(KdaRecurrentArgs), sizeof(KdaSpecCommitArgs), sizeof(KdaPrefillPlanIn), sizeof(KdaPrefillPlan), ' \
-          'sizeof(KdaPrefillArgs));return 0;}\n'
+          'sizeof(KdaPrefillArgs), sizeof(KdaDecodeArgs));return 0;}\n'
     with tempfile.TemporaryDirectory() as d:
         (Path(d) / "m.c").write_text(src)
         subprocess.run(["gcc", "-I", str(ROOT / "include"), str(Path(d) / "m.c"), "-o", str(Path(d) / "m")],
                        check=True)
         sizes = subprocess.run([str(Path(d) / "m")], capture_output=True, text=True, check=True).stdout.split()
     mirrors = [_lib.KdaRecurrentArgs, _lib.KdaSpecCommitArgs, _lib.KdaPrefillPlanIn, _lib.KdaPrefillPlan,
-               _lib.KdaPrefillArgs]
+               _lib.KdaPrefillArgs, _lib.KdaDecodeArgs]
     assert [int(x) for x in sizes] == [ctypes.sizeof(m) for m in mirrors]
 
 
@@ -111,3 +117,19 @@ def test_prefill_plan_splits_long_sequences():
     assert pl.num_pieces == 0
     pl, _ = plan([2048, 500], 2, 256)                    # 32 chunks -> 2 pieces of 16
     assert (pl.num_pieces, pl.num_split) == (2, 1)
+
+
+def test_decode_rejects_host_tensors():
+    """The fused decode wrapper raises TypeError for CPU tensors (the reference validator's device rule,
+    kda/mi350x/kda/decode/kernel_v13_a.py:705-707), before any device call."""
+    import pytest
+    import torch
+    import kda355
+    H, B = 1, 2
+    dim = H * 128
+    t = torch.zeros
+    with pytest.raises(TypeError):
+        kda355.decode(t(B, 3 * dim, dtype=torch.bfloat16), t(4, 3, 3 * dim, dtype=torch.bfloat16), t(3, 4, dim),
+                      t(B, H, 128, dtype=torch.bfloat16), t(B, H, dtype=torch.bfloat16), t(B, dim, dtype=torch.bfloat16),
+                      t(H), t(dim), t(128), t(4, H, 128, 128), t(B, dtype=torch.int32), None,
+                      torch.arange(B + 1, dtype=torch.int32), 1e-5, -5.0, t(B, dim, dtype=torch.bfloat16))

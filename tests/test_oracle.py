@@ -356,6 +356,48 @@ def test_decode_full_closed_forms(oracle):
         assert np.array_equal(cnew2[c, 2:4], x2[n * S:(n + 1) * S])
 
 
+def test_decode_full_conv_groups_taps_silu(oracle):
+    """Conv orientation pin (reference.py:144-157): conv_weight[group, tap, channel] with one-hot taps per group.
+    q and k select the same current input (so k_hat . q_hat = 1), v selects a history tap; beta = 1, no decay, zero
+    state: o = v / sqrt(128) and the gated RMSNorm output is SiLU(v_tap) / RMS(SiLU(v_tap)).  A transposed weight
+    layout, a reversed tap order, a wrong spec history offset or a missing SiLU all change which values come out."""
+    rng = np.random.default_rng(16)
+    H, slots = 1, 8
+    dim = H * D
+    C = 3 * dim
+    w = np.zeros((3, 4, dim), np.float32)
+    w[0, 3] = 1.0                                             # q: the current input
+    w[1, 3] = 1.0                                             # k: the current input
+    w[2, 1] = 1.0                                             # v: window row t + 1
+    nw = np.ones(D, np.float32)
+    A_log = np.zeros(H, np.float32)
+    dt = np.zeros(dim, np.float32)
+    ssm = np.zeros((slots, H, D, D), np.float32)
+
+    def expect(vt):
+        sv = vt * (1.0 / (1.0 + np.exp(-vt.astype(np.float64))))
+        return sv / np.sqrt((sv * sv).mean())
+
+    for spec, S, acc in ((False, 1, None), (True, 2, np.array([2, 1]))):
+        B = 2
+        T = B * S
+        taps = 2 + S if spec else 3
+        conv = oracle.bf16_round(rng.standard_normal((slots, taps, C)).astype(np.float32))
+        x = oracle.bf16_round(rng.standard_normal((T, C)).astype(np.float32))
+        x[:, dim:2 * dim] = x[:, :dim]
+        gate_in = np.full((T, H, D), -100.0, np.float32)      # sigmoid -> 0: g = 0
+        beta_in = np.full((T, H), 30.0, np.float32)           # sigmoid(30) = 1 in fp32
+        og = np.full((T, dim), 30.0, np.float32)
+        idx = np.array([[3, 4], [5, 6]]) if spec else np.array([3, 5])
+        out, _, _ = oracle.decode_full(x, conv, w, gate_in, beta_in, og, A_log, dt, nw, ssm, idx, acc, 1e-12, -5.0)
+        for n in range(B):
+            cs = idx[n, 0] if spec else idx[n]
+            start = acc[n] - 1 if spec else 0
+            vt = conv[cs, start + 1, 2 * dim:]                # window row 1 = history tap start + 1
+            got = out[n * S].astype(np.float64)
+            assert np.allclose(got, expect(vt), rtol=1.6e-2, atol=1e-2), (spec, n)
+
+
 def test_config0_shapes(oracle):
     """Config 0 (T = 1024, H = 4, zero initial state) runs and is finite; fp32 agrees with fp64."""
     q, k, v, gg, beta = config_inputs(1024, 4, gen(0))
