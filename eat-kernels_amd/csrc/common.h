@@ -46,6 +46,10 @@ __device__ __forceinline__ float sum16(float x) {
 
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + __expf(-x)); }
 
+// Workgroup barrier that orders LDS only: __syncthreads() also waits for every outstanding global load and store
+// (vmcnt(0)), which would stall on loads issued for later phases.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 // Thread-local error text for the C ABI.
 void set_error(const char* fmt, ...);
 

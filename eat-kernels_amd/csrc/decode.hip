@@ -1,26 +1,27 @@
 // Fused KDA decode / speculative verify on gfx950 (the vLLM-ROCm Kimi decode contract, kda/mi350x/kda/kernel.py:
 // 212-216; semantics kda/mi350x/reference.py:104-181).
 //
-// One workgroup of 256 threads (4 wave64) per (sequence n, head h).  Per call:
+// One workgroup of 512 threads (8 wave64) per (sequence n, head h).  Per call:
 //   * the head's 3 x 128 conv channels (q | k | v) of the window = 3 history taps of the bf16 conv cache followed by
 //     the S input rows go to LDS with the conv weights; the width-4 causal conv + SiLU of all S tokens is computed up
 //     front (it does not depend on the state), and the conv cache is committed: plain keeps the last 3 inputs, spec
 //     keeps window[1:] (2 + S taps);
-//   * the fp32 state (read row: idx[n] plain, idx[n, a-1] spec) is held in registers with the layout of the recurrent
-//     kernel (lane: rows 16p + 4w + l/16, columns 4(l%16)..+3 and 64 + 4(l%16)..+3);
+//   * the fp32 state (read row: idx[n] plain, idx[n, a-1] spec) is held in registers with the walker layout of
+//     walk.h (lane: rows 16p + 2w + (l/32)%2, columns 4(l%32)..+3), streamed in and out with its cache policy;
 //   * per token: q, k <- x * rsqrt(sum x^2 + 1e-6) (q also * 128^-1/2, applied as the output scale), the gate
 //     g = lb * sigmoid(exp(A_log[h]) * (gate + dt_bias)), beta = sigmoid(beta), the delta rule, then the gated RMSNorm
 //     y = bf16(o) * rsqrt(mean(bf16(o)^2) + eps) * norm_weight * sigmoid(out_gate) on the 128 outputs of the head
-//     (a cross-wave sum through LDS, double buffered per token); spec writes the state after token t to idx[n, t] > 0,
-//     plain writes the final state back to idx[n].
+//     (bf16 outputs and per-half-wave sums of squares of every token kept in LDS, finished by all threads after the
+//     walk behind one barrier); spec writes the state after token t to idx[n, t] > 0, plain writes the final state
+//     back to idx[n].
 // Slot rows <= 0 (and rows outside the pool) are padding (kda/mi350x/kda/decode/kda_v14_b.cu:1013-1042): a sequence
 // whose read row or conv row is padding gets zero output rows and writes nothing; spec writes skip padding rows.
-#include "common.h"
+#include "walk.h"
 
 namespace kda355 {
 namespace {
 
-constexpr int DC_THREADS = 256;
+constexpr int DC_THREADS = WK_THREADS;
 constexpr int DC_MAX_S = 16;
 constexpr int DC_CH = 3 * D;  // conv channels of one head: q | k | v
 
@@ -46,21 +47,25 @@ struct DecParams {
 
 __device__ __forceinline__ bool slot_ok(int64_t r, int lo, int64_t n) { return r >= lo && r < n; }
 
-template <bool SPEC>
+// SINGLE: one token per sequence (plain decode), S = 1 known at compile time.
+template <bool SPEC, bool SINGLE>
 __global__ void __launch_bounds__(DC_THREADS) decode_kernel(DecParams p) {
-    // dynamic LDS: conv weights [4][384] fp32 | conv + SiLU outputs [S][384] fp32 | window [3 + S][384] bf16
+    // dynamic LDS: conv weights [4][384] fp32 | conv + SiLU outputs [S][384] fp32 | bf16-rounded outputs [S][128] fp32
+    // | per-half-wave sums of squares [S][16] fp32 | window [3 + S][384] bf16
     extern __shared__ __align__(16) float dsm[];
     float* sCw = dsm;
-    float* sX = dsm + 4 * DC_CH;
-    uint16_t* sWin = reinterpret_cast<uint16_t*>(dsm + (4 + p.S) * DC_CH);
-    __shared__ float sO[2][D];                                        // head outputs of a token (double buffered)
-    __shared__ float sRed[2][4];                                      // per-wave sums of squares
+    float* sX = sCw + 4 * DC_CH;
+    float* sO = sX + p.S * DC_CH;
+    float* sRed = sO + p.S * D;
+    uint16_t* sWin = reinterpret_cast<uint16_t*>(sRed + p.S * 16);
 
-    const int n = blockIdx.x / p.H;
-    const int h = blockIdx.x - n * p.H;
+    // (sequence, head) of this workgroup, kept in SGPRs: buffer descriptors built from them must be wave-uniform
+    // values the compiler can see as such, or it wraps every buffer access in a waterfall loop
+    const int task = xcd_task(blockIdx.x, gridDim.x);
+    const int n = __builtin_amdgcn_readfirstlane(task / p.H);
+    const int h = __builtin_amdgcn_readfirstlane(task - n * p.H);
     const int tid = threadIdx.x;
-    const int w = tid >> 6, lane = tid & 63, grp = lane >> 4, j = lane & 15;
-    const int S = p.S, H = p.H;
+    const int S = SINGLE ? 1 : p.S, H = p.H;
     const int dim = H * D;
 
     int a = 1;
@@ -83,33 +88,57 @@ __global__ void __launch_bounds__(DC_THREADS) decode_kernel(DecParams p) {
         return;
     }
     const int start = SPEC ? a - 1 : 0;
+    const Walker wk(tid);
+    const int c0 = 4 * wk.c;
 
-    // ---- state (issued first: the largest transfer), then the window and conv weights
-    const int c0 = 4 * j;
-    const float* src = p.ssm + rd * p.ssm_ss + (int64_t)h * D * D;
-    f32x4 st[8][2];
-#pragma unroll
-    for (int pp = 0; pp < 8; ++pp) {
-        const int row = pp * 16 + w * 4 + grp;
-        st[pp][0] = *reinterpret_cast<const f32x4*>(src + row * D + c0);
-        st[pp][1] = *reinterpret_cast<const f32x4*>(src + row * D + 64 + c0);
-    }
-    // ---- window (3 history taps + S inputs) and conv weights of this head's channels
+    // ---- loads, in the order they are needed (vector memory completes in order): the window pieces and conv
+    // weights, token 0's operands, then the state.  Nothing waits for the state until the first token's walk.
     uint16_t* crow = p.conv + cs * p.conv_ss;
-    for (int i = tid; i < (3 + S) * (DC_CH / 8); i += DC_THREADS) {  // 16-byte pieces: 8 channels
+    const int npieces = (3 + S) * (DC_CH / 8);  // 16-byte window pieces: 8 channels each, at most 2 per thread
+    auto piece_src = [&](int i) {
         const int r = i / (DC_CH / 8), c8 = (i % (DC_CH / 8)) * 8;
-        const int grpc = c8 / D, ci = c8 % D;                        // q / k / v group, channel inside the head
-        const int64_t col = (int64_t)grpc * dim + h * D + ci;
-        const uint16_t* src = (r < 3) ? crow + (int64_t)(start + r) * p.conv_ts + col
-                                      : p.x + ((int64_t)n * S + (r - 3)) * p.x_rs + col;
-        *reinterpret_cast<u32x4*>(&sWin[r * DC_CH + c8]) = *reinterpret_cast<const u32x4*>(src);
+        const int64_t col = (int64_t)(c8 / D) * dim + h * D + c8 % D;
+        return (r < 3) ? crow + (int64_t)(start + r) * p.conv_ts + col : p.x + ((int64_t)n * S + (r - 3)) * p.x_rs + col;
+    };
+    u32x4 wp0 = {0u, 0u, 0u, 0u}, wp1 = {0u, 0u, 0u, 0u};
+    if (tid < npieces) wp0 = *reinterpret_cast<const u32x4*>(piece_src(tid));
+    if (tid + DC_THREADS < npieces) wp1 = *reinterpret_cast<const u32x4*>(piece_src(tid + DC_THREADS));
+    // conv weights: 4 taps x 384 channels = 384 quads; quad i -> tap i / 96, channels 4 (i % 96) .. + 3
+    f32x4 cwq = {0.f, 0.f, 0.f, 0.f};
+    const int cw_tap = tid / (DC_CH / 4), cw_c = (tid % (DC_CH / 4)) * 4;
+    if (tid < DC_CH) cwq = *reinterpret_cast<const f32x4*>(p.cw + ((int64_t)(cw_c / D) * 4 + cw_tap) * dim + h * D + cw_c % D);
+    struct Ops { u32x2 g; float beta; };
+    auto load_ops = [&](int t) {
+        Ops o;
+        const int64_t tok = (int64_t)n * S + t;
+        o.g = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(row_rsrc(p.gate + tok * p.gate_rs + h * D, D * 2),
+                                                                            8 * wk.c, 0, 0));
+        o.beta = sigmoidf_(bf2f(p.beta[tok * p.beta_rs + h]));
+        return o;
+    };
+    Ops op = load_ops(0);
+    // out_gate of the outputs this thread finishes after the walk: element i = tid + 512 k (token i / 128, row i % 128)
+    constexpr int OG_PER = (DC_MAX_S * D) / DC_THREADS;
+    uint32_t ogv[OG_PER];
+#pragma unroll
+    for (int k = 0; k < OG_PER; ++k) {
+        const int i = tid + k * DC_THREADS;
+        ogv[k] = i < S * D ? __builtin_amdgcn_raw_buffer_load_b16(
+                                 row_rsrc(p.og + ((int64_t)n * S + (i >> 7)) * p.og_rs + h * D, D * 2), 2 * (i & 127), 0, 0)
+                           : 0u;
     }
-    for (int i = tid; i < 4 * DC_CH; i += DC_THREADS) {
-        const int tap = i / DC_CH, c = i % DC_CH, grpc = c / D, ci = c % D;
-        sCw[i] = p.cw[((int64_t)grpc * 4 + tap) * dim + h * D + ci];
-    }
-    __syncthreads();
+    f32x4 st[8];
+    load_state(wk, p.ssm + rd * p.ssm_ss + (int64_t)h * D * D, st);
+    const float A = __expf(p.A_log[h]);
+    const f32x4 db = *reinterpret_cast<const f32x4*>(p.dt_bias + h * D + c0);
+    const float nw = p.nw[tid & (D - 1)];
+
+    if (tid < npieces) *reinterpret_cast<u32x4*>(&sWin[tid * 8]) = wp0;
+    if (tid + DC_THREADS < npieces) *reinterpret_cast<u32x4*>(&sWin[(tid + DC_THREADS) * 8]) = wp1;
+    if (tid < DC_CH) *reinterpret_cast<f32x4*>(&sCw[cw_tap * DC_CH + cw_c]) = cwq;
+    lds_barrier();
     // ---- conv + SiLU for every token; conv cache commit
+#pragma unroll 1
     for (int i = tid; i < S * DC_CH; i += DC_THREADS) {
         const int t = i / DC_CH, c = i % DC_CH;
         float acc = 0.f;
@@ -120,6 +149,7 @@ __global__ void __launch_bounds__(DC_THREADS) decode_kernel(DecParams p) {
     {
         // spec: taps [0, 2 + S) <- window[1 .. 3 + S);  plain: taps [0, 3) <- window[S .. S + 3)
         const int ntap = SPEC ? 2 + S : 3, first = SPEC ? 1 : S;
+#pragma unroll 1
         for (int i = tid; i < ntap * (DC_CH / 8); i += DC_THREADS) {
             const int r = i / (DC_CH / 8), c8 = (i % (DC_CH / 8)) * 8;
             const int grpc = c8 / D, ci = c8 % D;
@@ -127,106 +157,51 @@ __global__ void __launch_bounds__(DC_THREADS) decode_kernel(DecParams p) {
                 *reinterpret_cast<const u32x4*>(&sWin[(first + r) * DC_CH + c8]);
         }
     }
-    const float A = __expf(p.A_log[h]);
-    float db[8];
-#pragma unroll
-    for (int c = 0; c < 4; ++c) { db[c] = p.dt_bias[h * D + c0 + c]; db[4 + c] = p.dt_bias[h * D + 64 + c0 + c]; }
-    __syncthreads();  // sX complete
+    lds_barrier();  // sX complete
 
     for (int t = 0; t < S; ++t) {
-        const int64_t tok = (int64_t)n * S + t;
+        const Ops cur = op;
+        if (t + 1 < S) op = load_ops(t + 1);
         const float* xq = sX + t * DC_CH;
-        float kk[8], qq[8], dd[8], vv[8];
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            qq[c] = xq[c0 + c]; qq[4 + c] = xq[64 + c0 + c];
-            kk[c] = xq[D + c0 + c]; kk[4 + c] = xq[D + 64 + c0 + c];
-        }
+        const f32x4 q4 = *reinterpret_cast<const f32x4*>(xq + c0);
+        const f32x4 k4 = *reinterpret_cast<const f32x4*>(xq + D + c0);
+        float qq[4] = {q4.x, q4.y, q4.z, q4.w};
+        float kk[4] = {k4.x, k4.y, k4.z, k4.w};
+        float dd[4];
         {
-            const uint16_t* gb = p.gate + tok * p.gate_rs + h * D;
-            const u32x2 g0 = *reinterpret_cast<const u32x2*>(gb + c0);
-            const u32x2 g1 = *reinterpret_cast<const u32x2*>(gb + 64 + c0);
-            const float rg[8] = {bf2f(g0.x & 0xffffu), bf2f(g0.x >> 16), bf2f(g0.y & 0xffffu), bf2f(g0.y >> 16),
-                                 bf2f(g1.x & 0xffffu), bf2f(g1.x >> 16), bf2f(g1.y & 0xffffu), bf2f(g1.y >> 16)};
+            const float rg[4] = {bf2f(cur.g.x & 0xffffu), bf2f(cur.g.x >> 16), bf2f(cur.g.y & 0xffffu), bf2f(cur.g.y >> 16)};
+            const float d4[4] = {db.x, db.y, db.z, db.w};
 #pragma unroll
-            for (int c = 0; c < 8; ++c) dd[c] = __expf(p.lb * sigmoidf_(A * (rg[c] + db[c])));
+            for (int c = 0; c < 4; ++c) dd[c] = __expf(p.lb * sigmoidf_(A * (rg[c] + d4[c])));
         }
-        const float bt = sigmoidf_(bf2f(p.beta[tok * p.beta_rs + h]));
-        {  // x * rsqrt(sum x^2 + 1e-6)  (kda/mi350x/reference.py:159-160)
-            float sk = 0.f, sq = 0.f;
-#pragma unroll
-            for (int c = 0; c < 8; ++c) { sk += kk[c] * kk[c]; sq += qq[c] * qq[c]; }
-            sk = sum16(sk);
-            sq = sum16(sq);
-            const float ik = __frsqrt_rn(sk + 1e-6f), iq = __frsqrt_rn(sq + 1e-6f);
-#pragma unroll
-            for (int c = 0; c < 8; ++c) { kk[c] *= ik; qq[c] *= iq; }
-        }
-        float kq = 0.f;
-#pragma unroll
-        for (int c = 0; c < 8; ++c) kq += kk[c] * qq[c];
-        kq = sum16(kq);
-#pragma unroll
-        for (int pp = 0; pp < 8; ++pp) vv[pp] = xq[2 * D + pp * 16 + w * 4 + grp];
-        float ov[8];
-#pragma unroll
-        for (int pp = 0; pp < 8; ++pp) {
-            st[pp][0].x *= dd[0]; st[pp][0].y *= dd[1]; st[pp][0].z *= dd[2]; st[pp][0].w *= dd[3];
-            st[pp][1].x *= dd[4]; st[pp][1].y *= dd[5]; st[pp][1].z *= dd[6]; st[pp][1].w *= dd[7];
-            float ak = st[pp][0].x * kk[0] + st[pp][0].y * kk[1] + st[pp][0].z * kk[2] + st[pp][0].w * kk[3] +
-                       st[pp][1].x * kk[4] + st[pp][1].y * kk[5] + st[pp][1].z * kk[6] + st[pp][1].w * kk[7];
-            float aq = st[pp][0].x * qq[0] + st[pp][0].y * qq[1] + st[pp][0].z * qq[2] + st[pp][0].w * qq[3] +
-                       st[pp][1].x * qq[4] + st[pp][1].y * qq[5] + st[pp][1].z * qq[6] + st[pp][1].w * qq[7];
-            ak = sum16(ak);
-            aq = sum16(aq);
-            const float u = bt * (vv[pp] - ak);
-            ov[pp] = p.scale * (aq + u * kq);
-            st[pp][0].x += u * kk[0]; st[pp][0].y += u * kk[1]; st[pp][0].z += u * kk[2]; st[pp][0].w += u * kk[3];
-            st[pp][1].x += u * kk[4]; st[pp][1].y += u * kk[5]; st[pp][1].z += u * kk[6]; st[pp][1].w += u * kk[7];
-        }
-        if (j < 8) {  // lane j of each group holds row j * 16 + w * 4 + grp
-            float o = ov[0];
-#pragma unroll
-            for (int pp = 1; pp < 8; ++pp) o = (j == pp) ? ov[pp] : o;
-            sO[t & 1][j * 16 + w * 4 + grp] = o;
-        }
+        rsqrt_norm4(kk);  // x * rsqrt(sum x^2 + 1e-6)  (kda/mi350x/reference.py:159-160)
+        rsqrt_norm4(qq);
+        const float o = walk_token(st, kk, qq, dd, xq[2 * D + v_src_row(wk)], cur.beta, p.scale, wk.c);
+        // bf16(o) of the lane's row and the half wave's sum of squares (lanes c < 8 hold the half's 8 rows)
+        const float ob = bf2f(f2bf(o));
+        const float ss = sum32(wk.c < 8 ? ob * ob : 0.f);
+        if (wk.c < 8) sO[t * D + wk.row(wk.c)] = ob;
+        if (wk.c == 0) sRed[t * 16 + 2 * wk.w + wk.half] = ss;
         if (SPEC) {
             const int64_t wr = p.idx[(int64_t)n * S + t];
-            if (slot_ok(wr, 1, p.ssm_slots)) {
-                float* dst = p.ssm + wr * p.ssm_ss + (int64_t)h * D * D;
-#pragma unroll
-                for (int pp = 0; pp < 8; ++pp) {
-                    const int row = pp * 16 + w * 4 + grp;
-                    *reinterpret_cast<f32x4*>(dst + row * D + c0) = st[pp][0];
-                    *reinterpret_cast<f32x4*>(dst + row * D + 64 + c0) = st[pp][1];
-                }
-            }
-        }
-        __syncthreads();
-        // ---- gated RMSNorm over the head's 128 outputs (threads 0..127), y = bf16(o) rstd nw sigmoid(og)
-        float ob = 0.f;
-        if (tid < D) {
-            ob = bf2f(f2bf(sO[t & 1][tid]));
-            float ss = ob * ob;
-            ss += __shfl_xor(ss, 32);
-            ss = sum16(ss);
-            ss += __shfl_xor(ss, 16);
-            if (lane == 0) sRed[t & 1][w] = ss;
-        }
-        __syncthreads();
-        if (tid < D) {
-            const float rstd = __frsqrt_rn((sRed[t & 1][0] + sRed[t & 1][1]) * (1.f / D) + p.eps);
-            const float g = bf2f(p.og[tok * p.og_rs + h * D + tid]);
-            p.out[tok * p.out_rs + h * D + tid] = (uint16_t)f2bf(ob * rstd * p.nw[tid] * sigmoidf_(g));
+            if (slot_ok(wr, 1, p.ssm_slots)) store_state(wk, p.ssm + wr * p.ssm_ss + (int64_t)h * D * D, st);
         }
     }
-    if (!SPEC) {
-        float* dst = p.ssm + rd * p.ssm_ss + (int64_t)h * D * D;
+    if (!SPEC) store_state(wk, p.ssm + rd * p.ssm_ss + (int64_t)h * D * D, st);
+    lds_barrier();
+    // ---- gated RMSNorm of every token's 128 outputs: y = bf16(o) rsqrt(mean(bf16(o)^2) + eps) nw sigmoid(og)
 #pragma unroll
-        for (int pp = 0; pp < 8; ++pp) {
-            const int row = pp * 16 + w * 4 + grp;
-            *reinterpret_cast<f32x4*>(dst + row * D + c0) = st[pp][0];
-            *reinterpret_cast<f32x4*>(dst + row * D + 64 + c0) = st[pp][1];
+    for (int k = 0; k < OG_PER; ++k) {
+        const int i = tid + k * DC_THREADS;
+        if (i < S * D) {
+            const int t = i >> 7;
+            const f32x4* r4 = reinterpret_cast<const f32x4*>(sRed + t * 16);
+            const f32x4 s4 = (r4[0] + r4[1]) + (r4[2] + r4[3]);
+            const float rstd = __frsqrt_rn((s4.x + s4.y + s4.z + s4.w) * (1.f / D) + p.eps);
+            const float y = sO[i] * rstd * nw * sigmoidf_(bf2f(ogv[k]));
+            __builtin_amdgcn_raw_buffer_store_b16((unsigned short)f2bf(y),
+                                                  row_rsrc(p.out + ((int64_t)n * S + t) * p.out_rs + h * D, D * 2),
+                                                  2 * (i & 127), 0, 0);
         }
     }
 }
@@ -257,6 +232,7 @@ extern "C" int kda355_decode_launch(const KdaDecodeArgs* a, kda355_stream_t stre
     KDA_CHECK_ARG(aligned(a->conv_state, 16) && a->conv_slot_stride % 8 == 0 && a->conv_tap_stride % 8 == 0,
                   "decode: conv_state rows must be 16-byte aligned");
     KDA_CHECK_ARG(aligned(a->gate, 8) && a->gate_row_stride % 4 == 0, "decode: gate rows must be 8-byte aligned");
+    KDA_CHECK_ARG(aligned(a->conv_weight, 16) && aligned(a->dt_bias, 16), "decode: conv_weight and dt_bias must be 16-byte aligned");
     KDA_CHECK_ARG(aligned(a->ssm_state, 16) && a->ssm_slot_stride % 4 == 0, "decode: ssm_state must be 16-byte aligned");
     KDA_CHECK_ARG((int64_t)a->B * a->H < (1ll << 31), "decode: grid too large");
     DecParams p;
@@ -290,11 +266,14 @@ extern "C" int kda355_decode_launch(const KdaDecodeArgs* a, kda355_stream_t stre
     p.lb = a->lower_bound;
     p.scale = 0.08838834764831845f;  // 128^-1/2: the reference scales the normalized q
     const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    const size_t lds = (size_t)(4 + a->S) * DC_CH * sizeof(float) + (size_t)(3 + a->S) * DC_CH * sizeof(uint16_t);
+    const size_t lds = ((size_t)(4 + a->S) * DC_CH + (size_t)a->S * (D + 16)) * sizeof(float) +
+                       (size_t)(3 + a->S) * DC_CH * sizeof(uint16_t);
     if (spec)
-        hipLaunchKernelGGL(decode_kernel<true>, dim3(a->B * a->H), dim3(DC_THREADS), lds, s, p);
+        hipLaunchKernelGGL((decode_kernel<true, false>), dim3(a->B * a->H), dim3(DC_THREADS), lds, s, p);
+    else if (a->S == 1)
+        hipLaunchKernelGGL((decode_kernel<false, true>), dim3(a->B * a->H), dim3(DC_THREADS), lds, s, p);
     else
-        hipLaunchKernelGGL(decode_kernel<false>, dim3(a->B * a->H), dim3(DC_THREADS), lds, s, p);
+        hipLaunchKernelGGL((decode_kernel<false, false>), dim3(a->B * a->H), dim3(DC_THREADS), lds, s, p);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         set_error("decode: launch failed: %s", hipGetErrorString(e));

@@ -103,7 +103,6 @@ __device__ __forceinline__ float exp2_(float x) { return __builtin_amdgcn_exp2f(
 // Workgroup barrier for LDS traffic only.  __syncthreads() also fences global memory (s_waitcnt vmcnt(0)), which
 // would wait for the next chunk's prefetched loads and for the output stores at every phase boundary; the waves of
 // this kernel exchange data through LDS alone, so completing the LDS operations (lgkmcnt(0)) is sufficient.
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // Sum over each group of 8 consecutive lanes (quad swaps, then the mirrored quad).
 __device__ __forceinline__ float sum8(float x) {

@@ -1,20 +1,18 @@
 // Recurrent KDA decode / speculative verify on gfx950, and the commit of an accepted draft length.
 //
 // The step is a bandwidth-bound read-modify-write of the fp32 128 x 128 state of each (sequence, head): 64 KiB read,
-// 64 KiB written per stored state.  One workgroup of 256 threads (4 wave64) owns one (sequence, head):
-//   * lane l of wave w holds state rows  p*16 + w*4 + l/16  (p = 0..7)  and columns  4*(l%16) + {0..3}, 64 + 4*(l%16) + {0..3}
-//     -> 64 fp32 registers, each wave load instruction reads 4 rows x 256 contiguous bytes (16-byte lanes);
-//   * a state row lives in one group of 16 lanes, so both row reductions (S k and S q) are 4 DPP steps;
-//   * o_t = scale * (S' q + u (k . q)) with S' the decayed state before the rank-1 update -- the two reductions are
-//     independent, so they are issued together (algebraically the reference's o = scale * S_new q).
+// 64 KiB written per stored state.  One workgroup of 512 threads (8 wave64) owns one (sequence, head) and walks its
+// tokens with the state in registers (walk.h: row layout, cache policy, 32-lane row reductions);
+// o_t = scale * (S' q + u (k . q)) with S' the decayed state before the rank-1 update -- the two reductions are
+// independent, so they are issued together (algebraically the reference's o = scale * S_new q).
 // Semantics: kda/mi350x/reference.py:155-171 (recurrent core), slot rules kda/mi350x/kda/decode/kda_v14_b.cu:1013-1042
 // (padding slot 0 and out-of-range rows are never read or written; such a sequence's output rows are zero).
-#include "common.h"
+#include "walk.h"
 
 namespace kda355 {
 namespace {
 
-constexpr int REC_THREADS = 256;
+constexpr int REC_THREADS = WK_THREADS;
 
 struct RecParams {
     const uint16_t* q;
@@ -39,17 +37,20 @@ struct RecParams {
 
 __device__ __forceinline__ bool row_ok(int64_t r, int64_t lo, int64_t slots) { return r >= lo && r < slots; }
 
-template <bool RAW_GATE, bool RAW_BETA, bool NORM, bool PER_TOKEN>
+// MODE: REC_SINGLE one token per sequence (plain decode, S = 1 known at compile time), REC_MULTI several tokens with
+// the final state written back, REC_PER_TOKEN the state after every token written (spec verify).
+enum { REC_SINGLE = 0, REC_MULTI = 1, REC_PER_TOKEN_MODE = 2 };
+
+template <bool RAW_GATE, bool RAW_BETA, bool NORM, int MODE>
 __global__ void __launch_bounds__(REC_THREADS) recurrent_kernel(RecParams p) {
-    const int bid = blockIdx.x;
-    const int n = bid / p.H;
-    const int h = bid - n * p.H;
+    constexpr bool PER_TOKEN = MODE == REC_PER_TOKEN_MODE;
+    // (sequence, head) of this workgroup, kept in SGPRs: buffer descriptors built from them must be wave-uniform
+    // values the compiler can see as such, or it wraps every buffer access in a waterfall loop
+    const int task = xcd_task(blockIdx.x, gridDim.x);
+    const int n = __builtin_amdgcn_readfirstlane(task / p.H);
+    const int h = __builtin_amdgcn_readfirstlane(task - n * p.H);
     const int tid = threadIdx.x;
-    const int w = tid >> 6;
-    const int lane = tid & 63;
-    const int grp = lane >> 4;
-    const int j = lane & 15;
-    const int S = p.S;
+    const int S = MODE == REC_SINGLE ? 1 : p.S;
 
     int a = 1;
     if (p.num_accepted) {
@@ -70,151 +71,98 @@ __global__ void __launch_bounds__(REC_THREADS) recurrent_kernel(RecParams p) {
         return;
     }
 
-    // ---- load the state: 8 rows x 8 columns per thread
-    const int c0 = 4 * j;
-    const float* src = p.read_pool + rd * p.read_ss + (int64_t)h * D * D;
-    f32x4 st[8][2];
-#pragma unroll
-    for (int pp = 0; pp < 8; ++pp) {
-        const int row = pp * 16 + w * 4 + grp;
-        st[pp][0] = *reinterpret_cast<const f32x4*>(src + row * D + c0);
-        st[pp][1] = *reinterpret_cast<const f32x4*>(src + row * D + 64 + c0);
+    // Per-token operands of this head, raw (converted at use).  Token t + 1's are loaded before token t's state
+    // stores and token 0's before the state loads: vector memory completes in order, so an operand never waits
+    // behind a state transfer issued after it.
+    const Walker wk(tid);
+    struct Ops { u32x2 k, q, g2; f32x4 g4; uint32_t v; float beta; };
+    auto load_ops = [&](int t) {
+        Ops o;
+        const int64_t tok = (int64_t)n * S + t;
+        const int64_t ro = tok * p.qkv_rs + h * D;
+        o.k = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(row_rsrc(p.k + ro, D * 2), 8 * wk.c, 0, 0));
+        o.q = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(row_rsrc(p.q + ro, D * 2), 8 * wk.c, 0, 0));
+        o.v = __builtin_amdgcn_raw_buffer_load_b16(row_rsrc(p.v + ro, D * 2), 2 * v_src_row(wk), 0, 0);
+        if (RAW_GATE)
+            o.g2 = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(
+                row_rsrc(reinterpret_cast<const uint16_t*>(p.g) + tok * p.g_rs + h * D, D * 2), 8 * wk.c, 0, 0));
+        else
+            o.g4 = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                row_rsrc(reinterpret_cast<const float*>(p.g) + tok * p.g_rs + h * D, D * 4), 16 * wk.c, 0, 0));
+        if (RAW_BETA)
+            o.beta = sigmoidf_(bf2f(reinterpret_cast<const uint16_t*>(p.beta)[tok * p.beta_rs + h]));
+        else
+            o.beta = reinterpret_cast<const float*>(p.beta)[tok * p.beta_rs + h];
+        return o;
+    };
+    Ops op = load_ops(0);
+    // ---- state: 8 rows x 4 columns per lane
+    f32x4 st[8];
+    load_state(wk, p.read_pool + rd * p.read_ss + (int64_t)h * D * D, st);
+    float A = 0.f, db[4] = {0.f, 0.f, 0.f, 0.f};
+    if (RAW_GATE) {
+        A = __expf(p.A_log[h]);
+        const f32x4 d4 = *reinterpret_cast<const f32x4*>(p.dt_bias + h * D + 4 * wk.c);
+        db[0] = d4.x; db[1] = d4.y; db[2] = d4.z; db[3] = d4.w;
     }
 
     for (int t = 0; t < S; ++t) {
         const int64_t tok = (int64_t)n * S + t;
-        // k, q: columns c0..c0+3 and 64+c0..64+c0+3 (4 bf16 = 8 bytes each)
-        const uint16_t* kq_base = p.k + tok * p.qkv_rs + h * D;
-        const uint16_t* qq_base = p.q + tok * p.qkv_rs + h * D;
-        const u32x2 kb0 = *reinterpret_cast<const u32x2*>(kq_base + c0);
-        const u32x2 kb1 = *reinterpret_cast<const u32x2*>(kq_base + 64 + c0);
-        const u32x2 qb0 = *reinterpret_cast<const u32x2*>(qq_base + c0);
-        const u32x2 qb1 = *reinterpret_cast<const u32x2*>(qq_base + 64 + c0);
-        float kk[8], qq[8], dd[8];
-        kk[0] = bf2f(kb0.x & 0xffffu); kk[1] = bf2f(kb0.x >> 16); kk[2] = bf2f(kb0.y & 0xffffu); kk[3] = bf2f(kb0.y >> 16);
-        kk[4] = bf2f(kb1.x & 0xffffu); kk[5] = bf2f(kb1.x >> 16); kk[6] = bf2f(kb1.y & 0xffffu); kk[7] = bf2f(kb1.y >> 16);
-        qq[0] = bf2f(qb0.x & 0xffffu); qq[1] = bf2f(qb0.x >> 16); qq[2] = bf2f(qb0.y & 0xffffu); qq[3] = bf2f(qb0.y >> 16);
-        qq[4] = bf2f(qb1.x & 0xffffu); qq[5] = bf2f(qb1.x >> 16); qq[6] = bf2f(qb1.y & 0xffffu); qq[7] = bf2f(qb1.y >> 16);
+        const Ops cur = op;
+        if (t + 1 < S) op = load_ops(t + 1);
+        float kk[4] = {bf2f(cur.k.x & 0xffffu), bf2f(cur.k.x >> 16), bf2f(cur.k.y & 0xffffu), bf2f(cur.k.y >> 16)};
+        float qq[4] = {bf2f(cur.q.x & 0xffffu), bf2f(cur.q.x >> 16), bf2f(cur.q.y & 0xffffu), bf2f(cur.q.y >> 16)};
+        float dd[4];
         if (RAW_GATE) {
-            const uint16_t* gb = reinterpret_cast<const uint16_t*>(p.g) + tok * p.g_rs + h * D;
-            const u32x2 g0 = *reinterpret_cast<const u32x2*>(gb + c0);
-            const u32x2 g1 = *reinterpret_cast<const u32x2*>(gb + 64 + c0);
-            const float rg[8] = {bf2f(g0.x & 0xffffu), bf2f(g0.x >> 16), bf2f(g0.y & 0xffffu), bf2f(g0.y >> 16),
-                                 bf2f(g1.x & 0xffffu), bf2f(g1.x >> 16), bf2f(g1.y & 0xffffu), bf2f(g1.y >> 16)};
-            const float A = __expf(p.A_log[h]);
-            const f32x4 db0 = *reinterpret_cast<const f32x4*>(p.dt_bias + h * D + c0);
-            const f32x4 db1 = *reinterpret_cast<const f32x4*>(p.dt_bias + h * D + 64 + c0);
-            const float db[8] = {db0.x, db0.y, db0.z, db0.w, db1.x, db1.y, db1.z, db1.w};
+            const float rg[4] = {bf2f(cur.g2.x & 0xffffu), bf2f(cur.g2.x >> 16), bf2f(cur.g2.y & 0xffffu),
+                                 bf2f(cur.g2.y >> 16)};
 #pragma unroll
-            for (int c = 0; c < 8; ++c) dd[c] = __expf(p.lb * sigmoidf_(A * (rg[c] + db[c])));
+            for (int c = 0; c < 4; ++c) dd[c] = __expf(p.lb * sigmoidf_(A * (rg[c] + db[c])));
         } else {
-            const float* gb = reinterpret_cast<const float*>(p.g) + tok * p.g_rs + h * D;
-            const f32x4 g0 = *reinterpret_cast<const f32x4*>(gb + c0);
-            const f32x4 g1 = *reinterpret_cast<const f32x4*>(gb + 64 + c0);
-            dd[0] = __expf(g0.x); dd[1] = __expf(g0.y); dd[2] = __expf(g0.z); dd[3] = __expf(g0.w);
-            dd[4] = __expf(g1.x); dd[5] = __expf(g1.y); dd[6] = __expf(g1.z); dd[7] = __expf(g1.w);
-        }
-        float bt;
-        if (RAW_BETA) {
-            const uint16_t* bb = reinterpret_cast<const uint16_t*>(p.beta);
-            bt = sigmoidf_(bf2f(bb[tok * p.beta_rs + h]));
-        } else {
-            bt = reinterpret_cast<const float*>(p.beta)[tok * p.beta_rs + h];
+            dd[0] = __expf(cur.g4.x); dd[1] = __expf(cur.g4.y); dd[2] = __expf(cur.g4.z); dd[3] = __expf(cur.g4.w);
         }
         if (NORM) {  // x * rsqrt(sum x^2 + 1e-6)  (kda/mi350x/reference.py:159-160)
-            float sk = 0.f, sq = 0.f;
-#pragma unroll
-            for (int c = 0; c < 8; ++c) { sk += kk[c] * kk[c]; sq += qq[c] * qq[c]; }
-            sk = sum16(sk);
-            sq = sum16(sq);
-            const float ik = __frsqrt_rn(sk + 1e-6f), iq = __frsqrt_rn(sq + 1e-6f);
-#pragma unroll
-            for (int c = 0; c < 8; ++c) { kk[c] *= ik; qq[c] *= iq; }
+            rsqrt_norm4(kk);
+            rsqrt_norm4(qq);
         }
-        float kq = 0.f;
-#pragma unroll
-        for (int c = 0; c < 8; ++c) kq += kk[c] * qq[c];
-        kq = sum16(kq);
-
-        // v for this thread's 8 rows
-        const uint16_t* vb = p.v + tok * p.qkv_rs + h * D;
-        float vv[8];
-#pragma unroll
-        for (int pp = 0; pp < 8; ++pp) vv[pp] = bf2f(vb[pp * 16 + w * 4 + grp]);
-
-        float ov[8];
-#pragma unroll
-        for (int pp = 0; pp < 8; ++pp) {
-            st[pp][0].x *= dd[0]; st[pp][0].y *= dd[1]; st[pp][0].z *= dd[2]; st[pp][0].w *= dd[3];
-            st[pp][1].x *= dd[4]; st[pp][1].y *= dd[5]; st[pp][1].z *= dd[6]; st[pp][1].w *= dd[7];
-            float ak = st[pp][0].x * kk[0] + st[pp][0].y * kk[1] + st[pp][0].z * kk[2] + st[pp][0].w * kk[3] +
-                       st[pp][1].x * kk[4] + st[pp][1].y * kk[5] + st[pp][1].z * kk[6] + st[pp][1].w * kk[7];
-            float aq = st[pp][0].x * qq[0] + st[pp][0].y * qq[1] + st[pp][0].z * qq[2] + st[pp][0].w * qq[3] +
-                       st[pp][1].x * qq[4] + st[pp][1].y * qq[5] + st[pp][1].z * qq[6] + st[pp][1].w * qq[7];
-            ak = sum16(ak);
-            aq = sum16(aq);
-            const float u = bt * (vv[pp] - ak);
-            ov[pp] = p.scale * (aq + u * kq);
-            st[pp][0].x += u * kk[0]; st[pp][0].y += u * kk[1]; st[pp][0].z += u * kk[2]; st[pp][0].w += u * kk[3];
-            st[pp][1].x += u * kk[4]; st[pp][1].y += u * kk[5]; st[pp][1].z += u * kk[6]; st[pp][1].w += u * kk[7];
-        }
-        // output: lane j < 8 of each group writes row (j*16 + w*4 + grp)
-        {
-            float o = ov[0];
-#pragma unroll
-            for (int pp = 1; pp < 8; ++pp) o = (j == pp) ? ov[pp] : o;
-            if (j < 8) p.out[tok * p.out_rs + h * D + j * 16 + w * 4 + grp] = (uint16_t)f2bf(o);
-        }
+        const float o = walk_token(st, kk, qq, dd, bf2f(cur.v), cur.beta, p.scale, wk.c);
+        // output: lane c < 8 of each half wave writes row 16 c + 2 w + half
+        if (wk.c < 8)
+            __builtin_amdgcn_raw_buffer_store_b16((unsigned short)f2bf(o), row_rsrc(p.out + tok * p.out_rs + h * D, D * 2),
+                                                  2 * wk.row(wk.c), 0, 0);
         if (PER_TOKEN) {
             const int64_t wr = p.write_idx[(int64_t)n * S + t];
-            if (row_ok(wr, p.write_min, p.write_slots)) {
-                float* dst = p.write_pool + wr * p.write_ss + (int64_t)h * D * D;
-#pragma unroll
-                for (int pp = 0; pp < 8; ++pp) {
-                    const int row = pp * 16 + w * 4 + grp;
-                    *reinterpret_cast<f32x4*>(dst + row * D + c0) = st[pp][0];
-                    *reinterpret_cast<f32x4*>(dst + row * D + 64 + c0) = st[pp][1];
-                }
-            }
+            if (row_ok(wr, p.write_min, p.write_slots)) store_state(wk, p.write_pool + wr * p.write_ss + (int64_t)h * D * D, st);
         }
     }
-    if (!PER_TOKEN) {
-        float* dst = p.read_pool + rd * p.read_ss + (int64_t)h * D * D;
-#pragma unroll
-        for (int pp = 0; pp < 8; ++pp) {
-            const int row = pp * 16 + w * 4 + grp;
-            *reinterpret_cast<f32x4*>(dst + row * D + c0) = st[pp][0];
-            *reinterpret_cast<f32x4*>(dst + row * D + 64 + c0) = st[pp][1];
-        }
-    }
+    if (!PER_TOKEN) store_state(wk, p.read_pool + rd * p.read_ss + (int64_t)h * D * D, st);
 }
 
 // Copy one (sequence, head) state: scratch[scratch_idx[n, a-1]] -> pool[pool_idx[n]].
-__global__ void __launch_bounds__(256) spec_commit_kernel(KdaSpecCommitArgs a, bool slot0) {
-    const int n = blockIdx.x / a.H;
-    const int h = blockIdx.x - n * a.H;
+__global__ void __launch_bounds__(WK_THREADS) spec_commit_kernel(KdaSpecCommitArgs a, bool slot0) {
+    const int task = xcd_task(blockIdx.x, gridDim.x);
+    const int n = __builtin_amdgcn_readfirstlane(task / a.H);
+    const int h = __builtin_amdgcn_readfirstlane(task - n * a.H);
     int acc = a.num_accepted[n];
     acc = acc < 1 ? 1 : (acc > a.S ? a.S : acc);
     const int64_t sr = a.scratch_idx[(int64_t)n * a.S + acc - 1];
     const int64_t pr = a.pool_idx[n];
     if (sr < 0 || sr >= a.scratch_slots || pr < (slot0 ? 1 : 0) || pr >= a.pool_slots) return;
-    const f32x4* s = reinterpret_cast<const f32x4*>(a.scratch + sr * a.scratch_slot_stride + (int64_t)h * D * D);
-    f32x4* d = reinterpret_cast<f32x4*>(a.pool + pr * a.pool_slot_stride + (int64_t)h * D * D);
-    f32x4 buf[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) buf[i] = s[i * 256 + threadIdx.x];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) d[i * 256 + threadIdx.x] = buf[i];
+    const Walker wk(threadIdx.x);
+    f32x4 buf[8];
+    load_state(wk, a.scratch + sr * a.scratch_slot_stride + (int64_t)h * D * D, buf);
+    store_state(wk, a.pool + pr * a.pool_slot_stride + (int64_t)h * D * D, buf);
 }
 
-template <bool RG, bool RB, bool NM, bool PT>
+template <bool RG, bool RB, bool NM, int MODE>
 hipError_t launch_rec(const RecParams& p, hipStream_t s) {
-    hipLaunchKernelGGL((recurrent_kernel<RG, RB, NM, PT>), dim3(p.B * p.H), dim3(REC_THREADS), 0, s, p);
+    hipLaunchKernelGGL((recurrent_kernel<RG, RB, NM, MODE>), dim3(p.B * p.H), dim3(REC_THREADS), 0, s, p);
     return hipGetLastError();
 }
 template <bool RG, bool RB, bool NM>
 hipError_t disp3(const RecParams& p, bool pt, hipStream_t s) {
-    return pt ? launch_rec<RG, RB, NM, true>(p, s) : launch_rec<RG, RB, NM, false>(p, s);
+    if (pt) return launch_rec<RG, RB, NM, REC_PER_TOKEN_MODE>(p, s);
+    return p.S == 1 ? launch_rec<RG, RB, NM, REC_SINGLE>(p, s) : launch_rec<RG, RB, NM, REC_MULTI>(p, s);
 }
 template <bool RG, bool RB>
 hipError_t disp2(const RecParams& p, bool nm, bool pt, hipStream_t s) {
@@ -303,7 +251,7 @@ extern "C" int kda355_spec_commit_launch(const KdaSpecCommitArgs* a, kda355_stre
     KDA_CHECK_ARG(aligned(a->scratch, 16) && aligned(a->pool, 16) && a->scratch_slot_stride % 4 == 0 &&
                       a->pool_slot_stride % 4 == 0,
                   "spec_commit: pools must be 16-byte aligned");
-    hipLaunchKernelGGL(spec_commit_kernel, dim3(a->B * a->H), dim3(256), 0, reinterpret_cast<hipStream_t>(stream), *a,
+    hipLaunchKernelGGL(spec_commit_kernel, dim3(a->B * a->H), dim3(WK_THREADS), 0, reinterpret_cast<hipStream_t>(stream), *a,
                        (a->flags & KDA355_REC_SLOT0_RESERVED) != 0);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {

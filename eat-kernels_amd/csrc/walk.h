@@ -1,0 +1,135 @@
+// The per-token state walk shared by the recurrent decode kernel and the fused decode kernel (gfx950, wave64).
+//
+// One workgroup of 512 threads (8 wave64) owns the 64 KiB fp32 state [V = 128][K = 128] of one (sequence, head).
+// Lanes 32 h .. 32 h + 31 of wave w hold state row  16 p + 2 w + h  (p = 0..7) at columns  4 (l % 32) .. + 3:
+// 8 f32x4 registers per lane; one wave instruction touches 2 full rows (1 KiB contiguous) and the workgroup 8 KiB
+// contiguous per p.  A whole state in one workgroup with >= 8 waves, nontemporal loads and write-through stores
+// (sc0 | sc1) is the measured best read-modify-write pattern on MI355X (6.2 TB/s against 5.1 TB/s for 4-wave
+// workgroups with the default cache policy, and 5.4 TB/s for 8-wave workgroups on half a state).  Row reductions (S k, S q) run over 32 lanes: 4 DPP steps inside a row of 16 lanes and one
+// swizzle across the two rows.
+#pragma once
+#include "common.h"
+
+namespace kda355 {
+
+constexpr int WK_THREADS = 512;
+constexpr int WK_LOAD_AUX = 2;    // nt: streaming load
+constexpr int WK_STORE_AUX = 17;  // sc0 | sc1: system-scope store, written through the L2
+
+// Sum over the 32 lanes of each half wave; every lane of the half receives the total.
+__device__ __forceinline__ float sum32(float x) {
+    x = sum16(x);
+    // ds_swizzle bit mode: and 0x1f, or 0, xor 0x10 -> lane ^ 16 inside each group of 32
+    return x + __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(x), 0x401F));
+}
+
+// XCD-aware task order.  Workgroup b of a launch runs on XCD b % 8 (round-robin dispatch over the 8 XCDs of an
+// MI355X); giving each XCD a contiguous range of (sequence, head) tasks keeps the workgroups that touch neighbouring
+// 64 KiB state blocks on one XCD.  On page pools (state blocks not 64 KiB aligned) this is worth ~6% of bandwidth.
+// Exact bijection of [0, total): XCD x owns [x (total / 8) + min(x, total % 8), ...) of size total / 8 + (x < total % 8).
+__device__ __forceinline__ int xcd_task(int b, int total) {
+    const int x = b & 7, q = total >> 3, r = total & 7;
+    return x * q + (x < r ? x : r) + (b >> 3);
+}
+
+struct Walker {
+    int w, half, c;  // wave, half wave, column group (columns 4c .. 4c + 3)
+    __device__ __forceinline__ explicit Walker(int tid) : w(tid >> 6), half((tid >> 5) & 1), c(tid & 31) {}
+    __device__ __forceinline__ int row(int p) const { return 16 * p + 2 * w + half; }
+    // byte offset of row p = voff() + p * 8 KiB: the lane part stays in one VGPR, the row step is an SGPR offset
+    __device__ __forceinline__ int voff() const { return ((2 * w + half) * D + 4 * c) * 4; }
+};
+constexpr int WK_ROW_STEP = 16 * D * 4;
+
+// A wave-uniform address taken through readfirstlane: the compiler may otherwise compute uniform 64-bit address
+// arithmetic in VGPRs (v_lshl_add_u64), and a buffer descriptor built from a VGPR base becomes a waterfall loop.
+__device__ __forceinline__ void* uniform_ptr(const void* p) {
+    const uint64_t a = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+    return reinterpret_cast<void*>(((uint64_t)hi << 32) | lo);
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t state_rsrc(const float* base) {
+    return __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(base), (short)0, D * D * 4, 0x00020000);
+}
+
+__device__ __forceinline__ void load_state(const Walker& wk, const float* base, f32x4 (&st)[8]) {
+    const __amdgpu_buffer_rsrc_t rs = state_rsrc(base);
+#pragma unroll
+    for (int p = 0; p < 8; ++p)
+        st[p] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, wk.voff(), p * WK_ROW_STEP, WK_LOAD_AUX));
+}
+
+__device__ __forceinline__ void store_state(const Walker& wk, float* base, const f32x4 (&st)[8]) {
+    const __amdgpu_buffer_rsrc_t rs = state_rsrc(base);
+#pragma unroll
+    for (int p = 0; p < 8; ++p)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, st[p]), rs, wk.voff(), p * WK_ROW_STEP,
+                                               WK_STORE_AUX);
+}
+
+// A buffer descriptor over `bytes` bytes at a wave-uniform base (the per-token operand rows).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t row_rsrc(const void* base, int bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(base), (short)0, bytes, 0x00020000);
+}
+// 4 bf16 at byte offset off of a row -> fp32
+__device__ __forceinline__ void load_bf16x4(__amdgpu_buffer_rsrc_t rs, int off, float (&x)[4]) {
+    const u32x2 b = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, 0));
+    x[0] = bf2f(b.x & 0xffffu); x[1] = bf2f(b.x >> 16); x[2] = bf2f(b.y & 0xffffu); x[3] = bf2f(b.y >> 16);
+}
+
+// x * rsqrt(sum x^2 + 1e-6) over the 128 channels held 4 per lane by each half wave (kda/mi350x/reference.py:159-160).
+__device__ __forceinline__ void rsqrt_norm4(float (&x)[4]) {
+    const float s = sum32(x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3]);
+    const float r = __frsqrt_rn(s + 1e-6f);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x[i] *= r;
+}
+
+// v of row 16 p + 2 w + half from the lanes that hold it: lane c of each 16-lane row holds v[16 (c % 8) + 2 w + half]
+// (vsrc); ds_swizzle bit mode (and 0x10, or p) reads lane p of the caller's 16-lane row.
+template <int P>
+__device__ __forceinline__ float v_of_row(float vsrc) {
+    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(vsrc), (P << 5) | 0x10));
+}
+// Lane c's source row for v_of_row: 16 (c % 8) + 2 w + half.
+__device__ __forceinline__ int v_src_row(const Walker& wk) { return 16 * (wk.c & 7) + 2 * wk.w + wk.half; }
+
+// One token of the gated delta rule on this lane's 8 rows: S *= exp(g) along K; u = beta (v - S k); S += u k^T;
+// o = scale * (S_decayed q + u (k . q)) (= scale * S_new q).  dd = exp(g) of the lane's 4 key columns, vsrc = v at
+// row v_src_row() (each row's v is broadcast from it).  Every lane of a half wave computes its 8 rows' full sums; the
+// return value is o at row 16 c + 2 w + half (meaningful on lanes c < 8).  Rows are reduced in two groups of 4 to
+// keep few values live.
+__device__ __forceinline__ float walk_token(f32x4 (&st)[8], const float (&kk)[4], const float (&qq)[4],
+                                            const float (&dd)[4], float vsrc, float bt, float scale, int c) {
+    float vv[8];
+    vv[0] = v_of_row<0>(vsrc); vv[1] = v_of_row<1>(vsrc); vv[2] = v_of_row<2>(vsrc); vv[3] = v_of_row<3>(vsrc);
+    vv[4] = v_of_row<4>(vsrc); vv[5] = v_of_row<5>(vsrc); vv[6] = v_of_row<6>(vsrc); vv[7] = v_of_row<7>(vsrc);
+    const float kq = sum32(kk[0] * qq[0] + kk[1] * qq[1] + kk[2] * qq[2] + kk[3] * qq[3]);
+    float osel = 0.f;
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+        float ak[4], aq[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            f32x4& s = st[4 * g + i];
+            s.x *= dd[0]; s.y *= dd[1]; s.z *= dd[2]; s.w *= dd[3];
+            ak[i] = s.x * kk[0] + s.y * kk[1] + s.z * kk[2] + s.w * kk[3];
+            aq[i] = s.x * qq[0] + s.y * qq[1] + s.z * qq[2] + s.w * qq[3];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) { ak[i] = sum32(ak[i]); aq[i] = sum32(aq[i]); }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            f32x4& s = st[4 * g + i];
+            const float u = bt * (vv[4 * g + i] - ak[i]);
+            const float o = scale * (aq[i] + u * kq);
+            osel = (c == 4 * g + i) ? o : osel;
+            s.x += u * kk[0]; s.y += u * kk[1]; s.z += u * kk[2]; s.w += u * kk[3];
+        }
+    }
+    return osel;
+}
+
+}  // namespace kda355

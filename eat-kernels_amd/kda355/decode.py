@@ -6,7 +6,9 @@
 Same signature and argument meaning as the reference's `kernel.decode` (kda/mi350x/kda/kernel.py:212-216; semantics
 kda/mi350x/reference.py:104-181): one call runs the width-4 causal conv + SiLU with the rolling bf16 conv cache, the
 q/k norms, the gate and beta activations, the gated delta rule on the fp32 state pool and the gated RMSNorm, for
-B sequences of S tokens (T = B * S rows; S = 1 plain decode, S > 1 spec verify with num_accepted_tokens).  conv_state
+B sequences of S <= 16 tokens (T = B * S rows).  With num_accepted_tokens it is a spec verify; without, every token
+is decoded in order and the final state written back (S = 1 is plain decode; the reference serves S > 1 through its
+fallback path, kda/mi350x/kda/decode/kernel_v13_a.py:746-750, and so does this kernel directly).  conv_state
 and ssm_state are updated in place and may be strided views into one paged byte pool (the slot stride is honoured,
 rows must be dense).  Slot rows <= 0 are padding (zero output rows, nothing written).  `out` is written and returned.
 
@@ -61,9 +63,6 @@ def decode(mixed_qkv, conv_state, conv_weight, gate, beta, out_gate, A_log, dt_b
     S = T // B
     if S > MAX_S:
         raise ValueError(f"kda355 decode: S = {S} tokens per sequence exceeds {MAX_S}")
-    if not spec and S != 1:
-        raise ValueError(f"kda355 decode: plain decode takes one token per sequence (S = {S}); pass "
-                         "num_accepted_tokens for a spec verify")
     taps = (2 + S) if spec else 3
     _chk("mixed_qkv", mixed_qkv, torch.bfloat16, (T, 3 * dim), dev, True)
     if conv_state.dim() != 3 or conv_state.shape[1] < taps or conv_state.shape[2] != 3 * dim:

@@ -179,6 +179,11 @@ def test_plain_decode_extra_taps(oracle):
     _run(oracle, B=4, S=1, H=2, seed=4, spec=False, extra_taps=2)
 
 
+def test_plain_multi_token(oracle):
+    """Several tokens per sequence without num_accepted_tokens: decoded in order, final state and last 3 inputs kept."""
+    _run(oracle, B=4, S=3, H=2, seed=11, spec=False)
+
+
 def test_spec_verify_pages(oracle):
     _run(oracle, B=8, S=4, H=4, seed=5, spec=True)
 
