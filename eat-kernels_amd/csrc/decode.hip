@@ -100,42 +100,50 @@ __global__ void __launch_bounds__(DC_THREADS) decode_kernel(DecParams p) {
         const int64_t col = (int64_t)(c8 / D) * dim + h * D + c8 % D;
         return (r < 3) ? crow + (int64_t)(start + r) * p.conv_ts + col : p.x + ((int64_t)n * S + (r - 3)) * p.x_rs + col;
     };
-    u32x4 wp0 = {0u, 0u, 0u, 0u}, wp1 = {0u, 0u, 0u, 0u};
-    if (tid < npieces) wp0 = *reinterpret_cast<const u32x4*>(piece_src(tid));
-    if (tid + DC_THREADS < npieces) wp1 = *reinterpret_cast<const u32x4*>(piece_src(tid + DC_THREADS));
+    // loads are unconditional (indices clamped): a load under a divergent branch makes the compiler wait for it
+    // (vmcnt(0)) before the state loads are even issued
+    const u32x4 wp0 = *reinterpret_cast<const u32x4*>(piece_src(min(tid, npieces - 1)));
+    const u32x4 wp1 = *reinterpret_cast<const u32x4*>(piece_src(min(tid + DC_THREADS, npieces - 1)));
     // conv weights: 4 taps x 384 channels = 384 quads; quad i -> tap i / 96, channels 4 (i % 96) .. + 3
-    f32x4 cwq = {0.f, 0.f, 0.f, 0.f};
-    const int cw_tap = tid / (DC_CH / 4), cw_c = (tid % (DC_CH / 4)) * 4;
-    if (tid < DC_CH) cwq = *reinterpret_cast<const f32x4*>(p.cw + ((int64_t)(cw_c / D) * 4 + cw_tap) * dim + h * D + cw_c % D);
-    struct Ops { u32x2 g; float beta; };
-    auto load_ops = [&](int t) {
-        Ops o;
-        const int64_t tok = (int64_t)n * S + t;
-        o.g = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(row_rsrc(p.gate + tok * p.gate_rs + h * D, D * 2),
-                                                                            8 * wk.c, 0, 0));
-        o.beta = sigmoidf_(bf2f(p.beta[tok * p.beta_rs + h]));
-        return o;
+    const int cw_i = min(tid, DC_CH - 1);
+    const int cw_tap = cw_i / (DC_CH / 4), cw_c = (cw_i % (DC_CH / 4)) * 4;
+    const f32x4 cwq = *reinterpret_cast<const f32x4*>(p.cw + ((int64_t)(cw_c / D) * 4 + cw_tap) * dim + h * D + cw_c % D);
+    // per-token scalars, lane t of each wave holding token t's (read back with readlane in the walk): the raw beta
+    // and, in spec, the write row idx[n, t]
+    const int lt = min(tid & 63, S - 1);
+    const uint32_t beta_l = p.beta[((int64_t)n * S + lt) * p.beta_rs + h];
+    const int32_t wr_l = SPEC ? p.idx[(int64_t)n * S + lt] : 0;
+    auto load_gate = [&](int t) {
+        return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(
+                                             row_rsrc(p.gate + ((int64_t)n * S + t) * p.gate_rs + h * D, D * 2), 8 * wk.c, 0, 0));
     };
-    Ops op = load_ops(0);
+    u32x2 g_next = load_gate(0);
     // out_gate of the outputs this thread finishes after the walk: element i = tid + 512 k (token i / 128, row i % 128)
-    constexpr int OG_PER = (DC_MAX_S * D) / DC_THREADS;
+    constexpr int OG_PER = SINGLE ? 1 : (DC_MAX_S * D) / DC_THREADS;
     uint32_t ogv[OG_PER];
 #pragma unroll
     for (int k = 0; k < OG_PER; ++k) {
-        const int i = tid + k * DC_THREADS;
-        ogv[k] = i < S * D ? __builtin_amdgcn_raw_buffer_load_b16(
-                                 row_rsrc(p.og + ((int64_t)n * S + (i >> 7)) * p.og_rs + h * D, D * 2), 2 * (i & 127), 0, 0)
-                           : 0u;
+        const int i = min(tid + k * DC_THREADS, S * D - 1);
+        ogv[k] = __builtin_amdgcn_raw_buffer_load_b16(row_rsrc(p.og + ((int64_t)n * S + (i >> 7)) * p.og_rs + h * D, D * 2),
+                                                      2 * (i & 127), 0, 0);
     }
-    f32x4 st[8];
-    load_state(wk, p.ssm + rd * p.ssm_ss + (int64_t)h * D * D, st);
+    const float nw = p.nw[tid & (D - 1)];
     const float A = __expf(p.A_log[h]);
     const f32x4 db = *reinterpret_cast<const f32x4*>(p.dt_bias + h * D + c0);
-    const float nw = p.nw[tid & (D - 1)];
+    asm volatile("" ::: "memory");  // keep the loads above ahead of the state loads (completion is in issue order)
+    f32x4 st[8];
+    load_state(wk, p.ssm + rd * p.ssm_ss + (int64_t)h * D * D, st);
 
-    if (tid < npieces) *reinterpret_cast<u32x4*>(&sWin[tid * 8]) = wp0;
-    if (tid + DC_THREADS < npieces) *reinterpret_cast<u32x4*>(&sWin[(tid + DC_THREADS) * 8]) = wp1;
-    if (tid < DC_CH) *reinterpret_cast<f32x4*>(&sCw[cw_tap * DC_CH + cw_c]) = cwq;
+    // unconditional: threads past the end rewrite the last piece / quad with the same data
+    *reinterpret_cast<u32x4*>(&sWin[min(tid, npieces - 1) * 8]) = wp0;
+    *reinterpret_cast<u32x4*>(&sWin[min(tid + DC_THREADS, npieces - 1) * 8]) = wp1;
+    *reinterpret_cast<f32x4*>(&sCw[cw_tap * DC_CH + cw_c]) = cwq;
+    // nw * sigmoid(out_gate) of this thread's outputs, formed now: these loads are older than the state loads, and
+    // consuming them here keeps the epilogue from waiting on the state stores
+    float ogw[OG_PER];
+#pragma unroll
+    for (int k = 0; k < OG_PER; ++k) ogw[k] = nw * sigmoidf_(bf2f(ogv[k]));
+    const float dbA[4] = {A * db.x, A * db.y, A * db.z, A * db.w};  // gate = lb sigmoid(A gate + A dt_bias)
     lds_barrier();
     // ---- conv + SiLU for every token; conv cache commit
 #pragma unroll 1
@@ -158,10 +166,11 @@ __global__ void __launch_bounds__(DC_THREADS) decode_kernel(DecParams p) {
         }
     }
     lds_barrier();  // sX complete
+    if (!SINGLE) state_ready(st);
 
     for (int t = 0; t < S; ++t) {
-        const Ops cur = op;
-        if (t + 1 < S) op = load_ops(t + 1);
+        const u32x2 gcur = g_next;
+        g_next = load_gate(min(t + 1, S - 1));  // unconditional, issued before this token's state stores
         const float* xq = sX + t * DC_CH;
         const f32x4 q4 = *reinterpret_cast<const f32x4*>(xq + c0);
         const f32x4 k4 = *reinterpret_cast<const f32x4*>(xq + D + c0);
@@ -169,22 +178,23 @@ __global__ void __launch_bounds__(DC_THREADS) decode_kernel(DecParams p) {
         float kk[4] = {k4.x, k4.y, k4.z, k4.w};
         float dd[4];
         {
-            const float rg[4] = {bf2f(cur.g.x & 0xffffu), bf2f(cur.g.x >> 16), bf2f(cur.g.y & 0xffffu), bf2f(cur.g.y >> 16)};
-            const float d4[4] = {db.x, db.y, db.z, db.w};
+            const float rg[4] = {bf2f(gcur.x & 0xffffu), bf2f(gcur.x >> 16), bf2f(gcur.y & 0xffffu), bf2f(gcur.y >> 16)};
 #pragma unroll
-            for (int c = 0; c < 4; ++c) dd[c] = __expf(p.lb * sigmoidf_(A * (rg[c] + d4[c])));
+            for (int c = 0; c < 4; ++c) dd[c] = __expf(p.lb * sigmoidf_(A * rg[c] + dbA[c]));
         }
         rsqrt_norm4(kk);  // x * rsqrt(sum x^2 + 1e-6)  (kda/mi350x/reference.py:159-160)
         rsqrt_norm4(qq);
-        const float o = walk_token(st, kk, qq, dd, xq[2 * D + v_src_row(wk)], cur.beta, p.scale, wk.c);
+        const float bt = sigmoidf_(bf2f(__builtin_amdgcn_readlane(beta_l, t) & 0xffffu));
+        const float o = walk_token(st, kk, qq, dd, xq[2 * D + v_src_row(wk)], bt, p.scale, wk.c);
         // bf16(o) of the lane's row and the half wave's sum of squares (lanes c < 8 hold the half's 8 rows)
         const float ob = bf2f(f2bf(o));
         const float ss = sum32(wk.c < 8 ? ob * ob : 0.f);
         if (wk.c < 8) sO[t * D + wk.row(wk.c)] = ob;
         if (wk.c == 0) sRed[t * 16 + 2 * wk.w + wk.half] = ss;
         if (SPEC) {
-            const int64_t wr = p.idx[(int64_t)n * S + t];
-            if (slot_ok(wr, 1, p.ssm_slots)) store_state(wk, p.ssm + wr * p.ssm_ss + (int64_t)h * D * D, st);
+            const int64_t wr = __builtin_amdgcn_readlane(wr_l, t);
+            const bool ok = slot_ok(wr, 1, p.ssm_slots);
+            store_state(wk, p.ssm + (ok ? wr : 0) * p.ssm_ss + (int64_t)h * D * D, st, ok);
         }
     }
     if (!SPEC) store_state(wk, p.ssm + rd * p.ssm_ss + (int64_t)h * D * D, st);
@@ -198,7 +208,7 @@ __global__ void __launch_bounds__(DC_THREADS) decode_kernel(DecParams p) {
             const f32x4* r4 = reinterpret_cast<const f32x4*>(sRed + t * 16);
             const f32x4 s4 = (r4[0] + r4[1]) + (r4[2] + r4[3]);
             const float rstd = __frsqrt_rn((s4.x + s4.y + s4.z + s4.w) * (1.f / D) + p.eps);
-            const float y = sO[i] * rstd * nw * sigmoidf_(bf2f(ogv[k]));
+            const float y = sO[i] * rstd * ogw[k];
             __builtin_amdgcn_raw_buffer_store_b16((unsigned short)f2bf(y),
                                                   row_rsrc(p.out + ((int64_t)n * S + t) * p.out_rs + h * D, D * 2),
                                                   2 * (i & 127), 0, 0);

@@ -75,7 +75,12 @@ __global__ void __launch_bounds__(REC_THREADS) recurrent_kernel(RecParams p) {
     // stores and token 0's before the state loads: vector memory completes in order, so an operand never waits
     // behind a state transfer issued after it.
     const Walker wk(tid);
-    struct Ops { u32x2 k, q, g2; f32x4 g4; uint32_t v; float beta; };
+    // raw beta and (per-token writes) the write row of token t, held by lane t of each wave, read back with readlane
+    const int lt = min(tid & 63, S - 1);
+    const uint32_t beta_l = RAW_BETA ? (uint32_t)reinterpret_cast<const uint16_t*>(p.beta)[((int64_t)n * S + lt) * p.beta_rs + h]
+                                     : __float_as_uint(reinterpret_cast<const float*>(p.beta)[((int64_t)n * S + lt) * p.beta_rs + h]);
+    const int32_t wr_l = PER_TOKEN ? p.write_idx[(int64_t)n * S + lt] : 0;
+    struct Ops { u32x2 k, q, g2; f32x4 g4; uint32_t v; };
     auto load_ops = [&](int t) {
         Ops o;
         const int64_t tok = (int64_t)n * S + t;
@@ -89,10 +94,6 @@ __global__ void __launch_bounds__(REC_THREADS) recurrent_kernel(RecParams p) {
         else
             o.g4 = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
                 row_rsrc(reinterpret_cast<const float*>(p.g) + tok * p.g_rs + h * D, D * 4), 16 * wk.c, 0, 0));
-        if (RAW_BETA)
-            o.beta = sigmoidf_(bf2f(reinterpret_cast<const uint16_t*>(p.beta)[tok * p.beta_rs + h]));
-        else
-            o.beta = reinterpret_cast<const float*>(p.beta)[tok * p.beta_rs + h];
         return o;
     };
     Ops op = load_ops(0);
@@ -106,10 +107,13 @@ __global__ void __launch_bounds__(REC_THREADS) recurrent_kernel(RecParams p) {
         db[0] = d4.x; db[1] = d4.y; db[2] = d4.z; db[3] = d4.w;
     }
 
+    if (MODE != REC_SINGLE) state_ready(st);
     for (int t = 0; t < S; ++t) {
         const int64_t tok = (int64_t)n * S + t;
         const Ops cur = op;
-        if (t + 1 < S) op = load_ops(t + 1);
+        if (MODE != REC_SINGLE) op = load_ops(min(t + 1, S - 1));  // unconditional, issued before this token's stores
+        const uint32_t braw = __builtin_amdgcn_readlane(beta_l, t);
+        const float bt = RAW_BETA ? sigmoidf_(bf2f(braw & 0xffffu)) : __uint_as_float(braw);
         float kk[4] = {bf2f(cur.k.x & 0xffffu), bf2f(cur.k.x >> 16), bf2f(cur.k.y & 0xffffu), bf2f(cur.k.y >> 16)};
         float qq[4] = {bf2f(cur.q.x & 0xffffu), bf2f(cur.q.x >> 16), bf2f(cur.q.y & 0xffffu), bf2f(cur.q.y >> 16)};
         float dd[4];
@@ -125,14 +129,15 @@ __global__ void __launch_bounds__(REC_THREADS) recurrent_kernel(RecParams p) {
             rsqrt_norm4(kk);
             rsqrt_norm4(qq);
         }
-        const float o = walk_token(st, kk, qq, dd, bf2f(cur.v), cur.beta, p.scale, wk.c);
+        const float o = walk_token(st, kk, qq, dd, bf2f(cur.v), bt, p.scale, wk.c);
         // output: lane c < 8 of each half wave writes row 16 c + 2 w + half
         if (wk.c < 8)
             __builtin_amdgcn_raw_buffer_store_b16((unsigned short)f2bf(o), row_rsrc(p.out + tok * p.out_rs + h * D, D * 2),
                                                   2 * wk.row(wk.c), 0, 0);
         if (PER_TOKEN) {
-            const int64_t wr = p.write_idx[(int64_t)n * S + t];
-            if (row_ok(wr, p.write_min, p.write_slots)) store_state(wk, p.write_pool + wr * p.write_ss + (int64_t)h * D * D, st);
+            const int64_t wr = __builtin_amdgcn_readlane(wr_l, t);
+            const bool ok = row_ok(wr, p.write_min, p.write_slots);
+            store_state(wk, p.write_pool + (ok ? wr : 0) * p.write_ss + (int64_t)h * D * D, st, ok);
         }
     }
     if (!PER_TOKEN) store_state(wk, p.read_pool + rd * p.read_ss + (int64_t)h * D * D, st);

@@ -61,8 +61,19 @@ __device__ __forceinline__ void load_state(const Walker& wk, const float* base, 
         st[p] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, wk.voff(), p * WK_ROW_STEP, WK_LOAD_AUX));
 }
 
-__device__ __forceinline__ void store_state(const Walker& wk, float* base, const f32x4 (&st)[8]) {
-    const __amdgpu_buffer_rsrc_t rs = state_rsrc(base);
+// Wait for the state loads here rather than at the state's first use inside a token loop: the compiler's wait
+// there would also run on every later iteration, where it drains that iteration's predecessor's state stores.
+__device__ __forceinline__ void state_ready(f32x4 (&st)[8]) {
+#pragma unroll
+    for (int p = 0; p < 8; ++p) asm volatile("" : "+v"(st[p]));
+}
+
+// valid = false stores nothing: the descriptor then covers 0 bytes and the hardware drops out-of-range buffer
+// stores.  Keeping the store instructions unconditional keeps the compiler's memory-counter waits exact (a store
+// under a branch makes it wait for every older access on the path without it).
+__device__ __forceinline__ void store_state(const Walker& wk, float* base, const f32x4 (&st)[8], bool valid = true) {
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(base), (short)0, valid ? D * D * 4 : 0, 0x00020000);
 #pragma unroll
     for (int p = 0; p < 8; ++p)
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, st[p]), rs, wk.voff(), p * WK_ROW_STEP,
