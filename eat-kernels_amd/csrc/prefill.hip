@@ -18,9 +18,9 @@
 //       and the per-channel block factors (a, b, x, y, decay) -- two exponentials per element
 //   P4  Gram tiles on MFMA: the four diagonal 16 x 16 blocks from bf16 hi + lo operands (3 MFMAs: hi.hi + hi.lo +
 //       lo.hi; their gated operands span e^{+-8|g|}), the six off-diagonal blocks from fp16 operands <= 1 (the
-//       reference point is the last row before the row block)
-//   P5  diagonal-block inverses (I + L_II)^-1 by forward substitution (fp32); Q e^Gamma, K e^{Gamma_c - Gamma}
-//       and beta V to LDS in the walk's operand layouts
+//       reference point is the last row before the row block); each diagonal wave then inverts its block,
+//       (I + L_II)^-1 by forward substitution in fp32, while the off-diagonal waves finish
+//   P5  Q e^Gamma, K e^{Gamma_c - Gamma} and beta V to LDS in the walk's operand layouts
 //   P6  W and U by block forward substitution on MFMA: X_I = T_II (B_I - sum_{J<I} A_IJ X_J); wave w owns key
 //       channels [16w, 16w+16) of W and value columns [16w, 16w+16) of U, so no wave waits for another
 //   P7  the walk: wave w keeps the 128 x 16 slice S[:, 16w:16w+16] in fp32 registers (MFMA C layout) for the whole
@@ -510,6 +510,30 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
                 sAq[rw * RS16S + pos64(16 * I + m)] = (half_t)((m <= rr) ? aqk[e] : 0.f);
             }
             *reinterpret_cast<f32x4*>(&sL[(I * 16 + m) * 20 + 4 * g]) = lt;
+            // T_II = (I + L_II)^-1 of this wave's block while waves 4..7 still work on the off-diagonal blocks: lane j
+            // (every group of 16 lanes computes the same columns; lanes 0..15 write) solves column j by right-looking
+            // substitution.  The wave reads back the block it has just written: a wave's LDS operations complete in order.
+            {
+                const float* Lb = sL + I * 16 * 20;  // column k of L_II is the contiguous row k
+                float x[16];
+#pragma unroll
+                for (int ii = 0; ii < 16; ++ii) x[ii] = (ii == m) ? 1.f : 0.f;
+#pragma unroll
+                for (int k = 0; k < 15; ++k) {  // x[k] is final: push it into the rows below
+                    float col[16];
+#pragma unroll
+                    for (int q4 = 0; q4 < 4; ++q4) {
+                        const f32x4 c4 = *reinterpret_cast<const f32x4*>(&Lb[k * 20 + 4 * q4]);
+                        col[4 * q4] = c4[0]; col[4 * q4 + 1] = c4[1]; col[4 * q4 + 2] = c4[2]; col[4 * q4 + 3] = c4[3];
+                    }
+#pragma unroll
+                    for (int ii = k + 1; ii < 16; ++ii) x[ii] -= col[ii] * x[k];
+                }
+                if (g == 0) {
+#pragma unroll
+                    for (int ii = 0; ii < 16; ++ii) sAk[(16 * I + ii) * RS16S + 16 * I + m] = (half_t)x[ii];
+                }
+            }
         } else {
             const int I = (w == 4) ? 1 : ((w == 5) ? 2 : 3);
             const int J0 = (w == 7) ? 2 : 0;
@@ -565,7 +589,7 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
             }
         }
         lds_barrier();
-        // ================= P5: T_II (wave 0); Q~, Kd^T, beta v into their walk layouts (raw threads)
+        // ================= P5: Q~, Kd^T, beta v into their walk layouts (raw threads)
         // the next chunk's rows: issued here, consumed at the next P0 (their registers are free during P1..P4)
         if (cl + 1 < nch) load_row<RG>(p, h, t0 + 64, min(64, len - 64 * (cl + 1)), r, cb, RB, nx);
         float qfi[16], kfj[16], vf[16];
@@ -582,26 +606,6 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
             for (int j = 0; j < 4; ++j) { qfi[4 * i + j] = a[j]; kfj[4 * i + j] = b[j]; }
         }
         lds_barrier();  // regions B and C are rewritten below
-        if (w == 0) {  // T_II = (I + L_II)^-1, lane (block I, column j); overlaps the layout writes of the other waves
-            const int I = lane >> 4, j = lane & 15;
-            const float* Lb = sL + I * 16 * 20;  // column k of L_II is the contiguous row k
-            float x[16];
-#pragma unroll
-            for (int ii = 0; ii < 16; ++ii) x[ii] = (ii == j) ? 1.f : 0.f;
-#pragma unroll
-            for (int k = 0; k < 15; ++k) {  // right-looking: x[k] is final, push it into the rows below
-                float col[16];
-#pragma unroll
-                for (int q4 = 0; q4 < 4; ++q4) {
-                    const f32x4 c4 = *reinterpret_cast<const f32x4*>(&Lb[k * 20 + 4 * q4]);
-                    col[4 * q4] = c4[0]; col[4 * q4 + 1] = c4[1]; col[4 * q4 + 2] = c4[2]; col[4 * q4 + 3] = c4[3];
-                }
-#pragma unroll
-                for (int ii = k + 1; ii < 16; ++ii) x[ii] -= col[ii] * x[k];
-            }
-#pragma unroll
-            for (int ii = 0; ii < 16; ++ii) sAk[(16 * I + ii) * RS16S + 16 * I + j] = (half_t)x[ii];
-        }
         {
             const int I = r >> 4;
             const int hb = cb & 1, blk = cb >> 1;
