@@ -97,6 +97,11 @@ __device__ __forceinline__ f32x4 mfma16(f16x4 a, f16x4 b, f32x4 c) {
 // storage position of index q (0..31) inside a permuted 32-block: q = 16h + 4g + e  ->  8g + 4h + e
 __device__ __forceinline__ int pos32(int q) { return ((q >> 2) & 3) * 8 + ((q >> 4) << 2) + (q & 3); }
 __device__ __forceinline__ int pos64(int q) { return (q & 32) + pos32(q & 31); }
+// Channel swizzle of the fp32 row arrays (gate / Gamma, q^ fi, k^ fi, k^ fj; 132-float rows): logical channel c is
+// stored at c ^ (((c >> 5) & 3) << 2), i.e. the four 16-byte slots of the 16-channel segment of raw thread cb are
+// permuted by slot ^= cb >> 1.  The eight raw threads of a row then write 16-byte slots on distinct banks (unswizzled,
+// segments cb and cb + 4 sit 256 bytes apart and their writes conflict: 128 vs 55 cycles per wave instruction).
+__device__ __forceinline__ int swz(int c) { return c ^ (((c >> 5) & 3) << 2); }
 // 2^x (v_exp_f32)
 __device__ __forceinline__ float exp2_(float x) { return __builtin_amdgcn_exp2f(x); }
 
@@ -333,10 +338,11 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
         // The raw q, k, v go to LDS slots that only this thread reads back and later overwrites (q: first half of its
         // q^ fi slot in region B, k: of its k^ fj slot in region C, v: the W area, which is free until P6), so the
         // registers die here and the next chunk's loads reuse them without a loop-carried copy.
-        *reinterpret_cast<u32x4*>(lds + LDS_B + r * (4 * RS32) + 64 * cb) = nx.q[0];
-        *reinterpret_cast<u32x4*>(lds + LDS_B + r * (4 * RS32) + 64 * cb + 16) = nx.q[1];
-        *reinterpret_cast<u32x4*>(lds + LDS_C + r * (4 * RS32) + 64 * cb) = nx.k[0];
-        *reinterpret_cast<u32x4*>(lds + LDS_C + r * (4 * RS32) + 64 * cb + 16) = nx.k[1];
+        const int sl0 = 16 * (cb >> 1), sl1 = 16 * (1 ^ (cb >> 1));  // swizzled slots 0 and 1 of the segment
+        *reinterpret_cast<u32x4*>(lds + LDS_B + r * (4 * RS32) + 64 * cb + sl0) = nx.q[0];
+        *reinterpret_cast<u32x4*>(lds + LDS_B + r * (4 * RS32) + 64 * cb + sl1) = nx.q[1];
+        *reinterpret_cast<u32x4*>(lds + LDS_C + r * (4 * RS32) + 64 * cb + sl0) = nx.k[0];
+        *reinterpret_cast<u32x4*>(lds + LDS_C + r * (4 * RS32) + 64 * cb + sl1) = nx.k[1];
         *reinterpret_cast<u32x4*>(lds + LDS_W + r * (2 * RS16) + 32 * cb) = nx.v[0];
         *reinterpret_cast<u32x4*>(lds + LDS_W + r * (2 * RS16) + 32 * cb + 16) = nx.v[1];
         float gv[16];
@@ -378,7 +384,7 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
         const u32x4 o1 = *reinterpret_cast<const u32x4*>(lds + r * 528 + 64 * cb + 16);
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-            *reinterpret_cast<f32x4*>(&sG[r * RS32 + 16 * cb + 4 * i]) =
+            *reinterpret_cast<f32x4*>(&sG[r * RS32 + 16 * cb + 4 * (i ^ (cb >> 1))]) =
                 f32x4{gv[4 * i], gv[4 * i + 1], gv[4 * i + 2], gv[4 * i + 3]};
         if (cb == 0) sBeta[r] = bt;
         if (!P1 && cl > 0) {  // the previous chunk was a full one
@@ -392,11 +398,11 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
             const int c = tid & 127, s = tid >> 7;
             float x[16];
 #pragma unroll
-            for (int i = 0; i < 16; ++i) x[i] = sG[(16 * s + i) * RS32 + c];
+            for (int i = 0; i < 16; ++i) x[i] = sG[(16 * s + i) * RS32 + swz(c)];
 #pragma unroll
             for (int i = 1; i < 16; ++i) x[i] += x[i - 1];
 #pragma unroll
-            for (int i = 0; i < 16; ++i) sG[(16 * s + i) * RS32 + c] = x[i];
+            for (int i = 0; i < 16; ++i) sG[(16 * s + i) * RS32 + swz(c)] = x[i];
             sWt[s * 128 + c] = x[15];
         }
         lds_barrier();
@@ -405,17 +411,19 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
         {
             float qf[16], kf[16], qfi[16], kfj[16];
             {
-                const u32x4* qs = reinterpret_cast<const u32x4*>(lds + LDS_B + r * (4 * RS32) + 64 * cb);
-                const u32x4* ks = reinterpret_cast<const u32x4*>(lds + LDS_C + r * (4 * RS32) + 64 * cb);
-                const u32x4 a[2] = {qs[0], qs[1]}, b[2] = {ks[0], ks[1]};
+                const unsigned char* qs = lds + LDS_B + r * (4 * RS32) + 64 * cb;
+                const unsigned char* ks = lds + LDS_C + r * (4 * RS32) + 64 * cb;
+                const int sl0 = 16 * (cb >> 1), sl1 = 16 * (1 ^ (cb >> 1));
+                const u32x4 a[2] = {*reinterpret_cast<const u32x4*>(qs + sl0), *reinterpret_cast<const u32x4*>(qs + sl1)};
+                const u32x4 b[2] = {*reinterpret_cast<const u32x4*>(ks + sl0), *reinterpret_cast<const u32x4*>(ks + sl1)};
                 unpack16(a, qf);
                 unpack16(b, kf);
             }
             const int I = r >> 4, mr = 16 * I + 7;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const f32x4 a = *reinterpret_cast<const f32x4*>(&sG[r * RS32 + 16 * cb + 4 * i]);
-                const f32x4 b = *reinterpret_cast<const f32x4*>(&sG[mr * RS32 + 16 * cb + 4 * i]);
+                const f32x4 a = *reinterpret_cast<const f32x4*>(&sG[r * RS32 + 16 * cb + 4 * (i ^ (cb >> 1))]);
+                const f32x4 b = *reinterpret_cast<const f32x4*>(&sG[mr * RS32 + 16 * cb + 4 * (i ^ (cb >> 1))]);
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     const int c = 4 * i + j;
@@ -429,9 +437,9 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
             }
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                *reinterpret_cast<f32x4*>(&sQA[r * RS32 + 16 * cb + 4 * i]) =
+                *reinterpret_cast<f32x4*>(&sQA[r * RS32 + 16 * cb + 4 * (i ^ (cb >> 1))]) =
                     f32x4{qfi[4 * i], qfi[4 * i + 1], qfi[4 * i + 2], qfi[4 * i + 3]};
-                *reinterpret_cast<f32x4*>(&sKB[r * RS32 + 16 * cb + 4 * i]) =
+                *reinterpret_cast<f32x4*>(&sKB[r * RS32 + 16 * cb + 4 * (i ^ (cb >> 1))]) =
                     f32x4{kfj[4 * i], kfj[4 * i + 1], kfj[4 * i + 2], kfj[4 * i + 3]};
             }
         }
@@ -442,7 +450,7 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 const float off = (i < 2) ? 0.f : (i < 4) ? o1 : (i < 6) ? o2 : o3;
-                gr[i] = sG[(8 * i + 7) * RS32 + c] + off;
+                gr[i] = sG[(8 * i + 7) * RS32 + swz(c)] + off;
             }
 #pragma unroll
             for (int f = 0; f < F_ROWS; ++f) {  // unrolled: gr[] is indexed by constants only (stays in registers)
@@ -470,7 +478,7 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
         // ================= P3: k^ fi over the (now unused) gate rows
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-            *reinterpret_cast<f32x4*>(&sKA[r * RS32 + 16 * cb + 4 * i]) =
+            *reinterpret_cast<f32x4*>(&sKA[r * RS32 + 16 * cb + 4 * (i ^ (cb >> 1))]) =
                 f32x4{kfi[4 * i], kfi[4 * i + 1], kfi[4 * i + 2], kfi[4 * i + 3]};
         lds_barrier();
         // ================= P4: Gram tiles
@@ -483,9 +491,9 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
                 bf16x8 kah, kal, qah, qal, kbh, kbl;
 #pragma unroll
                 for (int hf = 0; hf < 2; ++hf) {
-                    const f32x4 ka = *reinterpret_cast<const f32x4*>(&sKA[i * RS32 + c0 + 4 * hf]);
-                    const f32x4 qa = *reinterpret_cast<const f32x4*>(&sQA[i * RS32 + c0 + 4 * hf]);
-                    const f32x4 kb = *reinterpret_cast<const f32x4*>(&sKB[i * RS32 + c0 + 4 * hf]);
+                    const f32x4 ka = *reinterpret_cast<const f32x4*>(&sKA[i * RS32 + swz(c0 + 4 * hf)]);
+                    const f32x4 qa = *reinterpret_cast<const f32x4*>(&sQA[i * RS32 + swz(c0 + 4 * hf)]);
+                    const f32x4 kb = *reinterpret_cast<const f32x4*>(&sKB[i * RS32 + swz(c0 + 4 * hf)]);
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
                         const int e = 4 * hf + j;
@@ -548,8 +556,8 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
                 f16x8 ka, qa;
 #pragma unroll
                 for (int hf = 0; hf < 2; ++hf) {
-                    const f32x4 a = *reinterpret_cast<const f32x4*>(&sKA[i * RS32 + c0 + 4 * hf]);
-                    const f32x4 q4 = *reinterpret_cast<const f32x4*>(&sQA[i * RS32 + c0 + 4 * hf]);
+                    const f32x4 a = *reinterpret_cast<const f32x4*>(&sKA[i * RS32 + swz(c0 + 4 * hf)]);
+                    const f32x4 q4 = *reinterpret_cast<const f32x4*>(&sQA[i * RS32 + swz(c0 + 4 * hf)]);
                     const f32x4 fa = *reinterpret_cast<const f32x4*>(&sF[(F_A + I - 1) * 128 + c0 + 4 * hf]);
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
@@ -565,7 +573,7 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
                         f16x8 kb;
 #pragma unroll
                         for (int hf = 0; hf < 2; ++hf) {
-                            const f32x4 b = *reinterpret_cast<const f32x4*>(&sKB[jr * RS32 + c0 + 4 * hf]);
+                            const f32x4 b = *reinterpret_cast<const f32x4*>(&sKB[jr * RS32 + swz(c0 + 4 * hf)]);
                             const f32x4 fbv = *reinterpret_cast<const f32x4*>(&sF[fb * 128 + c0 + 4 * hf]);
 #pragma unroll
                             for (int j = 0; j < 4; ++j) kb[4 * hf + j] = (half_t)(b[j] * fbv[j]);
@@ -600,8 +608,8 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const f32x4 a = *reinterpret_cast<const f32x4*>(&sQA[r * RS32 + 16 * cb + 4 * i]);
-            const f32x4 b = *reinterpret_cast<const f32x4*>(&sKB[r * RS32 + 16 * cb + 4 * i]);
+            const f32x4 a = *reinterpret_cast<const f32x4*>(&sQA[r * RS32 + 16 * cb + 4 * (i ^ (cb >> 1))]);
+            const f32x4 b = *reinterpret_cast<const f32x4*>(&sKB[r * RS32 + 16 * cb + 4 * (i ^ (cb >> 1))]);
 #pragma unroll
             for (int j = 0; j < 4; ++j) { qfi[4 * i + j] = a[j]; kfj[4 * i + j] = b[j]; }
         }
@@ -647,7 +655,7 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const int rw = 16 * I + 4 * g + e;
-                    aw[e] = sBeta[rw] * sKA[rw * RS32 + c] * xI;
+                    aw[e] = sBeta[rw] * sKA[rw * RS32 + swz(c)] * xI;
                     au[e] = (float)sBV[rw * RS16 + c];
                 }
 #pragma unroll
