@@ -506,17 +506,19 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
                 akk = mfma32bf(kah, kbh, akk);
                 akk = mfma32bf(kah, kbl, akk);
                 akk = mfma32bf(kal, kbh, akk);
-                aqk = mfma32bf(qah, kbh, aqk);
-                aqk = mfma32bf(qah, kbl, aqk);
-                aqk = mfma32bf(qal, kbh, aqk);
+                aqk = mfma32bf(kbh, qah, aqk);  // transposed: lane (g, m) holds row 16 I + m, columns 16 I + 4 g .. + 3
+                aqk = mfma32bf(kbl, qah, aqk);
+                aqk = mfma32bf(kbh, qal, aqk);
             }
             f32x4 lt;
+            f16x4 aq;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int rr = 4 * g + e, rw = 16 * I + rr;
                 lt[e] = (m < rr) ? sBeta[rw] * akk[e] : 0.f;
-                sAq[rw * RS16S + pos64(16 * I + m)] = (half_t)((m <= rr) ? aqk[e] : 0.f);
+                aq[e] = (half_t)((rr <= m) ? aqk[e] : 0.f);  // A_qk[16 I + m][16 I + rr], causal within the block
             }
+            *reinterpret_cast<f16x4*>(&sAq[i * RS16S + pos64(16 * I + 4 * g)]) = aq;
             *reinterpret_cast<f32x4*>(&sL[(I * 16 + m) * 20 + 4 * g]) = lt;
             // T_II = (I + L_II)^-1 of this wave's block while waves 4..7 still work on the off-diagonal blocks: lane j
             // (every group of 16 lanes computes the same columns; lanes 0..15 write) solves column j by right-looking
@@ -578,21 +580,21 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
 #pragma unroll
                             for (int j = 0; j < 4; ++j) kb[4 * hf + j] = (half_t)(b[j] * fbv[j]);
                         }
-                        akk[t] = mfma32(ka, kb, akk[t]);
-                        aqk[t] = mfma32(qa, kb, aqk[t]);
+                        akk[t] = mfma32(kb, ka, akk[t]);  // transposed tiles: lane (g, m) holds row 16 I + m,
+                        aqk[t] = mfma32(kb, qa, aqk[t]);  // columns 16 J + 4 g .. + 3
                     }
                 }
             }
+            const float nb = -sBeta[i];
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
                 if (t < nJ) {
                     const int J = J0 + t;
+                    f16x4 ak, aq;
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const int rw = 16 * I + 4 * g + e, col = 16 * J + m;
-                        sAk[rw * RS16S + col] = (half_t)(-sBeta[rw] * akk[t][e]);
-                        sAq[rw * RS16S + pos64(col)] = (half_t)aqk[t][e];
-                    }
+                    for (int e = 0; e < 4; ++e) { ak[e] = (half_t)(nb * akk[t][e]); aq[e] = (half_t)aqk[t][e]; }
+                    *reinterpret_cast<f16x4*>(&sAk[i * RS16S + 16 * J + 4 * g]) = ak;
+                    *reinterpret_cast<f16x4*>(&sAq[i * RS16S + pos64(16 * J + 4 * g)]) = aq;
                 }
             }
         }
@@ -756,22 +758,24 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
                     VB[s][e] = (half_t)Vp[2 * s][e];
                     VB[s][4 + e] = (half_t)Vp[2 * s + 1][e];
                 }
-            // O is staged in region A: token tk, value v at byte tk * 528 + 64 (v / 16) + 2 (v % 16) -- the first half of
-            // the 64-byte slot the raw thread (tk, v / 16) later fills with its gate values
-            uint16_t* sO = reinterpret_cast<uint16_t*>(lds + LDS_A) + 32 * w + m;
+            // O^T = S^T Q~^T + V'^T A_qk^T: the same fragments with the MFMA operands swapped give the transposed tile, so
+            // lane (g, m) holds token 16 it + m, values 16 w + 4 g .. + 3 and stages them with one 8-byte store.  O is
+            // staged in region A: token tk, value v at byte tk * 528 + 64 (v / 16) + 2 (v % 16) -- the first half of the
+            // 64-byte slot the raw thread (tk, v / 16) later fills with its gate values
 #pragma unroll
             for (int it = 0; it < 4; ++it) {
                 f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int s = 0; s < 4; ++s)
-                    acc = mfma32(*reinterpret_cast<const f16x8*>(&sQt[(16 * it + m) * RS16 + 32 * s + 8 * g]), SB[s], acc);
+                    acc = mfma32(SB[s], *reinterpret_cast<const f16x8*>(&sQt[(16 * it + m) * RS16 + 32 * s + 8 * g]), acc);
 #pragma unroll
                 for (int s = 0; s < 2; ++s)
                     if (s <= (it >> 1))
-                        acc = mfma32(*reinterpret_cast<const f16x8*>(&sAq[(16 * it + m) * RS16S + 32 * s + 8 * g]), VB[s],
+                        acc = mfma32(VB[s], *reinterpret_cast<const f16x8*>(&sAq[(16 * it + m) * RS16S + 32 * s + 8 * g]),
                                      acc);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) sO[(16 * it + 4 * g + e) * (2 * RS32)] = (uint16_t)f2bf(p.scale * acc[e]);
+                const u32x2 o = {f2bf(p.scale * acc[0]) | (f2bf(p.scale * acc[1]) << 16),
+                                 f2bf(p.scale * acc[2]) | (f2bf(p.scale * acc[3]) << 16)};
+                *reinterpret_cast<u32x2*>(lds + LDS_A + (16 * it + m) * (4 * RS32) + 64 * w + 8 * g) = o;
             }
 #pragma unroll
             for (int dt = 0; dt < 8; ++dt) {
