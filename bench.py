@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """KDA on one MI355X: chunked prefill throughput (the headline), recurrent decode, speculative verify, long prefill.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs c1,c3,c4,c2] [--cpu-seconds 10]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs c1,c3,c4,d1,c2] [--cpu-seconds 10]
 
 Prints ONE JSON line on stdout.  `value` is the prefill throughput of configuration 1: the
 fla `chunk_kda` plain call over 8 varlen sequences (lengths U[256, 8192] from seed 1, 38,881 tokens), H = 32,
@@ -12,6 +12,8 @@ The other configurations are reported beside it (never as `value`):
   decode       configs[3]: B = 256 x 1 token, H = 32, fp32 pool of 4096 slots, captured in a HIP graph, us/step
   spec_verify  configs[4]: B = 64 x 4 draft tokens at H = 64 and 96, pool of 1024 slots, per-token states into a
                [64*4, H, 128, 128] scratch, then the accepted length committed to the pool slot (one graph)
+  fused_decode the vLLM-contract fused decode (conv1d + SiLU, norms, recurrence, gated RMSNorm) on the vLLM page
+               layout at the configs[3] shape and at the reference's s8_h96_b32 spec-verify workload
   long_prefill configs[2]: one sequence of 131,072 tokens, H = 32, paged fp32 pool of 64 slots at a seeded slot,
                bf16 checkpoints every 4096 tokens into 32 seeded rows
 
@@ -257,6 +259,50 @@ def bench_c2(kda, torch, dev, steps, warmup):
                 mfma_frac=flops / (ms * 1e-3) / (MFMA_PEAK_TFLOPS * 1e12))
 
 
+def bench_fused_decode(kda, torch, dev, steps, warmup, H, B, S):
+    """The vLLM-contract fused decode (`kda355.decode`) on the vLLM page layout (conv state then SSM state in one page
+    per slot, pages padded; mixed_qkv / out_gate / beta as column slices of one input projection), graph replay."""
+    dim, T = H * D, B * S
+    spec = S > 1
+    taps = 2 + S if spec else 3
+    slots = 2 * B * S + 16
+    conv_bytes = taps * 3 * dim * 2
+    page = -(-(conv_bytes + H * D * D * 4 + 4096) // 256) * 256
+    gen = torch.Generator(device=dev).manual_seed(7 + H + S)
+    raw = torch.zeros(slots * page, dtype=torch.uint8, device=dev)
+    conv = torch.as_strided(raw.view(torch.bfloat16), (slots, taps, 3 * dim), (page // 2, 3 * dim, 1), 0)
+    ssm = torch.as_strided(raw.view(torch.float32), (slots, H, D, D), (page // 4, D * D, D, 1), conv_bytes // 4)
+    conv.copy_(torch.randn(conv.shape, generator=gen, device=dev).bfloat16())
+    ssm.copy_(torch.randn(ssm.shape, generator=gen, device=dev) * 0.05)
+    Wp = -(-(4 * dim + D + H) // 16) * 16
+    P = torch.randn(T, Wp, generator=gen, device=dev).bfloat16()
+    mixed, og, beta = P[:, :3 * dim], P[:, 3 * dim:4 * dim], P[:, 4 * dim + D:4 * dim + D + H]
+    gate = torch.randn(T, H, D, generator=gen, device=dev).bfloat16()
+    cw = torch.randn(3, 4, dim, generator=gen, device=dev) * 0.4
+    A_log = torch.rand(H, generator=gen, device=dev) * 2 - 1
+    dtb = torch.randn(dim, generator=gen, device=dev) * 0.5
+    nw = 1 + torch.randn(D, generator=gen, device=dev) * 0.1
+    cpu = torch.Generator().manual_seed(7 + H + S)
+    perm = (torch.randperm(slots - 1, generator=cpu)[:B * S] + 1).to(torch.int32)
+    idx = (perm.view(B, S) if spec else perm[:B]).contiguous().to(dev)
+    acc = torch.randint(1, S + 1, (B,), generator=cpu, dtype=torch.int32).to(dev) if spec else None
+    cu = torch.arange(0, T + 1, S, dtype=torch.int32, device=dev)
+    out = torch.empty(T, dim, dtype=torch.bfloat16, device=dev)
+
+    def call():
+        kda.decode(mixed, conv, cw, gate, beta, og, A_log, dtb, nw, ssm, idx, acc, cu, 1e-5, -5.0, out)
+
+    call()
+    torch.cuda.synchronize()
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr):
+        call()
+    ms, _ = time_steps(gr.replay, steps * 5, warmup * 5, torch)
+    state_bytes = B * H * D * D * 4 * (1 + S)
+    del raw, P
+    return dict(H=H, B=B, S=S, us=ms * 1e3, state_bytes=state_bytes)
+
+
 # ------------------------------------------------------------------------------------------------ CPU baseline
 def cpu_baseline(inputs, lens, seconds, torch):
     """The oracle's fp32 token recurrence (OpenMP over (sequence, head) chains) on the whole configuration-1
@@ -302,7 +348,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--configs", default="c1,c3,c4,c2")
+    ap.add_argument("--configs", default="c1,c3,c4,d1,c2")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a 1 GiB device-to-device copy 5x (the known-size kernel for HBM counter scaling)")
@@ -359,6 +405,16 @@ def main():
                          "verify_commit_GBs": round(gbs2, 1)})
             log(f"spec H={H}: verify {s['verify_us']:.1f} us ({gbs:.0f} GB/s), +commit {s['verify_commit_us']:.1f} us")
         extra["spec_verify"] = rows
+    if "d1" in cfgs:
+        rows = []
+        for H, B, S, name in ((32, 256, 1, "configs[3] shape"), (96, 32, 8, "reference workload s8_h96_b32")):
+            f = bench_fused_decode(kda355, torch, dev, args.steps, args.warmup, H, B, S)
+            gbs = f["state_bytes"] / (f["us"] * 1e-6) / 1e9
+            rows.append({"workload": name, "H": H, "B": B, "S": S, "us_per_step": round(f["us"], 2),
+                         "state_GBs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)})
+            log(f"fused decode H={H} B={B} S={S}: {f['us']:.1f} us ({gbs:.0f} GB/s state traffic)")
+        extra["fused_decode"] = {"config": "kda355.decode (vLLM contract: conv1d + SiLU, norms, gated delta rule, gated "
+                                           "RMSNorm) on the vLLM page layout, HIP graph replay", "rows": rows}
     if "c2" in cfgs:
         c2 = bench_c2(kda355, torch, dev, args.steps, args.warmup)
         extra["long_prefill"] = {"config": "configs[2]: T=131072, H=32, pool slot, bf16 checkpoints every 4096 tokens",
@@ -386,7 +442,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "algorithmic_bytes": c1["bytes"],
-                     "kernel": "prefill launch (chunk prologue + chain walk kernels)",
+                     "kernel": "chunk_kernel (fused chunk-64 prefill, one workgroup per (sequence, head))",
                      "mfma": {"achieved": round(tflops, 2), "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                               "frac": round(tflops / MFMA_PEAK_TFLOPS, 4), "flops": c1["flops"]}},
         "cpu_baseline": cpu,
