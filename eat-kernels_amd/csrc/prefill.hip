@@ -32,6 +32,7 @@
 // |x| < 65504 (state, U, T entries); the diagonal blocks need |Gamma_i - Gamma_m| < 88 over 8 tokens, i.e. a
 // per-token log-decay above ~ -11 (gate-in-kernel calls with lower_bound >= -11 always satisfy it).
 #include <algorithm>
+#include <functional>
 #include <numeric>
 #include <vector>
 
@@ -71,17 +72,26 @@ constexpr int F_DEC = 17;   // e^{Gamma_c}
 constexpr int F_ROWS = 18;
 
 constexpr uint32_t PLAN_MAGIC = 0x4b443535u;  // "KD55"
-// table header words
-// Table: header, then three lists of entries.  The final list holds every piece that produces outputs (a whole
-// sequence, or one piece of a split sequence); the transition list holds every piece of a split sequence (run first,
-// from a zero state, recording its local end state and its state transition); the scan list holds the split
-// sequences (their pieces' start states are composed between the two).
-enum { H_MAGIC = 0, H_N, H_T, H_NCHUNK, H_EVERY, H_CKROWS, H_OFF_FINAL, H_NFINAL, H_OFF_TRANS, H_NTRANS, H_OFF_SCAN,
-       H_NSCAN, H_NSLOTS, H_WORDS = 16 };
+// Table: a header, then four lists.  The chain list holds every piece run by the chunk kernel (a whole sequence, the
+// first piece of a split sequence from its true start state, or a later piece from S = 0 carrying its transition);
+// the scan list holds the split sequences (the start states of their later pieces and their final states are composed
+// after the chunk kernel); the fixup list holds one task per group of up to 8 chunks of a later piece (their outputs
+// get R S_start added); the compose list holds the checkpoints inside later pieces (row = P S_start + S_local).
+enum { H_MAGIC = 0, H_N, H_T, H_NCHUNK, H_EVERY, H_CKROWS, H_OFF_FINAL, H_NFINAL, H_OFF_FIX, H_NFIX, H_OFF_SCAN,
+       H_NSCAN, H_NSLOTS, H_OFF_CKC, H_NCKC, H_NRSLOTS, H_NCKSLOTS, H_WORDS = 20 };
 // one piece entry: chunks [0, nch) starting at sequence chunk `first` of sequence n, tokens [t_start, t_start + len)
-enum { C_SEQ = 0, C_NCH, C_TSTART, C_LEN, C_CKSINGLE, C_CKROW0, C_FIRST, C_FLAGS, C_SLOT, C_SEQCH, C_WORDS = 12 };
-enum { PIECE_READ_WS = 1, PIECE_LAST = 2 };  // C_FLAGS: start state from the workspace; the piece ends the sequence
+enum { C_SEQ = 0, C_NCH, C_TSTART, C_LEN, C_CKSINGLE, C_CKROW0, C_FIRST, C_FLAGS, C_SLOT, C_SEQCH, C_RBASE, C_CKWS,
+       C_CKWS1, C_WORDS = 13 };
+// C_FLAGS: PIECE_FIX: a non-first piece of a split sequence (runs from S = 0 carrying its transition, writes fp16
+// partial outputs and the per-chunk correction operands R); PIECE_LAST: the entry ends an unsplit sequence (writes the
+// final state); PIECE_STORE_END: the first piece of a split sequence (its end state is the second piece's start)
+enum { PIECE_FIX = 1, PIECE_LAST = 2, PIECE_STORE_END = 4 };
 enum { S_SEQ = 0, S_NP, S_SLOT0, S_WORDS = 4 };  // scan entry: sequence, pieces, slot of piece 0
+enum { X_TSTART = 0, X_LEN, X_RSLOT, X_SSLOT, X_WORDS = 4 };  // fixup task: token rows of a chunk group, first R slot,
+                                                              // start-state slot
+// compose task: ck_idx position, ck slot, start slot, kind (1: the single checkpoint, 2: an every-n row); the plan
+// schedules both kinds from the layout, the launch's checkpoint mode picks one
+enum { K_CKIDX = 0, K_WSSLOT, K_SSLOT, K_KIND, K_WORDS = 4 };
 
 typedef _Float16 half_t;
 
@@ -140,7 +150,9 @@ struct PfParams {
     float scale, lb;
     uint32_t flags;
     int ck_bf16;
-    float* ws;   // split sequences: [3][slots][H][128][128] fp32 = local end states, transitions, start states
+    float* ws;   // split sequences: [3][slots][H][128][128] fp32 = local end states, transitions, start states;
+                 // then [ck slots][2][H][128][128] fp32 checkpoint (local state, transition) pairs; then
+                 // [R slots][H][64][128] fp16 correction operands
 };
 
 // Raw inputs of one chunk row slice: row r, channels 16 cb .. 16 cb + 15.
@@ -232,8 +244,10 @@ __device__ __forceinline__ void store_state_bf16(uint16_t* dst, const f32x4 (&S)
     }
 }
 
-// P1 = false: the chunk walk with outputs, checkpoints and states.  P1 = true: a piece of a split sequence from a
-// zero state, also carrying the piece's state transition P (S_end = P S_start + S_loc); no outputs, no checkpoints.
+// The chunk walk with outputs, checkpoints and states.  P1 = true compiles in the pieces of split sequences: an entry
+// flagged PIECE_FIX starts from S = 0 and also carries its state transition P (S_end = P S_start + S_loc); its outputs
+// are partial (fp16, without the S_start term), and for every chunk it stores R = Q~ P + A_qk (-W P), the operand of
+// the correction O += scale R S_start; its checkpoints go to the workspace as (S_loc, P) pairs.
 template <bool RG, bool P1>
 __global__ void __launch_bounds__(PF_THREADS, 1)
     chunk_kernel(PfParams p, const int32_t* __restrict__ tab, const int32_t* __restrict__ ck_idx, int list_off) {
@@ -263,9 +277,12 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
     const int32_t* chain = tab + list_off + C_WORDS * ci;
     const int n = chain[C_SEQ], nch = chain[C_NCH], tstart = chain[C_TSTART], len = chain[C_LEN];
     const int first = chain[C_FIRST], pflags = chain[C_FLAGS], slot = chain[C_SLOT], seqch = chain[C_SEQCH];
+    const bool fix = P1 && (pflags & PIECE_FIX);
     const int every = tab[H_EVERY];
     const int64_t ws_arr = (int64_t)tab[H_NSLOTS] * H * D * D;  // floats per workspace array
     float* ws_h = p.ws + ((int64_t)slot * H + h) * D * D;        // this piece-head in array 0 (+ ws_arr: 1, 2)
+    float* ws_ck = p.ws + 3 * ws_arr;                            // checkpoint (S_loc, P) pairs
+    half_t* ws_r = reinterpret_cast<half_t*>(ws_ck + (int64_t)tab[H_NCKSLOTS] * 2 * H * D * D);  // R operands
     const bool pool = (p.flags & KDA355_PF_POOL) != 0;
     const bool RB = (p.flags & KDA355_PF_RAW_BETA) != 0;
     const bool NORM = (p.flags & KDA355_PF_NORMALIZE_QK) != 0;
@@ -276,10 +293,8 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
     const float* src = nullptr;
     int64_t row = -1;
     if (pool) row = p.state_idx[n];
-    if (P1) {
-        // a piece's local run starts from zero
-    } else if (pflags & PIECE_READ_WS) {
-        src = ws_h + 2 * ws_arr;  // start state composed by the scan
+    if (fix) {
+        // a later piece's local run starts from zero
     } else if (pool) {
         if (row >= 0 && row < p.state_slots && p.has_init[n]) src = p.state_pool + row * p.state_ss + (int64_t)h * D * D;
     } else if (p.init_state) {
@@ -288,15 +303,15 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt)
         S[dt] = src ? *reinterpret_cast<const f32x4*>(src + (16 * w + m) * D + 16 * dt + 4 * g) : f32x4{0.f, 0.f, 0.f, 0.f};
-    f32x4 Pm[8];  // P1: the transition, P[k][k'] at (k = 16dt + 4g + e, k' = 16w + m); starts as the identity
-    if (P1) {
+    f32x4 Pm[8];  // fix: the transition, P[k][k'] at (k = 16dt + 4g + e, k' = 16w + m); starts as the identity
+    if (fix) {
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
             for (int e = 0; e < 4; ++e) Pm[dt][e] = (16 * dt + 4 * g + e == 16 * w + m) ? 1.f : 0.f;
     }
 
-    const int ck_mode = P1 ? 0 : (p.flags & KDA355_PF_CK_EVERY) ? 2 : ((p.flags & KDA355_PF_CK_SINGLE) ? 1 : 0);
+    const int ck_mode = (p.flags & KDA355_PF_CK_EVERY) ? 2 : ((p.flags & KDA355_PF_CK_SINGLE) ? 1 : 0);
     auto ck_store = [&](int64_t rr) {
         if (rr < 0 || rr >= p.ck_slots) return;
         if (p.ck_bf16)
@@ -387,7 +402,7 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
             *reinterpret_cast<f32x4*>(&sG[r * RS32 + 16 * cb + 4 * (i ^ (cb >> 1))]) =
                 f32x4{gv[4 * i], gv[4 * i + 1], gv[4 * i + 2], gv[4 * i + 3]};
         if (cb == 0) sBeta[r] = bt;
-        if (!P1 && cl > 0) {  // the previous chunk was a full one
+        if (cl > 0) {  // the previous chunk was a full one
             u32x4* dst = reinterpret_cast<u32x4*>(p.out + ((int64_t)t0 - 64 + r) * p.out_rs + (int64_t)h * D + 16 * cb);
             dst[0] = o0;
             dst[1] = o1;
@@ -685,7 +700,7 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
         }
         lds_barrier();
         // ================= P7: the walk
-        if (P1) {  // S <- (diag(d) - Kd^T W) S + Kd^T U and P <- (diag(d) - Kd^T W) P, sharing every A fragment
+        if (fix) {  // S <- (diag(d) - Kd^T W) S + Kd^T U and P <- (diag(d) - Kd^T W) P, sharing every A fragment
             f16x8 SB[4], PB[4];
 #pragma unroll
             for (int s = 0; s < 4; ++s)
@@ -719,6 +734,32 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
                     WB[s][e] = (half_t)Wp[2 * s][e];
                     WB[s][4 + e] = (half_t)Wp[2 * s + 1][e];
                 }
+            // partial O^T = S^T Q~^T + V'^T A_qk^T (staged as fp16) and R^T = P^T Q~^T + W'^T A_qk^T (to the workspace),
+            // transposed tiles sharing the Q~ and A_qk fragments: lane (g, m) holds token 16 it + m, columns
+            // 16 w + 4 g .. + 3
+            half_t* rdst = ws_r + ((int64_t)(chain[C_RBASE] + cl) * H + h) * (64 * D) + 16 * w + 4 * g;
+#pragma unroll
+            for (int it = 0; it < 4; ++it) {
+                f32x4 acc = {0.f, 0.f, 0.f, 0.f}, acr = acc;
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    const f16x8 B = *reinterpret_cast<const f16x8*>(&sQt[(16 * it + m) * RS16 + 32 * s + 8 * g]);
+                    acc = mfma32(SB[s], B, acc);
+                    acr = mfma32(PB[s], B, acr);
+                }
+#pragma unroll
+                for (int s = 0; s < 2; ++s)
+                    if (s <= (it >> 1)) {
+                        const f16x8 B = *reinterpret_cast<const f16x8*>(&sAq[(16 * it + m) * RS16S + 32 * s + 8 * g]);
+                        acc = mfma32(VB[s], B, acc);
+                        acr = mfma32(WB[s], B, acr);
+                    }
+                f16x4 o, rr;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) { o[e] = (half_t)(p.scale * acc[e]); rr[e] = (half_t)acr[e]; }
+                *reinterpret_cast<f16x4*>(lds + LDS_A + (16 * it + m) * (4 * RS32) + 64 * w + 8 * g) = o;
+                *reinterpret_cast<f16x4*>(rdst + (16 * it + m) * D) = rr;
+            }
 #pragma unroll
             for (int dt = 0; dt < 8; ++dt) {
                 const f32x4 d4 = *reinterpret_cast<const f32x4*>(&sF[F_DEC * 128 + 16 * dt + 4 * g]);
@@ -790,16 +831,30 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
         }
         // checkpoints at chunk boundaries, counted in chunks of the whole sequence
         const int cs = first + cl + 1;
-        if (ck_mode == 1 && cs == ck_single) ck_store(ck_idx[n]);
-        if (ck_mode == 2 && every > 0 && cs % every == 0 && cs < seqch) ck_store(ck_idx[ck_row0 + cs / every]);
+        if (fix) {  // the pair (S_loc, P) of this chunk boundary; the row is composed once S_start is known
+            int wsl = -1;
+            if (ck_mode == 1 && cs == ck_single) wsl = chain[C_CKWS1];
+            if (ck_mode == 2 && every > 0 && cs % every == 0 && cs < seqch) wsl = chain[C_CKWS] + cs / every - (first / every + 1);
+            if (wsl >= 0) {
+                store_state(ws_ck + ((int64_t)(2 * wsl) * H + h) * D * D, S, w, g, m);
+                store_state(ws_ck + ((int64_t)(2 * wsl + 1) * H + h) * D * D, Pm, w, g, m);
+            }
+        } else {
+            if (ck_mode == 1 && cs == ck_single) ck_store(ck_idx[n]);
+            if (ck_mode == 2 && every > 0 && cs % every == 0 && cs < seqch) ck_store(ck_idx[ck_row0 + cs / every]);
+        }
         lds_barrier();
     }
-    if (P1) {  // the piece's local end state and transition (stored [k'][k])
+    if (nch > 0) store_out_slot(p, h, tstart + 64 * (nch - 1), min(64, len - 64 * (nch - 1)), r, cb, lds);
+    if (fix) {  // the piece's local end state and transition (stored [k'][k])
         store_state(ws_h, S, w, g, m);
         store_state(ws_h + ws_arr, Pm, w, g, m);
         return;
     }
-    if (nch > 0) store_out_slot(p, h, tstart + 64 * (nch - 1), min(64, len - 64 * (nch - 1)), r, cb, lds);
+    if (P1 && (pflags & PIECE_STORE_END)) {  // the first piece of a split sequence: the second piece's start state
+        store_state(p.ws + 2 * ws_arr + ((int64_t)(slot + 1) * H + h) * D * D, S, w, g, m);
+        return;
+    }
     // ---- final state (the last piece of a sequence)
     if (!(pflags & PIECE_LAST)) return;
     if (pool) {
@@ -809,61 +864,223 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
     }
 }
 
-// Start states of the pieces of split sequences: S_start(0) = the sequence's initial state, S_start(p+1) =
-// P_p S_start(p) + S_loc(p), in fp32.  V-major storage makes each step the plain product S_vm[v][:] . P^T[:][k]
-// (P^T as stored by the transition pass).  One workgroup of 256 threads per (sequence, head); thread (v, half)
-// computes 64 outputs of row v.
+// Row-block composition used by the scan and the checkpoint compose: out[v][k] = L[v][k] + sum_k' X[v][k'] P[k'][k]
+// in fp32, P as the chunk kernel stores it ([k'][k]).  Row v of the result depends on row v of X alone, so one
+// workgroup of 256 threads takes a block of 16 rows (grid: entries x H x 8): thread t computes row t % 16 of the block
+// at columns 8 (t / 16) .. + 7.  The block's X rows sit in LDS (row stride 132 floats), P is staged whole in LDS.
 constexpr int SC_THREADS = 256;
-constexpr int SC_RS = 129;  // padded rows of the state copy (row v read along k by 64 different rows at once)
+constexpr int SC_ROWS = 16;
+constexpr int SC_XS = 132;
+constexpr int SC_SMEM = D * D * 4 + SC_ROWS * SC_XS * 4;
+
+__device__ __forceinline__ void stage_P(const float* __restrict__ P, float* sP) {
+    f32x4 r[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) r[j] = reinterpret_cast<const f32x4*>(P)[threadIdx.x + SC_THREADS * j];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) reinterpret_cast<f32x4*>(sP)[threadIdx.x + SC_THREADS * j] = r[j];
+}
+// the 16 rows starting at X (row stride D) -> sX
+__device__ __forceinline__ void stage_X(const float* __restrict__ X, float* sX) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int i = threadIdx.x + SC_THREADS * j, rr = i >> 5, c4 = i & 31;
+        *reinterpret_cast<f32x4*>(sX + rr * SC_XS + 4 * c4) = *reinterpret_cast<const f32x4*>(X + rr * D + 4 * c4);
+    }
+}
+// acc = Lrow[8 kq .. + 7] + sum_k' sX[vr][k'] sP[k'][8 kq .. + 7] (vr = t % 16, kq = t / 16); sX and sP staged and synced
+__device__ __forceinline__ void compose_rows(const float* sX, const float* sP, const float* __restrict__ Lrow,
+                                             float (&acc)[8]) {
+    const int vr = threadIdx.x & 15, kq = threadIdx.x >> 4;
+    const f32x4 l0 = *reinterpret_cast<const f32x4*>(Lrow + 8 * kq), l1 = *reinterpret_cast<const f32x4*>(Lrow + 8 * kq + 4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) { acc[j] = l0[j]; acc[4 + j] = l1[j]; }
+    for (int k4 = 0; k4 < D / 4; ++k4) {
+        const f32x4 xv = *reinterpret_cast<const f32x4*>(sX + vr * SC_XS + 4 * k4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const f32x4 p0 = *reinterpret_cast<const f32x4*>(sP + (4 * k4 + e) * D + 8 * kq);
+            const f32x4 p1 = *reinterpret_cast<const f32x4*>(sP + (4 * k4 + e) * D + 8 * kq + 4);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) { acc[j] += xv[e] * p0[j]; acc[4 + j] += xv[e] * p1[j]; }
+        }
+    }
+}
+
+// Split sequences: X_1 = the first piece's end state (stored by that piece), X_{p+1} = P_p X_p + S_loc(p) for the
+// later pieces p = 1 .. np-1; X_p is the start state of piece p, X_np the sequence's final state.  One workgroup per
+// (sequence, head, block of 16 state rows).
 __global__ void __launch_bounds__(SC_THREADS) scan_kernel(PfParams p, const int32_t* __restrict__ tab) {
     extern __shared__ __align__(16) unsigned char lds[];
-    float* sS = reinterpret_cast<float*>(lds);                          // [128][129]
-    float* sP = reinterpret_cast<float*>(lds + 128 * SC_RS * 4 + 16);   // [128][128] P^T
+    float* sP = reinterpret_cast<float*>(lds);
+    float* sX = reinterpret_cast<float*>(lds + D * D * 4);
     const int H = p.H;
-    const int si = blockIdx.x / H;
-    const int h = blockIdx.x - si * H;
+    const int rb = blockIdx.x & 7, eh = blockIdx.x >> 3;
+    const int si = eh / H;
+    const int h = eh - si * H;
     const int32_t* e = tab + tab[H_OFF_SCAN] + S_WORDS * si;
     const int n = e[S_SEQ], np = e[S_NP], slot0 = e[S_SLOT0];
     const int64_t ws_arr = (int64_t)tab[H_NSLOTS] * H * D * D;
-    const int t = threadIdx.x, v = t & 127, kh = t >> 7;
-    // the sequence's initial state (same rules as the chunk walk)
-    const float* src = nullptr;
+    const int t = threadIdx.x, vr = t & 15, kq = t >> 4, v = SC_ROWS * rb + vr;
+    stage_X(p.ws + 2 * ws_arr + ((int64_t)(slot0 + 1) * H + h) * D * D + SC_ROWS * rb * D, sX);
+    float* fin = nullptr;  // the final state's destination (same rules as the chunk walk)
     if (p.flags & KDA355_PF_POOL) {
         const int64_t row = p.state_idx[n];
-        if (row >= 0 && row < p.state_slots && p.has_init[n]) src = p.state_pool + row * p.state_ss + (int64_t)h * D * D;
-    } else if (p.init_state) {
-        src = p.init_state + ((int64_t)n * H + h) * D * D;
+        if (row >= 0 && row < p.state_slots) fin = p.state_pool + row * p.state_ss + (int64_t)h * D * D;
+    } else {
+        fin = p.final_state + ((int64_t)n * H + h) * D * D;
     }
-    for (int i = t; i < D * D; i += SC_THREADS) sS[(i >> 7) * SC_RS + (i & 127)] = src ? src[i] : 0.f;
-    for (int pc = 0; pc + 1 < np; ++pc) {
-        const float* P = p.ws + ws_arr + ((int64_t)(slot0 + pc) * H + h) * D * D;
-        const float* L = p.ws + ((int64_t)(slot0 + pc) * H + h) * D * D;
-        for (int i = t; i < D * D / 4; i += SC_THREADS)
-            reinterpret_cast<f32x4*>(sP)[i] = reinterpret_cast<const f32x4*>(P)[i];
+    for (int pc = 1; pc < np; ++pc) {
+        const int64_t so = ((int64_t)(slot0 + pc) * H + h) * D * D;
+        stage_P(p.ws + ws_arr + so, sP);
         __syncthreads();
-        float acc[64];
+        float acc[8];
+        compose_rows(sX, sP, p.ws + so + (int64_t)v * D, acc);
+        __syncthreads();  // every thread has read sX and sP
+        float* dst = (pc + 1 < np) ? p.ws + 2 * ws_arr + ((int64_t)(slot0 + pc + 1) * H + h) * D * D : fin;
+        const f32x4 a0 = {acc[0], acc[1], acc[2], acc[3]}, a1 = {acc[4], acc[5], acc[6], acc[7]};
+        *reinterpret_cast<f32x4*>(sX + vr * SC_XS + 8 * kq) = a0;
+        *reinterpret_cast<f32x4*>(sX + vr * SC_XS + 8 * kq + 4) = a1;
+        if (dst) {
+            *reinterpret_cast<f32x4*>(dst + (int64_t)v * D + 8 * kq) = a0;
+            *reinterpret_cast<f32x4*>(dst + (int64_t)v * D + 8 * kq + 4) = a1;
+        }
+    }
+}
+
+// Checkpoints inside later pieces: row = P_c S_start + S_loc(c) (fp32), then stored like the chunk walk's checkpoints.
+// One workgroup per (task, head, block of 16 state rows); tasks of the checkpoint kind the launch does not use exit.
+__global__ void __launch_bounds__(SC_THREADS) ck_compose_kernel(PfParams p, const int32_t* __restrict__ tab) {
+    extern __shared__ __align__(16) unsigned char lds[];
+    float* sP = reinterpret_cast<float*>(lds);
+    float* sX = reinterpret_cast<float*>(lds + D * D * 4);
+    const int H = p.H;
+    const int rb = blockIdx.x & 7, eh = blockIdx.x >> 3;
+    const int ti = eh / H;
+    const int h = eh - ti * H;
+    const int32_t* e = tab + tab[H_OFF_CKC] + K_WORDS * ti;
+    const int ck_mode = (p.flags & KDA355_PF_CK_EVERY) ? 2 : ((p.flags & KDA355_PF_CK_SINGLE) ? 1 : 0);
+    if (e[K_KIND] != ck_mode) return;
+    const int64_t ws_arr = (int64_t)tab[H_NSLOTS] * H * D * D;
+    const float* ws_ck = p.ws + 3 * ws_arr;
+    const int t = threadIdx.x, kq = t >> 4, v = SC_ROWS * rb + (t & 15);
+    stage_X(p.ws + 2 * ws_arr + ((int64_t)e[K_SSLOT] * H + h) * D * D + SC_ROWS * rb * D, sX);
+    stage_P(ws_ck + ((int64_t)(2 * e[K_WSSLOT] + 1) * H + h) * D * D, sP);
+    __syncthreads();
+    float acc[8];
+    compose_rows(sX, sP, ws_ck + ((int64_t)(2 * e[K_WSSLOT]) * H + h) * D * D + (int64_t)v * D, acc);
+    const int64_t rr = p.ck_idx[e[K_CKIDX]];
+    if (rr < 0 || rr >= p.ck_slots) return;
+    const int64_t off = rr * p.ck_ss + (int64_t)h * D * D + (int64_t)v * D + 8 * kq;
+    if (p.ck_bf16) {
+        u32x4 b;
+        b.x = f2bf(acc[0]) | (f2bf(acc[1]) << 16);
+        b.y = f2bf(acc[2]) | (f2bf(acc[3]) << 16);
+        b.z = f2bf(acc[4]) | (f2bf(acc[5]) << 16);
+        b.w = f2bf(acc[6]) | (f2bf(acc[7]) << 16);
+        *reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(p.ck_pool) + off) = b;
+    } else {
+        float* dst = reinterpret_cast<float*>(p.ck_pool) + off;
+        *reinterpret_cast<f32x4*>(dst) = f32x4{acc[0], acc[1], acc[2], acc[3]};
+        *reinterpret_cast<f32x4*>(dst + 4) = f32x4{acc[4], acc[5], acc[6], acc[7]};
+    }
+}
+
+// The outputs of later pieces: O = partial (fp16, as the chunk kernel left it in `out`) + scale R S_start, stored as
+// bf16.  One workgroup of 256 threads (4 waves) per (group of up to FX_GROUP chunks of one piece, head): the start
+// state is read once per group.  Wave w produces value columns 32 w .. 32 w + 31 on 16x16x32 f16 MFMAs with the
+// state as the A operand, so the result tile is transposed (lane (g, m): token m); the A rows are ordered so that the
+// two tiles of a lane cover the 8 consecutive values 32 w + 8 g .. + 7 (one 16-byte load and store per token).
+// Memory accesses go through buffer descriptors that end at the group's last token and last R tile: tokens past them
+// (the tail of a partial last chunk, the prefetch past the last chunk) read zeros and their stores are dropped, so no
+// access sits under a branch.
+constexpr int FX_THREADS = 256;
+constexpr int FX_GROUP = 8;
+__global__ void __launch_bounds__(FX_THREADS) fixup_kernel(PfParams p, const int32_t* __restrict__ tab) {
+    const int H = p.H;
+    const int ti = blockIdx.x / H;
+    const int h = blockIdx.x - ti * H;
+    const int32_t* e = tab + tab[H_OFF_FIX] + X_WORDS * ti;
+    const int tstart = e[X_TSTART], L = e[X_LEN];
+    const int64_t ws_arr = (int64_t)tab[H_NSLOTS] * H * D * D;
+    const float* Sst = p.ws + 2 * ws_arr + ((int64_t)e[X_SSLOT] * H + h) * D * D;  // V-major [v][k]
+    const half_t* R0 = reinterpret_cast<const half_t*>(p.ws + 3 * ws_arr + (int64_t)tab[H_NCKSLOTS] * 2 * H * D * D) +
+                       ((int64_t)e[X_RSLOT] * H + h) * (64 * D);                  // [token][k], chunk c at + c H 64 D
+    const int64_t rstep = (int64_t)H * 64 * D;
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, m = lane & 15, g = lane >> 4;
+    f16x8 Y[2][4];  // S_start rows: tile vt, A row m <-> value 32 w + 8 (m / 4) + 4 vt + m % 4; k = 32 ks + 8 g .. + 7
 #pragma unroll
-        for (int j = 0; j < 64; ++j) acc[j] = L[v * D + 64 * kh + j];
-        for (int kk = 0; kk < D; ++kk) {
-            const float sv = sS[v * SC_RS + kk];
-            const f32x4* pr = reinterpret_cast<const f32x4*>(sP + kk * D + 64 * kh);
+    for (int vt = 0; vt < 2; ++vt)
 #pragma unroll
-            for (int j4 = 0; j4 < 16; ++j4) {
-                const f32x4 pv = pr[j4];
-                acc[4 * j4] += sv * pv[0];
-                acc[4 * j4 + 1] += sv * pv[1];
-                acc[4 * j4 + 2] += sv * pv[2];
-                acc[4 * j4 + 3] += sv * pv[3];
+        for (int ks = 0; ks < 4; ++ks) {
+            const float* src = Sst + (32 * w + 8 * (m >> 2) + 4 * vt + (m & 3)) * D + 32 * ks + 8 * g;
+            const f32x4 a = *reinterpret_cast<const f32x4*>(src), b = *reinterpret_cast<const f32x4*>(src + 4);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) { Y[vt][ks][j] = (half_t)a[j]; Y[vt][ks][4 + j] = (half_t)b[j]; }
+        }
+    const int rs = p.out_rs * 2;  // bytes per output row
+    const __amdgpu_buffer_rsrc_t ob = __builtin_amdgcn_make_buffer_rsrc(
+        p.out + (int64_t)tstart * p.out_rs + (int64_t)h * D, (short)0, (L - 1) * rs + D * 2, 0x00020000);
+    const int nchk = (L + 63) >> 6;
+    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<half_t*>(R0), (short)0, (int)((nchk - 1) * rstep * 2 + 64 * D * 2), 0x00020000);
+    const int col = (32 * w + 8 * g) * 2;
+    const int roff = (m * D + 8 * g) * 2;
+    // one chunk's operands: R rows (token 16 tt + m, k = 32 ks + 8 g .. + 7) and the fp16 partial outputs; a chunk
+    // past the group reads zeros
+    struct Ops { f16x8 X[4][4]; f16x8 part[4]; };
+    auto load = [&](Ops& b, int c0) {
+        const int rbase = (int)((c0 >> 6) * rstep * 2) + roff;
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) {
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks)
+                b.X[tt][ks] = __builtin_bit_cast(
+                    f16x8, __builtin_amdgcn_raw_buffer_load_b128(rb, rbase + (16 * tt * D + 32 * ks) * 2, 0, 0));
+            b.part[tt] = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(ob, (c0 + 16 * tt + m) * rs + col, 0, 0));
+        }
+    };
+    // wait for b's loads here (later loads stay in flight) and keep the next chunk's loads above this point
+    auto ready = [&](Ops& b) {
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) {
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) asm volatile("" : "+v"(b.X[tt][ks])::"memory");
+            asm volatile("" : "+v"(b.part[tt])::"memory");
+        }
+    };
+    auto finish = [&](const Ops& b, int c0) {
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) {
+            f32x4 acc[2];
+#pragma unroll
+            for (int vt = 0; vt < 2; ++vt) {
+                acc[vt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int ks = 0; ks < 4; ++ks) acc[vt] = mfma32(Y[vt][ks], b.X[tt][ks], acc[vt]);
             }
+            const f16x8& part = b.part[tt];
+            u32x4 r;
+            r.x = f2bf((float)part[0] + p.scale * acc[0][0]) | (f2bf((float)part[1] + p.scale * acc[0][1]) << 16);
+            r.y = f2bf((float)part[2] + p.scale * acc[0][2]) | (f2bf((float)part[3] + p.scale * acc[0][3]) << 16);
+            r.z = f2bf((float)part[4] + p.scale * acc[1][0]) | (f2bf((float)part[5] + p.scale * acc[1][1]) << 16);
+            r.w = f2bf((float)part[6] + p.scale * acc[1][2]) | (f2bf((float)part[7] + p.scale * acc[1][3]) << 16);
+            __builtin_amdgcn_raw_buffer_store_b128(r, ob, (c0 + 16 * tt + m) * rs + col, 0, 0);
         }
-        __syncthreads();  // every thread has read sS and sP
-        float* dst = p.ws + 2 * ws_arr + ((int64_t)(slot0 + pc + 1) * H + h) * D * D;
+    };
+    // each chunk's loads are issued one chunk ahead; the loop is unrolled whole (straight-line waits)
+    Ops A, B;
+    load(A, 0);
 #pragma unroll
-        for (int j = 0; j < 64; ++j) {
-            sS[v * SC_RS + 64 * kh + j] = acc[j];
-            dst[v * D + 64 * kh + j] = acc[j];
-        }
-        __syncthreads();
+    for (int i = 0; i < FX_GROUP; i += 2) {
+        if (i + 1 < FX_GROUP) load(B, 64 * (i + 1));
+        ready(A);
+        finish(A, 64 * i);
+        if (64 * (i + 1) >= L) break;
+        if (i + 2 < FX_GROUP) load(A, 64 * (i + 2));
+        ready(B);
+        finish(B, 64 * (i + 1));
+        if (64 * (i + 2) >= L) break;
     }
 }
 
@@ -880,16 +1097,27 @@ hipError_t launch_chunk(const PfParams& p, int list_off, int entries, hipStream_
                        list_off);
     return hipGetLastError();
 }
-hipError_t launch_scan(const PfParams& p, int entries, hipStream_t s) {
-    const int smem = 128 * SC_RS * 4 + 16 + D * D * 4;
-    static bool attr_set = false;
-    if (!attr_set) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&scan_kernel),
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+template <typename K>
+hipError_t launch_composer(K kernel, const PfParams& p, int entries, hipStream_t s, bool& attr_set) {
+    if (!attr_set) {  // idempotent; a race only repeats the call
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, SC_SMEM);
         if (e != hipSuccess) return e;
         attr_set = true;
     }
-    hipLaunchKernelGGL(scan_kernel, dim3(entries * p.H), dim3(SC_THREADS), smem, s, p, p.tab);
+    hipLaunchKernelGGL(kernel, dim3(entries * p.H * (D / SC_ROWS)), dim3(SC_THREADS), SC_SMEM, s, p, p.tab);
+    return hipGetLastError();
+}
+hipError_t launch_scan(const PfParams& p, int entries, hipStream_t s) {
+    static bool attr_set = false;
+    return launch_composer(scan_kernel, p, entries, s, attr_set);
+}
+hipError_t launch_ck_compose(const PfParams& p, int entries, hipStream_t s) {
+    static bool attr_set = false;
+    return launch_composer(ck_compose_kernel, p, entries, s, attr_set);
+}
+hipError_t launch_fixup(const PfParams& p, int entries, hipStream_t s) {
+    hipLaunchKernelGGL(fixup_kernel, dim3(entries * p.H), dim3(FX_THREADS), 0, s, p, p.tab);
     return hipGetLastError();
 }
 
@@ -919,41 +1147,119 @@ extern "C" int kda355_prefill_plan(const KdaPrefillPlanIn* in, KdaPrefillPlan* p
         nch[n] = (int)((cu[n + 1] - cu[n] + 63) / 64);
         nchunks += nch[n];
     }
-    // Pieces: when the (sequence, head) chains alone would leave CUs idle, long sequences are cut into pieces of about
-    // the chunk count a CU would get at perfect balance (at least MIN_PIECE chunks each).  Split sequences run a
-    // transition pass and a scan before the final pass.
+    // Pieces.  A workgroup walks one (piece, head) chain and a CU holds one such workgroup at a time; the chain list is
+    // dispatched longest first.  Candidate cuts: every sequence longer than a piece length T is cut into
+    // ceil(nch / T) near-equal pieces of >= MIN_PIECE chunks, for T on a geometric ladder.  Each candidate is costed by
+    // list-scheduling its chains onto the CUs (every chunk costs one unit, later pieces as much as first ones), plus
+    // the passes a split adds: the scan (~SCAN_UNITS chunk times) and the output fixup (~FIX_UNITS chunk times per
+    // chunk-head of later pieces, spread over the chip).  The cheapest candidate wins; ties keep fewer pieces.  The
+    // first piece of a split sequence runs from the true start state; later pieces run from S = 0, carry their
+    // transition and are completed by the scan, fixup and checkpoint-compose kernels.
     constexpr int MIN_PIECE = 16;
+    constexpr double SCAN_UNITS = 4.0, FIX_UNITS = 0.0012;
     const int num_cus = in->num_cus > 0 ? in->num_cus : 256;
     std::vector<int> npieces(N, 1);
-    if ((int64_t)N * in->H < num_cus && nchunks > 0) {
-        const int64_t target = std::max<int64_t>(MIN_PIECE, (nchunks * in->H + num_cus - 1) / num_cus);
-        for (int n = 0; n < N; ++n) {
-            const int most = nch[n] / MIN_PIECE;
-            const int np = (int)std::min<int64_t>(most, (nch[n] + target / 2) / target);
-            npieces[n] = std::max(1, np);
+    if (nchunks > 0) {
+        int maxc = 0;
+        for (int n = 0; n < N; ++n) maxc = std::max(maxc, nch[n]);
+        const int64_t avg = std::max<int64_t>(1, (nchunks * in->H + num_cus - 1) / num_cus);
+        const bool idle = (int64_t)N * in->H < num_cus;
+        if ((idle || 4 * (int64_t)maxc > 5 * avg) && maxc >= 2 * MIN_PIECE) {
+            auto cut = [&](int n, int T) { return nch[n] > T ? std::max(1, std::min(nch[n] / MIN_PIECE, (nch[n] + T - 1) / T)) : 1; };
+            std::vector<int> counts;
+            std::vector<int64_t> cusload;
+            auto cost = [&](int T) {
+                counts.clear();
+                int64_t fixch = 0;
+                bool split = false;
+                for (int n = 0; n < N; ++n) {
+                    const int np = cut(n, T);
+                    for (int pc = 0; pc < np; ++pc) {
+                        const int c = nch[n] / np + (pc < nch[n] % np ? 1 : 0);
+                        counts.push_back(c);
+                        if (pc > 0) fixch += c;
+                    }
+                    split |= np > 1;
+                }
+                std::stable_sort(counts.begin(), counts.end(), std::greater<int>());
+                cusload.assign(num_cus, 0);  // min-heap of CU finish times (a zero-filled array is a valid heap)
+                int64_t span = 0;
+                for (int c : counts)
+                    for (int h = 0; h < in->H; ++h) {
+                        std::pop_heap(cusload.begin(), cusload.end(), std::greater<int64_t>());
+                        cusload.back() += c;
+                        span = std::max(span, cusload.back());
+                        std::push_heap(cusload.begin(), cusload.end(), std::greater<int64_t>());
+                    }
+                return (double)span + (split ? SCAN_UNITS + FIX_UNITS * (double)fixch * in->H : 0.0);
+            };
+            int bestT = maxc;
+            double best = cost(maxc);
+            for (double t = MIN_PIECE; t < maxc; t *= 1.12) {
+                const int T = (int)t;
+                const double c = cost(T);
+                if (c < best - 1e-9) { best = c; bestT = T; }
+            }
+            for (int n = 0; n < N; ++n) npieces[n] = cut(n, bestT);
         }
     }
-    struct Piece { int n, first, count, slot; };
+    std::vector<int> ck_chunk(N, 0), ck_row0(N, 0);
+    {
+        int64_t ckstart = 0;
+        for (int n = 0; n < N; ++n) {
+            if (in->ck_offsets) {
+                const int32_t o = in->ck_offsets[n];
+                // kda/mi350x/kda/prefill/main.cpp:110-118: offsets that are not positive multiples of 64 within the
+                // sequence write nothing
+                if (o > 0 && o % 64 == 0 && o <= cu[n + 1] - cu[n]) ck_chunk[n] = o / 64;
+            }
+            ck_row0[n] = (int)ckstart;
+            if (every_chunks) ckstart += (nch[n] + every_chunks - 1) / every_chunks;
+        }
+    }
+    struct Piece { int n, first, count, slot, rbase, ckws, ckws1, flags; };
+    struct CkTask { int ckidx, wsslot, sslot, kind; };
     std::vector<Piece> pieces;
-    int nslots = 0, nsplit = 0, ntrans = 0;
+    std::vector<CkTask> cktasks;
+    int nslots = 0, nsplit = 0, nrslots = 0, nfix = 0, nsplitpieces = 0;
     for (int n = 0; n < N; ++n) {
         const int np = npieces[n];
         int f = 0;
         for (int pc = 0; pc < np; ++pc) {
             const int c = nch[n] / np + (pc < nch[n] % np ? 1 : 0);
-            pieces.push_back({n, f, c, np > 1 ? nslots + pc : 0});
+            Piece P{n, f, c, np > 1 ? nslots + pc : 0, 0, 0, 0, 0};
+            if (np == 1) {
+                P.flags = PIECE_LAST;
+            } else if (pc == 0) {
+                P.flags = PIECE_STORE_END;
+            } else {
+                P.flags = PIECE_FIX;
+                P.rbase = nrslots;
+                nrslots += c;
+                nfix += (c + FX_GROUP - 1) / FX_GROUP;
+                // checkpoints of both kinds the layout defines (the launch's mode uses one): the single one at
+                // ck_chunk, every-n rows j at chunk j * every (row 0 is the start state, in the first piece)
+                P.ckws1 = (int)cktasks.size();
+                if (ck_chunk[n] > f && ck_chunk[n] <= f + c) cktasks.push_back({n, (int)cktasks.size(), P.slot, 1});
+                P.ckws = (int)cktasks.size();
+                if (every_chunks > 0)
+                    for (int j = f / every_chunks + 1; (int64_t)j * every_chunks <= f + c && j * every_chunks < nch[n]; ++j)
+                        cktasks.push_back({ck_row0[n] + j, (int)cktasks.size(), P.slot, 2});
+            }
+            pieces.push_back(P);
             f += c;
         }
         if (np > 1) {
             nslots += np;
             ++nsplit;
-            ntrans += np;
+            nsplitpieces += np;
         }
     }
-    const int nfinal = (int)pieces.size();
-    const int64_t off_final = H_WORDS, off_trans = off_final + (int64_t)C_WORDS * nfinal;
-    const int64_t off_scan = off_trans + (int64_t)C_WORDS * ntrans;
-    const int64_t words = off_scan + (int64_t)S_WORDS * nsplit;
+    const int nfinal = (int)pieces.size(), nck = (int)cktasks.size();
+    const int64_t off_final = H_WORDS, off_fix = off_final + (int64_t)C_WORDS * nfinal;
+    const int64_t off_scan = off_fix + (int64_t)X_WORDS * nfix;
+    const int64_t off_ckc = off_scan + (int64_t)S_WORDS * nsplit;
+    const int64_t words = off_ckc + (int64_t)K_WORDS * nck;
     plan->T = T;
     plan->N = N;
     plan->H = in->H;
@@ -965,15 +1271,19 @@ extern "C" int kda355_prefill_plan(const KdaPrefillPlanIn* in, KdaPrefillPlan* p
         maxc = std::max(maxc, nch[n]);
         if (every_chunks) ckrows += (nch[n] + every_chunks - 1) / every_chunks;
     }
+    const int64_t dd = (int64_t)KDA355_HEAD_DIM * KDA355_HEAD_DIM;
     plan->max_chain_chunks = maxc;
     plan->table_words = words;
-    plan->workspace_bytes = (int64_t)3 * nslots * in->H * KDA355_HEAD_DIM * KDA355_HEAD_DIM * 4;
+    plan->workspace_bytes = ((int64_t)3 * nslots + 2 * (int64_t)nck) * in->H * dd * 4 +
+                            (int64_t)nrslots * in->H * 64 * KDA355_HEAD_DIM * 2;
     plan->ck_rows = ckrows;
     plan->magic = PLAN_MAGIC;
     plan->flags = in->flags;
     plan->ck_every = in->ck_every;
-    plan->num_pieces = ntrans;
+    plan->num_pieces = nsplitpieces;
     plan->num_split = nsplit;
+    plan->num_fix_tasks = nfix;
+    plan->num_ck_tasks = nck;
     if (!tables) return 0;
     KDA_CHECK_ARG(capacity >= words, "prefill_plan: table capacity %lld < %lld words", (long long)capacity, (long long)words);
     int32_t* t = tables;
@@ -986,24 +1296,16 @@ extern "C" int kda355_prefill_plan(const KdaPrefillPlanIn* in, KdaPrefillPlan* p
     t[H_CKROWS] = (int32_t)ckrows;
     t[H_OFF_FINAL] = (int32_t)off_final;
     t[H_NFINAL] = nfinal;
-    t[H_OFF_TRANS] = (int32_t)off_trans;
-    t[H_NTRANS] = ntrans;
+    t[H_OFF_FIX] = (int32_t)off_fix;
+    t[H_NFIX] = nfix;
     t[H_OFF_SCAN] = (int32_t)off_scan;
     t[H_NSCAN] = nsplit;
     t[H_NSLOTS] = nslots;
-    std::vector<int> ck_chunk(N, 0), ck_row0(N, 0);
-    int64_t ckstart = 0;
-    for (int n = 0; n < N; ++n) {
-        if (in->ck_offsets) {
-            const int32_t o = in->ck_offsets[n];
-            // kda/mi350x/kda/prefill/main.cpp:110-118: offsets that are not positive multiples of 64 within the sequence
-            // write nothing
-            if (o > 0 && o % 64 == 0 && o <= cu[n + 1] - cu[n]) ck_chunk[n] = o / 64;
-        }
-        ck_row0[n] = (int)ckstart;
-        if (every_chunks) ckstart += (nch[n] + every_chunks - 1) / every_chunks;
-    }
-    auto fill = [&](int32_t* e, const Piece& pc, int flags) {
+    t[H_OFF_CKC] = (int32_t)off_ckc;
+    t[H_NCKC] = nck;
+    t[H_NRSLOTS] = nrslots;
+    t[H_NCKSLOTS] = nck;
+    auto fill = [&](int32_t* e, const Piece& pc) {
         const int64_t len = cu[pc.n + 1] - cu[pc.n];
         e[C_SEQ] = pc.n;
         e[C_NCH] = pc.count;
@@ -1012,30 +1314,44 @@ extern "C" int kda355_prefill_plan(const KdaPrefillPlanIn* in, KdaPrefillPlan* p
         e[C_CKSINGLE] = ck_chunk[pc.n];
         e[C_CKROW0] = ck_row0[pc.n];
         e[C_FIRST] = pc.first;
-        e[C_FLAGS] = flags;
+        e[C_FLAGS] = pc.flags;
         e[C_SLOT] = pc.slot;
         e[C_SEQCH] = nch[pc.n];
+        e[C_RBASE] = pc.rbase;
+        e[C_CKWS] = pc.ckws;
+        e[C_CKWS1] = pc.ckws1;
     };
-    // final pass: longest pieces first (they start earliest when the grid runs in several waves)
+    // chain list: longest pieces first (they start earliest when the grid runs in several rounds)
     std::vector<int> order(nfinal);
     std::iota(order.begin(), order.end(), 0);
     std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return pieces[a].count > pieces[b].count; });
-    for (int i = 0; i < nfinal; ++i) {
-        const Piece& pc = pieces[order[i]];
-        const bool last = pc.first + pc.count == nch[pc.n];
-        fill(t + off_final + (int64_t)C_WORDS * i, pc, (pc.first > 0 ? PIECE_READ_WS : 0) | (last ? PIECE_LAST : 0));
-    }
-    int ti = 0, si = 0;
-    for (int i = 0; i < nfinal; ++i) {
-        const Piece& pc = pieces[i];
-        if (npieces[pc.n] == 1) continue;
-        fill(t + off_trans + (int64_t)C_WORDS * ti++, pc, 0);
-        if (pc.first == 0) {
+    for (int i = 0; i < nfinal; ++i) fill(t + off_final + (int64_t)C_WORDS * i, pieces[order[i]]);
+    int xi = 0, si = 0;
+    for (const Piece& pc : pieces) {
+        if (pc.flags & PIECE_FIX) {
+            const int64_t len = cu[pc.n + 1] - cu[pc.n];
+            for (int c = 0; c < pc.count; c += FX_GROUP) {
+                int32_t* e = t + off_fix + (int64_t)X_WORDS * xi++;
+                const int64_t c0 = 64 * (int64_t)(pc.first + c);
+                e[X_TSTART] = (int32_t)(cu[pc.n] + c0);
+                e[X_LEN] = (int32_t)std::min<int64_t>(64 * (int64_t)std::min(FX_GROUP, pc.count - c), len - c0);
+                e[X_RSLOT] = pc.rbase + c;
+                e[X_SSLOT] = pc.slot;
+            }
+        }
+        if (pc.flags & PIECE_STORE_END) {
             int32_t* e = t + off_scan + (int64_t)S_WORDS * si++;
             e[S_SEQ] = pc.n;
             e[S_NP] = npieces[pc.n];
             e[S_SLOT0] = pc.slot;
         }
+    }
+    for (int i = 0; i < nck; ++i) {
+        int32_t* e = t + off_ckc + (int64_t)K_WORDS * i;
+        e[K_CKIDX] = cktasks[i].ckidx;
+        e[K_WSSLOT] = cktasks[i].wsslot;
+        e[K_SSLOT] = cktasks[i].sslot;
+        e[K_KIND] = cktasks[i].kind;
     }
     return 0;
 }
@@ -1111,14 +1427,19 @@ extern "C" int kda355_prefill_launch(const KdaPrefillArgs* a, kda355_stream_t st
     p.ws = static_cast<float*>(a->workspace);
     const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const bool rg = (f & KDA355_PF_RAW_GATE) != 0;
-    const int off_final = H_WORDS, off_trans = off_final + C_WORDS * pl->num_chains;
+    const int off_final = H_WORDS;
     hipError_t e = hipSuccess;
-    if (pl->num_pieces > 0) {  // split sequences: local runs with transitions, then the start states of their pieces
-        e = rg ? launch_chunk<true, true>(p, off_trans, pl->num_pieces, s) : launch_chunk<false, true>(p, off_trans, pl->num_pieces, s);
+    if (pl->num_split > 0) {
+        // one chunk launch for every piece (first pieces from their true start states, later pieces from zero with their
+        // transitions), then the start / final states of the split sequences, the later pieces' outputs and their
+        // checkpoints
+        e = rg ? launch_chunk<true, true>(p, off_final, pl->num_chains, s) : launch_chunk<false, true>(p, off_final, pl->num_chains, s);
         if (e == hipSuccess) e = launch_scan(p, pl->num_split, s);
-    }
-    if (e == hipSuccess)
+        if (e == hipSuccess && pl->num_fix_tasks > 0) e = launch_fixup(p, pl->num_fix_tasks, s);
+        if (e == hipSuccess && pl->num_ck_tasks > 0) e = launch_ck_compose(p, pl->num_ck_tasks, s);
+    } else {
         e = rg ? launch_chunk<true, false>(p, off_final, pl->num_chains, s) : launch_chunk<false, false>(p, off_final, pl->num_chains, s);
+    }
     if (e != hipSuccess) {
         set_error("prefill: launch failed: %s", hipGetErrorString(e));
         return KDA355_ELAUNCH;

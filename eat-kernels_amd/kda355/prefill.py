@@ -73,8 +73,9 @@ class PrefillMeta:
 
 def plan(cu_seqlens, num_heads, checkpoint_offsets=None, ck_every=0, device=None, num_cus=None):
     """Host-only schedule from the layout (never the data); one H2D copy of the table when device is a GPU.
-    num_cus: CUs to fill (default: the device's); when the (sequence, head) chains alone leave CUs idle, long sequences
-    are split into pieces (a transition pass and a scan run before the final pass, with a workspace)."""
+    num_cus: CUs to fill (default: the device's); when the (sequence, head) chains alone leave CUs idle or the longest
+    chains would finish well after the rest, long sequences are split into pieces of >= 16 chunks (later pieces run
+    from a zero state carrying their transition; a scan and an output fixup complete them, with a workspace)."""
     cu = np.ascontiguousarray(torch.as_tensor(cu_seqlens).detach().cpu().numpy(), dtype=np.int64)
     N = cu.size - 1
     if N < 1:

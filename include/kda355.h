@@ -174,9 +174,10 @@ typedef struct KdaPrefillPlanIn {
     const int32_t* ck_offsets;  /* host [N] single-checkpoint offsets (tokens) or NULL */
     int32_t N, H;
     int32_t ck_every;           /* every-n interval in tokens (multiple of 64) or 0 */
-    int32_t num_cus;            /* CUs of the device (0: 256); sequences are split into pieces when the (sequence, head)
-                                   chains alone would leave CUs idle */
-    uint32_t flags;
+    int32_t num_cus;            /* CUs of the device (0: 256); long sequences are split into pieces of >= 16 chunks
+                                   when that shortens the schedule (the chains alone would leave CUs idle, or the
+                                   longest ones would finish well after the rest) */
+    uint32_t flags;             /* unused (0): checkpoint work is scheduled for every kind the layout defines */
     int32_t reserved;
 } KdaPrefillPlanIn;
 
@@ -190,6 +191,9 @@ typedef struct KdaPrefillPlan {
     uint32_t magic, flags;
     int32_t num_pieces;         /* pieces of split sequences (0: no sequence is split) */
     int32_t num_split;          /* split sequences */
+    int32_t num_fix_tasks;      /* groups of <= 8 chunks of the later pieces of split sequences (outputs completed after
+                                   the scan) */
+    int32_t num_ck_tasks;       /* checkpoints inside later pieces (composed after the scan) */
 } KdaPrefillPlan;
 
 /*

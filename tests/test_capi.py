@@ -72,11 +72,18 @@ def test_prefill_plan_host_only():
     pin = _lib.KdaPrefillPlanIn()
     pin.cu_seqlens = ctypes.c_void_p(cu.ctypes.data)
     pin.N, pin.H, pin.ck_every = 4, 8, 128
-    pin.num_cus = 16                                     # 32 chains fill 16 CUs: no sequence is split
+    pin.num_cus = 64                                     # 32 chains, 9 chunks per CU at balance: 64 > 1.25 x 9
     pl = _lib.KdaPrefillPlan()
     assert L.kda355_prefill_plan(ctypes.byref(pin), ctypes.byref(pl), None, 0) == 0
     assert pl.num_chunks == 2 + 0 + 4 + 64 and pl.T == 4396 and pl.ck_rows == 1 + 0 + 2 + 32
-    assert L.kda355_prefill_workspace_bytes(ctypes.byref(pl)) == 0   # the fused kernel keeps chunk operands on chip
+    # the 64-chunk sequence is cut into 4 pieces of 16 (the minimum piece); pieces 2..4 each keep one 16 KiB R tile
+    # per chunk and head, every piece a start / local-state / transition slot per head, and the every-2-chunk rows
+    # inside pieces 2..4 (chunks 18, 20, .., 62: 8 + 8 + 7) a (local state, transition) pair per head
+    assert (pl.num_pieces, pl.num_split, pl.num_chains, pl.num_fix_tasks, pl.num_ck_tasks) == (4, 1, 7, 6, 23)
+    assert L.kda355_prefill_workspace_bytes(ctypes.byref(pl)) == (3 * 4 + 2 * 23) * 8 * 65536 + 48 * 8 * 16384
+    pin.num_cus = 4                                      # 140 chunks per CU: nothing is split, no workspace
+    assert L.kda355_prefill_plan(ctypes.byref(pin), ctypes.byref(pl), None, 0) == 0
+    assert pl.num_pieces == 0 and L.kda355_prefill_workspace_bytes(ctypes.byref(pl)) == 0
     tab = np.zeros(pl.table_words, np.int32)
     assert L.kda355_prefill_plan(ctypes.byref(pin), ctypes.byref(pl), ctypes.c_void_p(tab.ctypes.data), tab.size) == 0
     assert L.kda355_prefill_plan(ctypes.byref(pin), ctypes.byref(pl), ctypes.c_void_p(tab.ctypes.data), 3) == _lib.EINVAL
@@ -106,13 +113,21 @@ def test_prefill_plan_splits_long_sequences():
         return pl, tab
 
     pl, tab = plan([131072], 32, 256)                    # configuration 2: 2048 chunks x 32 heads on 256 CUs
-    assert (pl.num_pieces, pl.num_split, pl.num_chains) == (8, 1, 8)
-    assert pl.workspace_bytes == 3 * 8 * 32 * 128 * 128 * 4
-    final = tab[16:16 + 12 * 8].reshape(8, 12)
+    assert (pl.num_pieces, pl.num_split, pl.num_chains, pl.num_fix_tasks) == (8, 1, 8, 7 * 256 // 8)
+    assert pl.workspace_bytes == 3 * 8 * 32 * 128 * 128 * 4 + 7 * 256 * 32 * 64 * 128 * 2
+    final = tab[20:20 + 13 * 8].reshape(8, 13)
     assert sorted(final[:, 6]) == list(range(0, 2048, 256)) and set(final[:, 1]) == {256}   # first chunk, count
-    assert final[:, 7].tolist().count(2) + final[:, 7].tolist().count(3) == 1                # one last piece
-    pl, _ = plan([4011, 4318, 6249, 7799, 532, 1400, 6787, 7785], 32, 256)   # configuration 1 fills the chip
-    assert pl.num_pieces == 0 and pl.workspace_bytes == 0
+    assert sorted(final[:, 7].tolist()) == [1] * 7 + [4]   # pieces 2..8 run from zero; piece 1 hands over its end
+    lens1 = [4011, 4318, 6249, 7799, 532, 1400, 6787, 7785]   # configuration 1: 256 chains on 256 CUs
+    pl, tab = plan(lens1, 32, 256)
+    # 611 chunks x 32 heads = 77 per CU at balance, but the longest chain has 122 chunks: the long sequences are cut
+    # into pieces of >= 16 chunks, none longer than 64, covering every chunk once
+    counts = tab[20:20 + 13 * pl.num_chains].reshape(-1, 13)
+    assert pl.num_split >= 2 and pl.num_pieces > pl.num_split
+    assert counts[:, 1].max() <= 64 and counts[counts[:, 1] < 16, 1].tolist() in ([], [9]) and counts[:, 1].sum() == 611
+    assert list(counts[:, 1]) == sorted(counts[:, 1], reverse=True)                         # longest first
+    pl, _ = plan(lens1, 32, 64)                          # a quarter of the CUs: 306 chunks per CU, nothing is split
+    assert pl.num_pieces == 0
     pl, _ = plan([1000, 900], 2, 256)                    # 16 chunks: too short to split
     assert pl.num_pieces == 0
     pl, _ = plan([2048, 500], 2, 256)                    # 32 chunks -> 2 pieces of 16
