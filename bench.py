@@ -21,7 +21,7 @@ Roofline: prefill is bound by HBM at these shapes (arithmetic intensity ~120 FLO
 so `roofline` is the HBM fraction of the prefill launch: compulsory bytes (q, k, v, out bf16; g fp32; beta fp32;
 initial + final states fp32) / the launch's average duration from HIP events on the launch stream.  The MFMA fraction
 of the chunked-matmul FLOPs is reported beside it.  `traffic` is the measured HBM bytes per launch from the committed
-rocprofv3 FETCH_SIZE / WRITE_SIZE summary (profiles/prefill_c1_traffic.md), or null.
+rocprofv3 FETCH_SIZE / WRITE_SIZE summary (profiles/prefill_c1_c2_split.md), or null.
 
 `cpu_baseline` times the CPU restatement of the reference's fp32 token recurrence (oracle/, OpenMP over the
 (sequence, head) chains) on the same configuration-1 workload on this host; it is a reported baseline, not the target.
@@ -430,7 +430,7 @@ def main():
     s = c1["ms"] * 1e-3
     achieved = c1["bytes"] / s / 1e9
     tflops = c1["flops"] / s / 1e12
-    traffic = read_traffic("prefill_c1_traffic.md")
+    traffic = read_traffic("prefill_c1_c2_split.md")
     line = {
         "metric": METRIC, "value": round(c1["T"] / s, 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(c1["ms"], 4), "higher_is_better": True, "scaling": "weak",

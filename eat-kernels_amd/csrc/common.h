@@ -30,6 +30,15 @@ __device__ __forceinline__ uint32_t f2bf(float x) {
     return (uint32_t)__builtin_bit_cast(uint16_t, b);
 }
 
+// XCD-aware task order.  Workgroup b of a launch runs on XCD b % 8 (round-robin dispatch over the 8 XCDs of an
+// MI355X); giving each XCD a contiguous range of (sequence, head) tasks keeps the workgroups that touch neighbouring
+// data (neighbouring 64 KiB state blocks, or the row blocks of one state) on one XCD and its L2.
+// Exact bijection of [0, total): XCD x owns [x (total / 8) + min(x, total % 8), ...) of size total / 8 + (x < total % 8).
+__device__ __forceinline__ int xcd_task(int b, int total) {
+    const int x = b & 7, q = total >> 3, r = total & 7;
+    return x * q + (x < r ? x : r) + (b >> 3);
+}
+
 // DPP lane moves inside a row of 16 lanes (quad_perm / row_half_mirror / row_mirror).
 template <int CTRL>
 __device__ __forceinline__ float dpp(float x) {

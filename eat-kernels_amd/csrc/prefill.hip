@@ -866,20 +866,16 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
 
 // Row-block composition used by the scan and the checkpoint compose: out[v][k] = L[v][k] + sum_k' X[v][k'] P[k'][k]
 // in fp32, P as the chunk kernel stores it ([k'][k]).  Row v of the result depends on row v of X alone, so one
-// workgroup of 256 threads takes a block of 16 rows (grid: entries x H x 8): thread t computes row t % 16 of the block
-// at columns 8 (t / 16) .. + 7.  The block's X rows sit in LDS (row stride 132 floats), P is staged whole in LDS.
+// workgroup of 256 threads takes a block of 16 rows (grid: entries x H x 8, the 8 blocks of one state on one XCD so
+// that P is fetched into one L2).  The product runs on fp32 MFMAs (16x16x4): wave w owns the columns 32 w .. 32 w + 31
+// as two 16-column tiles; MFMA step s covers k' = 32 (lane / 16) + s, so a lane's A values (X rows from LDS, row
+// stride 132 floats) are 4 consecutive floats per LDS read and its B values come from P in global memory (L2).
+// Result lane layout: rows 4 (lane / 16) + e of the block, column 32 w + 16 ct + lane % 16.
 constexpr int SC_THREADS = 256;
 constexpr int SC_ROWS = 16;
 constexpr int SC_XS = 132;
-constexpr int SC_SMEM = D * D * 4 + SC_ROWS * SC_XS * 4;
+constexpr int SC_SMEM = SC_ROWS * SC_XS * 4;
 
-__device__ __forceinline__ void stage_P(const float* __restrict__ P, float* sP) {
-    f32x4 r[16];
-#pragma unroll
-    for (int j = 0; j < 16; ++j) r[j] = reinterpret_cast<const f32x4*>(P)[threadIdx.x + SC_THREADS * j];
-#pragma unroll
-    for (int j = 0; j < 16; ++j) reinterpret_cast<f32x4*>(sP)[threadIdx.x + SC_THREADS * j] = r[j];
-}
 // the 16 rows starting at X (row stride D) -> sX
 __device__ __forceinline__ void stage_X(const float* __restrict__ X, float* sX) {
 #pragma unroll
@@ -888,23 +884,33 @@ __device__ __forceinline__ void stage_X(const float* __restrict__ X, float* sX) 
         *reinterpret_cast<f32x4*>(sX + rr * SC_XS + 4 * c4) = *reinterpret_cast<const f32x4*>(X + rr * D + 4 * c4);
     }
 }
-// acc = Lrow[8 kq .. + 7] + sum_k' sX[vr][k'] sP[k'][8 kq .. + 7] (vr = t % 16, kq = t / 16); sX and sP staged and synced
-__device__ __forceinline__ void compose_rows(const float* sX, const float* sP, const float* __restrict__ Lrow,
-                                             float (&acc)[8]) {
-    const int vr = threadIdx.x & 15, kq = threadIdx.x >> 4;
-    const f32x4 l0 = *reinterpret_cast<const f32x4*>(Lrow + 8 * kq), l1 = *reinterpret_cast<const f32x4*>(Lrow + 8 * kq + 4);
+// acc[ct] = Lblk (the block's rows of L) + sX P on this lane's tile elements; sX staged and synced
+__device__ __forceinline__ void compose_rows(const float* sX, const float* __restrict__ P, const float* __restrict__ Lblk,
+                                             f32x4 (&acc)[2]) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, j = lane & 15, kq = lane >> 4;
+    const float* pc = P + (32 * kq) * D + 32 * w + j;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) { acc[j] = l0[j]; acc[4 + j] = l1[j]; }
-    for (int k4 = 0; k4 < D / 4; ++k4) {
-        const f32x4 xv = *reinterpret_cast<const f32x4*>(sX + vr * SC_XS + 4 * k4);
+    for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[ct][e] = Lblk[(4 * kq + e) * D + 32 * w + 16 * ct + j];
+#pragma unroll
+    for (int s4 = 0; s4 < 8; ++s4) {
+        const f32x4 a = *reinterpret_cast<const f32x4*>(sX + j * SC_XS + 32 * kq + 4 * s4);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            const f32x4 p0 = *reinterpret_cast<const f32x4*>(sP + (4 * k4 + e) * D + 8 * kq);
-            const f32x4 p1 = *reinterpret_cast<const f32x4*>(sP + (4 * k4 + e) * D + 8 * kq + 4);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) { acc[j] += xv[e] * p0[j]; acc[4 + j] += xv[e] * p1[j]; }
+            const int s = 4 * s4 + e;
+            acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], pc[s * D], acc[0], 0, 0, 0);
+            acc[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], pc[s * D + 16], acc[1], 0, 0, 0);
         }
     }
+}
+// (entry, head, row block) of this workgroup: XCD-contiguous order keeps an entry-head's 8 blocks on one XCD
+__device__ __forceinline__ void scan_task(int H, int& ei, int& h, int& rb) {
+    const int t = xcd_task(blockIdx.x, gridDim.x);
+    rb = t & 7;
+    const int eh = t >> 3;
+    ei = eh / H;
+    h = eh - ei * H;
 }
 
 // Split sequences: X_1 = the first piece's end state (stored by that piece), X_{p+1} = P_p X_p + S_loc(p) for the
@@ -912,17 +918,16 @@ __device__ __forceinline__ void compose_rows(const float* sX, const float* sP, c
 // (sequence, head, block of 16 state rows).
 __global__ void __launch_bounds__(SC_THREADS) scan_kernel(PfParams p, const int32_t* __restrict__ tab) {
     extern __shared__ __align__(16) unsigned char lds[];
-    float* sP = reinterpret_cast<float*>(lds);
-    float* sX = reinterpret_cast<float*>(lds + D * D * 4);
+    float* sX = reinterpret_cast<float*>(lds);
     const int H = p.H;
-    const int rb = blockIdx.x & 7, eh = blockIdx.x >> 3;
-    const int si = eh / H;
-    const int h = eh - si * H;
+    int si, h, rb;
+    scan_task(H, si, h, rb);
     const int32_t* e = tab + tab[H_OFF_SCAN] + S_WORDS * si;
     const int n = e[S_SEQ], np = e[S_NP], slot0 = e[S_SLOT0];
     const int64_t ws_arr = (int64_t)tab[H_NSLOTS] * H * D * D;
-    const int t = threadIdx.x, vr = t & 15, kq = t >> 4, v = SC_ROWS * rb + vr;
-    stage_X(p.ws + 2 * ws_arr + ((int64_t)(slot0 + 1) * H + h) * D * D + SC_ROWS * rb * D, sX);
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, j = lane & 15, kq = lane >> 4;
+    const int64_t blk = (int64_t)SC_ROWS * rb * D;  // the block's first element in a state
+    stage_X(p.ws + 2 * ws_arr + ((int64_t)(slot0 + 1) * H + h) * D * D + blk, sX);
     float* fin = nullptr;  // the final state's destination (same rules as the chunk walk)
     if (p.flags & KDA355_PF_POOL) {
         const int64_t row = p.state_idx[n];
@@ -932,19 +937,19 @@ __global__ void __launch_bounds__(SC_THREADS) scan_kernel(PfParams p, const int3
     }
     for (int pc = 1; pc < np; ++pc) {
         const int64_t so = ((int64_t)(slot0 + pc) * H + h) * D * D;
-        stage_P(p.ws + ws_arr + so, sP);
-        __syncthreads();
-        float acc[8];
-        compose_rows(sX, sP, p.ws + so + (int64_t)v * D, acc);
-        __syncthreads();  // every thread has read sX and sP
+        __syncthreads();  // sX holds X_pc
+        f32x4 acc[2];
+        compose_rows(sX, p.ws + ws_arr + so, p.ws + so + blk, acc);
+        __syncthreads();  // every wave has read sX
         float* dst = (pc + 1 < np) ? p.ws + 2 * ws_arr + ((int64_t)(slot0 + pc + 1) * H + h) * D * D : fin;
-        const f32x4 a0 = {acc[0], acc[1], acc[2], acc[3]}, a1 = {acc[4], acc[5], acc[6], acc[7]};
-        *reinterpret_cast<f32x4*>(sX + vr * SC_XS + 8 * kq) = a0;
-        *reinterpret_cast<f32x4*>(sX + vr * SC_XS + 8 * kq + 4) = a1;
-        if (dst) {
-            *reinterpret_cast<f32x4*>(dst + (int64_t)v * D + 8 * kq) = a0;
-            *reinterpret_cast<f32x4*>(dst + (int64_t)v * D + 8 * kq + 4) = a1;
-        }
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+            for (int ee = 0; ee < 4; ++ee) {
+                const int rr = 4 * kq + ee, col = 32 * w + 16 * ct + j;
+                sX[rr * SC_XS + col] = acc[ct][ee];
+                if (dst) dst[blk + rr * D + col] = acc[ct][ee];
+            }
     }
 }
 
@@ -952,38 +957,35 @@ __global__ void __launch_bounds__(SC_THREADS) scan_kernel(PfParams p, const int3
 // One workgroup per (task, head, block of 16 state rows); tasks of the checkpoint kind the launch does not use exit.
 __global__ void __launch_bounds__(SC_THREADS) ck_compose_kernel(PfParams p, const int32_t* __restrict__ tab) {
     extern __shared__ __align__(16) unsigned char lds[];
-    float* sP = reinterpret_cast<float*>(lds);
-    float* sX = reinterpret_cast<float*>(lds + D * D * 4);
+    float* sX = reinterpret_cast<float*>(lds);
     const int H = p.H;
-    const int rb = blockIdx.x & 7, eh = blockIdx.x >> 3;
-    const int ti = eh / H;
-    const int h = eh - ti * H;
+    int ti, h, rb;
+    scan_task(H, ti, h, rb);
     const int32_t* e = tab + tab[H_OFF_CKC] + K_WORDS * ti;
     const int ck_mode = (p.flags & KDA355_PF_CK_EVERY) ? 2 : ((p.flags & KDA355_PF_CK_SINGLE) ? 1 : 0);
     if (e[K_KIND] != ck_mode) return;
     const int64_t ws_arr = (int64_t)tab[H_NSLOTS] * H * D * D;
     const float* ws_ck = p.ws + 3 * ws_arr;
-    const int t = threadIdx.x, kq = t >> 4, v = SC_ROWS * rb + (t & 15);
-    stage_X(p.ws + 2 * ws_arr + ((int64_t)e[K_SSLOT] * H + h) * D * D + SC_ROWS * rb * D, sX);
-    stage_P(ws_ck + ((int64_t)(2 * e[K_WSSLOT] + 1) * H + h) * D * D, sP);
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, j = lane & 15, kq = lane >> 4;
+    const int64_t blk = (int64_t)SC_ROWS * rb * D;
+    stage_X(p.ws + 2 * ws_arr + ((int64_t)e[K_SSLOT] * H + h) * D * D + blk, sX);
     __syncthreads();
-    float acc[8];
-    compose_rows(sX, sP, ws_ck + ((int64_t)(2 * e[K_WSSLOT]) * H + h) * D * D + (int64_t)v * D, acc);
+    f32x4 acc[2];
+    compose_rows(sX, ws_ck + ((int64_t)(2 * e[K_WSSLOT] + 1) * H + h) * D * D,
+                 ws_ck + ((int64_t)(2 * e[K_WSSLOT]) * H + h) * D * D + blk, acc);
     const int64_t rr = p.ck_idx[e[K_CKIDX]];
     if (rr < 0 || rr >= p.ck_slots) return;
-    const int64_t off = rr * p.ck_ss + (int64_t)h * D * D + (int64_t)v * D + 8 * kq;
-    if (p.ck_bf16) {
-        u32x4 b;
-        b.x = f2bf(acc[0]) | (f2bf(acc[1]) << 16);
-        b.y = f2bf(acc[2]) | (f2bf(acc[3]) << 16);
-        b.z = f2bf(acc[4]) | (f2bf(acc[5]) << 16);
-        b.w = f2bf(acc[6]) | (f2bf(acc[7]) << 16);
-        *reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(p.ck_pool) + off) = b;
-    } else {
-        float* dst = reinterpret_cast<float*>(p.ck_pool) + off;
-        *reinterpret_cast<f32x4*>(dst) = f32x4{acc[0], acc[1], acc[2], acc[3]};
-        *reinterpret_cast<f32x4*>(dst + 4) = f32x4{acc[4], acc[5], acc[6], acc[7]};
-    }
+    const int64_t off = rr * p.ck_ss + (int64_t)h * D * D + blk;
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+        for (int ee = 0; ee < 4; ++ee) {
+            const int64_t o = off + (4 * kq + ee) * D + 32 * w + 16 * ct + j;
+            if (p.ck_bf16)
+                reinterpret_cast<uint16_t*>(p.ck_pool)[o] = (uint16_t)f2bf(acc[ct][ee]);
+            else
+                reinterpret_cast<float*>(p.ck_pool)[o] = acc[ct][ee];
+        }
 }
 
 // The outputs of later pieces: O = partial (fp16, as the chunk kernel left it in `out`) + scale R S_start, stored as

@@ -23,15 +23,6 @@ __device__ __forceinline__ float sum32(float x) {
     return x + __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(x), 0x401F));
 }
 
-// XCD-aware task order.  Workgroup b of a launch runs on XCD b % 8 (round-robin dispatch over the 8 XCDs of an
-// MI355X); giving each XCD a contiguous range of (sequence, head) tasks keeps the workgroups that touch neighbouring
-// 64 KiB state blocks on one XCD.  On page pools (state blocks not 64 KiB aligned) this is worth ~6% of bandwidth.
-// Exact bijection of [0, total): XCD x owns [x (total / 8) + min(x, total % 8), ...) of size total / 8 + (x < total % 8).
-__device__ __forceinline__ int xcd_task(int b, int total) {
-    const int x = b & 7, q = total >> 3, r = total & 7;
-    return x * q + (x < r ? x : r) + (b >> 3);
-}
-
 struct Walker {
     int w, half, c;  // wave, half wave, column group (columns 4c .. 4c + 3)
     __device__ __forceinline__ explicit Walker(int tid) : w(tid >> 6), half((tid >> 5) & 1), c(tid & 31) {}
