@@ -75,8 +75,8 @@ constexpr uint32_t PLAN_MAGIC = 0x4b443535u;  // "KD55"
 // Table: a header, then four lists.  The chain list holds every piece run by the chunk kernel (a whole sequence, the
 // first piece of a split sequence from its true start state, or a later piece from S = 0 carrying its transition);
 // the scan list holds the split sequences (the start states of their later pieces and their final states are composed
-// after the chunk kernel); the fixup list holds one task per group of up to 8 chunks of a later piece (their outputs
-// get R S_start added); the compose list holds the checkpoints inside later pieces (row = P S_start + S_local).
+// after the chunk kernel); the fixup list holds one task per group of up to FX_GROUP chunks of a later piece (their
+// outputs get R S_start added); the compose list holds the checkpoints inside later pieces (row = P S_start + S_local).
 enum { H_MAGIC = 0, H_N, H_T, H_NCHUNK, H_EVERY, H_CKROWS, H_OFF_FINAL, H_NFINAL, H_OFF_FIX, H_NFIX, H_OFF_SCAN,
        H_NSCAN, H_NSLOTS, H_OFF_CKC, H_NCKC, H_NRSLOTS, H_NCKSLOTS, H_WORDS = 20 };
 // one piece entry: chunks [0, nch) starting at sequence chunk `first` of sequence n, tokens [t_start, t_start + len)
@@ -990,15 +990,20 @@ __global__ void __launch_bounds__(SC_THREADS) ck_compose_kernel(PfParams p, cons
 
 // The outputs of later pieces: O = partial (fp16, as the chunk kernel left it in `out`) + scale R S_start, stored as
 // bf16.  One workgroup of 256 threads (4 waves) per (group of up to FX_GROUP chunks of one piece, head): the start
-// state is read once per group.  Wave w produces value columns 32 w .. 32 w + 31 on 16x16x32 f16 MFMAs with the
-// state as the A operand, so the result tile is transposed (lane (g, m): token m); the A rows are ordered so that the
-// two tiles of a lane cover the 8 consecutive values 32 w + 8 g .. + 7 (one 16-byte load and store per token).
-// Memory accesses go through buffer descriptors that end at the group's last token and last R tile: tokens past them
-// (the tail of a partial last chunk, the prefetch past the last chunk) read zeros and their stores are dropped, so no
-// access sits under a branch.
+// state goes to LDS once per group (fp16 [v][k], rows of 17 16-byte slots, slot s of row v stored at s ^ 4 (v / 32)
+// so that the A-fragment reads below hit 16 distinct slots).  Wave w takes tokens 16 w .. 16 w + 15 of every chunk:
+// 16x16x32 f16 MFMAs with the state as the A operand (tile vt, A row i <-> value 32 (i / 4) + 4 vt + i % 4) and the R
+// rows as the B operand, so lane (g, m) ends with the 32 consecutive values 32 g .. 32 g + 31 of token 16 w + m (four
+// 16-byte loads of the partial and four stores).  Each chunk's R rows and partials are loaded one chunk ahead, through
+// buffer descriptors that end at the group's last token and last R tile: rows past them read zeros and their stores
+// are dropped, so no access sits under a branch.
 constexpr int FX_THREADS = 256;
-constexpr int FX_GROUP = 8;
+constexpr int FX_GROUP = 2;  // measured: 2 chunks per group beats 1, 4 and 8 (start-state reads vs. tail)
+constexpr int FX_ROW = 17 * 16;        // bytes per fp16 state row in LDS
+constexpr int FX_SMEM = D * FX_ROW;
+__device__ __forceinline__ int fx_slot(int v, int s) { return v * FX_ROW + 16 * (s ^ (4 * (v >> 5))); }
 __global__ void __launch_bounds__(FX_THREADS) fixup_kernel(PfParams p, const int32_t* __restrict__ tab) {
+    extern __shared__ __align__(16) unsigned char lds[];
     const int H = p.H;
     const int ti = blockIdx.x / H;
     const int h = blockIdx.x - ti * H;
@@ -1009,65 +1014,68 @@ __global__ void __launch_bounds__(FX_THREADS) fixup_kernel(PfParams p, const int
     const half_t* R0 = reinterpret_cast<const half_t*>(p.ws + 3 * ws_arr + (int64_t)tab[H_NCKSLOTS] * 2 * H * D * D) +
                        ((int64_t)e[X_RSLOT] * H + h) * (64 * D);                  // [token][k], chunk c at + c H 64 D
     const int64_t rstep = (int64_t)H * 64 * D;
-    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, m = lane & 15, g = lane >> 4;
-    f16x8 Y[2][4];  // S_start rows: tile vt, A row m <-> value 32 w + 8 (m / 4) + 4 vt + m % 4; k = 32 ks + 8 g .. + 7
+    {  // S_start -> LDS fp16: thread t converts 4 values at a time (v = i / 32, k = 4 (i % 32))
+        f32x4 x[16];
 #pragma unroll
-    for (int vt = 0; vt < 2; ++vt)
+        for (int j = 0; j < 16; ++j) x[j] = reinterpret_cast<const f32x4*>(Sst)[threadIdx.x + FX_THREADS * j];
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-            const float* src = Sst + (32 * w + 8 * (m >> 2) + 4 * vt + (m & 3)) * D + 32 * ks + 8 * g;
-            const f32x4 a = *reinterpret_cast<const f32x4*>(src), b = *reinterpret_cast<const f32x4*>(src + 4);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) { Y[vt][ks][j] = (half_t)a[j]; Y[vt][ks][4 + j] = (half_t)b[j]; }
+        for (int j = 0; j < 16; ++j) {
+            const int i = threadIdx.x + FX_THREADS * j, v = i >> 5, c4 = i & 31;
+            const f16x4 hv = {(half_t)x[j][0], (half_t)x[j][1], (half_t)x[j][2], (half_t)x[j][3]};
+            *reinterpret_cast<f16x4*>(lds + fx_slot(v, c4 >> 1) + 8 * (c4 & 1)) = hv;
         }
+    }
+    __syncthreads();
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, m = lane & 15, g = lane >> 4;
     const int rs = p.out_rs * 2;  // bytes per output row
+    const int tok = 16 * w + m;   // this lane's token inside a chunk
     const __amdgpu_buffer_rsrc_t ob = __builtin_amdgcn_make_buffer_rsrc(
         p.out + (int64_t)tstart * p.out_rs + (int64_t)h * D, (short)0, (L - 1) * rs + D * 2, 0x00020000);
     const int nchk = (L + 63) >> 6;
     const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<half_t*>(R0), (short)0, (int)((nchk - 1) * rstep * 2 + 64 * D * 2), 0x00020000);
-    const int col = (32 * w + 8 * g) * 2;
-    const int roff = (m * D + 8 * g) * 2;
-    // one chunk's operands: R rows (token 16 tt + m, k = 32 ks + 8 g .. + 7) and the fp16 partial outputs; a chunk
-    // past the group reads zeros
-    struct Ops { f16x8 X[4][4]; f16x8 part[4]; };
+    const int roff = (tok * D + 8 * g) * 2, col = 64 * g;
+    // one chunk's operands of this lane: R row tok (k = 32 ks + 8 g .. + 7) and the partial values 32 g .. + 31
+    struct Ops { f16x8 X[4]; f16x8 part[4]; };
     auto load = [&](Ops& b, int c0) {
         const int rbase = (int)((c0 >> 6) * rstep * 2) + roff;
+        const int obase = (c0 + tok) * rs + col;
 #pragma unroll
-        for (int tt = 0; tt < 4; ++tt) {
-#pragma unroll
-            for (int ks = 0; ks < 4; ++ks)
-                b.X[tt][ks] = __builtin_bit_cast(
-                    f16x8, __builtin_amdgcn_raw_buffer_load_b128(rb, rbase + (16 * tt * D + 32 * ks) * 2, 0, 0));
-            b.part[tt] = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(ob, (c0 + 16 * tt + m) * rs + col, 0, 0));
+        for (int i = 0; i < 4; ++i) {
+            b.X[i] = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(rb, rbase + 64 * i, 0, 0));
+            b.part[i] = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(ob, obase + 16 * i, 0, 0));
         }
     };
     // wait for b's loads here (later loads stay in flight) and keep the next chunk's loads above this point
     auto ready = [&](Ops& b) {
 #pragma unroll
-        for (int tt = 0; tt < 4; ++tt) {
-#pragma unroll
-            for (int ks = 0; ks < 4; ++ks) asm volatile("" : "+v"(b.X[tt][ks])::"memory");
-            asm volatile("" : "+v"(b.part[tt])::"memory");
+        for (int i = 0; i < 4; ++i) {
+            asm volatile("" : "+v"(b.X[i])::"memory");
+            asm volatile("" : "+v"(b.part[i])::"memory");
         }
     };
     auto finish = [&](const Ops& b, int c0) {
+        f32x4 acc[8];
 #pragma unroll
-        for (int tt = 0; tt < 4; ++tt) {
-            f32x4 acc[2];
+        for (int vt = 0; vt < 8; ++vt) {
+            acc[vt] = f32x4{0.f, 0.f, 0.f, 0.f};
+            const int v = 32 * (m >> 2) + 4 * vt + (m & 3);
 #pragma unroll
-            for (int vt = 0; vt < 2; ++vt) {
-                acc[vt] = f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int ks = 0; ks < 4; ++ks)
+                acc[vt] = mfma32(*reinterpret_cast<const f16x8*>(lds + fx_slot(v, 4 * ks + g)), b.X[ks], acc[vt]);
+        }
+        const int obase = (c0 + tok) * rs + col;
 #pragma unroll
-                for (int ks = 0; ks < 4; ++ks) acc[vt] = mfma32(Y[vt][ks], b.X[tt][ks], acc[vt]);
-            }
-            const f16x8& part = b.part[tt];
+        for (int i = 0; i < 4; ++i) {  // values 32 g + 8 i .. + 7 = tiles 2 i and 2 i + 1
+            const f16x8& pt = b.part[i];
+            const f32x4& a0 = acc[2 * i];
+            const f32x4& a1 = acc[2 * i + 1];
             u32x4 r;
-            r.x = f2bf((float)part[0] + p.scale * acc[0][0]) | (f2bf((float)part[1] + p.scale * acc[0][1]) << 16);
-            r.y = f2bf((float)part[2] + p.scale * acc[0][2]) | (f2bf((float)part[3] + p.scale * acc[0][3]) << 16);
-            r.z = f2bf((float)part[4] + p.scale * acc[1][0]) | (f2bf((float)part[5] + p.scale * acc[1][1]) << 16);
-            r.w = f2bf((float)part[6] + p.scale * acc[1][2]) | (f2bf((float)part[7] + p.scale * acc[1][3]) << 16);
-            __builtin_amdgcn_raw_buffer_store_b128(r, ob, (c0 + 16 * tt + m) * rs + col, 0, 0);
+            r.x = f2bf((float)pt[0] + p.scale * a0[0]) | (f2bf((float)pt[1] + p.scale * a0[1]) << 16);
+            r.y = f2bf((float)pt[2] + p.scale * a0[2]) | (f2bf((float)pt[3] + p.scale * a0[3]) << 16);
+            r.z = f2bf((float)pt[4] + p.scale * a1[0]) | (f2bf((float)pt[5] + p.scale * a1[1]) << 16);
+            r.w = f2bf((float)pt[6] + p.scale * a1[2]) | (f2bf((float)pt[7] + p.scale * a1[3]) << 16);
+            __builtin_amdgcn_raw_buffer_store_b128(r, ob, obase + 16 * i, 0, 0);
         }
     };
     // each chunk's loads are issued one chunk ahead; the loop is unrolled whole (straight-line waits)
@@ -1119,7 +1127,7 @@ hipError_t launch_ck_compose(const PfParams& p, int entries, hipStream_t s) {
     return launch_composer(ck_compose_kernel, p, entries, s, attr_set);
 }
 hipError_t launch_fixup(const PfParams& p, int entries, hipStream_t s) {
-    hipLaunchKernelGGL(fixup_kernel, dim3(entries * p.H), dim3(FX_THREADS), 0, s, p, p.tab);
+    hipLaunchKernelGGL(fixup_kernel, dim3(entries * p.H), dim3(FX_THREADS), FX_SMEM, s, p, p.tab);
     return hipGetLastError();
 }
 

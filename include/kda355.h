@@ -191,7 +191,7 @@ typedef struct KdaPrefillPlan {
     uint32_t magic, flags;
     int32_t num_pieces;         /* pieces of split sequences (0: no sequence is split) */
     int32_t num_split;          /* split sequences */
-    int32_t num_fix_tasks;      /* groups of <= 8 chunks of the later pieces of split sequences (outputs completed after
+    int32_t num_fix_tasks;      /* groups of <= 2 chunks of the later pieces of split sequences (outputs completed after
                                    the scan) */
     int32_t num_ck_tasks;       /* checkpoints inside later pieces (composed after the scan) */
 } KdaPrefillPlan;

@@ -79,7 +79,7 @@ def test_prefill_plan_host_only():
     # the 64-chunk sequence is cut into 4 pieces of 16 (the minimum piece); pieces 2..4 each keep one 16 KiB R tile
     # per chunk and head, every piece a start / local-state / transition slot per head, and the every-2-chunk rows
     # inside pieces 2..4 (chunks 18, 20, .., 62: 8 + 8 + 7) a (local state, transition) pair per head
-    assert (pl.num_pieces, pl.num_split, pl.num_chains, pl.num_fix_tasks, pl.num_ck_tasks) == (4, 1, 7, 6, 23)
+    assert (pl.num_pieces, pl.num_split, pl.num_chains, pl.num_fix_tasks, pl.num_ck_tasks) == (4, 1, 7, 24, 23)
     assert L.kda355_prefill_workspace_bytes(ctypes.byref(pl)) == (3 * 4 + 2 * 23) * 8 * 65536 + 48 * 8 * 16384
     pin.num_cus = 4                                      # 140 chunks per CU: nothing is split, no workspace
     assert L.kda355_prefill_plan(ctypes.byref(pin), ctypes.byref(pl), None, 0) == 0
@@ -113,7 +113,7 @@ def test_prefill_plan_splits_long_sequences():
         return pl, tab
 
     pl, tab = plan([131072], 32, 256)                    # configuration 2: 2048 chunks x 32 heads on 256 CUs
-    assert (pl.num_pieces, pl.num_split, pl.num_chains, pl.num_fix_tasks) == (8, 1, 8, 7 * 256 // 8)
+    assert (pl.num_pieces, pl.num_split, pl.num_chains, pl.num_fix_tasks) == (8, 1, 8, 7 * 256 // 2)
     assert pl.workspace_bytes == 3 * 8 * 32 * 128 * 128 * 4 + 7 * 256 * 32 * 64 * 128 * 2
     final = tab[20:20 + 13 * 8].reshape(8, 13)
     assert sorted(final[:, 6]) == list(range(0, 2048, 256)) and set(final[:, 1]) == {256}   # first chunk, count
