@@ -172,18 +172,33 @@ __device__ __forceinline__ u32x4 bload16(__amdgpu_buffer_rsrc_t rs, int off) {
     return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
 }
 
-// One chunk's raw row slice for this thread (row r, channels 16 cb .. 16 cb + 15); rows >= L read as zeros.
-template <bool RG>
-__device__ __forceinline__ void load_row(const PfParams& p, int h, int t0, int L, int r, int cb, bool RB, RawRow& x) {
+// One chunk's raw row slice for this thread (row r, channels 16 cb .. 16 cb + 15); rows >= L read as zeros.  The
+// next chunk's slice is issued in three parts in three phases (q and k; v and beta; the gate): the 80 KiB a chunk
+// loads take ~1.3 k cycles of the CU's address unit, and issued at once they stall the waves that issue them.
+__device__ __forceinline__ void load_row_qk(const PfParams& p, int h, int t0, int L, int r, int cb, RawRow& x) {
     const int64_t o = (int64_t)t0 * p.qkv_rs + (int64_t)h * D;
     const int64_t qp = p.qkv_rs * 2;
     const int qo = r * (int)qp + 32 * cb;
     const __amdgpu_buffer_rsrc_t rq = rows_rsrc(p.q + o, L, qp, 256);
     const __amdgpu_buffer_rsrc_t rk = rows_rsrc(p.k + o, L, qp, 256);
-    const __amdgpu_buffer_rsrc_t rv = rows_rsrc(p.v + o, L, qp, 256);
     x.q[0] = bload16(rq, qo); x.q[1] = bload16(rq, qo + 16);
     x.k[0] = bload16(rk, qo); x.k[1] = bload16(rk, qo + 16);
+}
+__device__ __forceinline__ void load_row_vb(const PfParams& p, int h, int t0, int L, int r, int cb, bool RB, RawRow& x) {
+    const int64_t o = (int64_t)t0 * p.qkv_rs + (int64_t)h * D;
+    const int64_t qp = p.qkv_rs * 2;
+    const int qo = r * (int)qp + 32 * cb;
+    const __amdgpu_buffer_rsrc_t rv = rows_rsrc(p.v + o, L, qp, 256);
     x.v[0] = bload16(rv, qo); x.v[1] = bload16(rv, qo + 16);
+    const int es = RB ? 2 : 4;
+    const int64_t bp = p.beta_rs * es;
+    const __amdgpu_buffer_rsrc_t rb =
+        rows_rsrc(reinterpret_cast<const unsigned char*>(p.beta) + ((int64_t)t0 * p.beta_rs + h) * es, L, bp, es);
+    x.beta = RB ? (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rb, r * (int)bp, 0, 0)
+                : __builtin_amdgcn_raw_buffer_load_b32(rb, r * (int)bp, 0, 0);
+}
+template <bool RG>
+__device__ __forceinline__ void load_row_g(const PfParams& p, int h, int t0, int L, int r, int cb, RawRow& x) {
     const int64_t go = (int64_t)t0 * p.g_rs + (int64_t)h * D;
     if (RG) {
         const int64_t gp = p.g_rs * 2;
@@ -198,12 +213,12 @@ __device__ __forceinline__ void load_row(const PfParams& p, int h, int t0, int L
         x.g[0] = bload16(rg, off); x.g[1] = bload16(rg, off + 16);
         x.g[2] = bload16(rg, off + 32); x.g[3] = bload16(rg, off + 48);
     }
-    const int es = RB ? 2 : 4;
-    const int64_t bp = p.beta_rs * es;
-    const __amdgpu_buffer_rsrc_t rb =
-        rows_rsrc(reinterpret_cast<const unsigned char*>(p.beta) + ((int64_t)t0 * p.beta_rs + h) * es, L, bp, es);
-    x.beta = RB ? (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rb, r * (int)bp, 0, 0)
-                : __builtin_amdgcn_raw_buffer_load_b32(rb, r * (int)bp, 0, 0);
+}
+template <bool RG>
+__device__ __forceinline__ void load_row(const PfParams& p, int h, int t0, int L, int r, int cb, bool RB, RawRow& x) {
+    load_row_qk(p, h, t0, L, r, cb, x);
+    load_row_vb(p, h, t0, L, r, cb, RB, x);
+    load_row_g<RG>(p, h, t0, L, r, cb, x);
 }
 
 __device__ __forceinline__ void unpack16(const u32x4 (&w)[2], float (&f)[16]) {
@@ -615,8 +630,8 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
         }
         lds_barrier();
         // ================= P5: Q~, Kd^T, beta v into their walk layouts (raw threads)
-        // the next chunk's rows: issued here, consumed at the next P0 (their registers are free during P1..P4)
-        if (cl + 1 < nch) load_row<RG>(p, h, t0 + 64, min(64, len - 64 * (cl + 1)), r, cb, RB, nx);
+        // the next chunk's q, k rows: issued here, consumed at the next P0 (their registers are free during P1..P4)
+        if (cl + 1 < nch) load_row_qk(p, h, t0 + 64, min(64, len - 64 * (cl + 1)), r, cb, nx);
         float qfi[16], kfj[16], vf[16];
         {
             const u32x4* vs = reinterpret_cast<const u32x4*>(lds + LDS_W + r * (2 * RS16) + 32 * cb);
@@ -661,6 +676,7 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
         }
         lds_barrier();
         // ================= P6: W and U by block forward substitution (wave w: channel / value tile w)
+        if (cl + 1 < nch) load_row_vb(p, h, t0 + 64, min(64, len - 64 * (cl + 1)), r, cb, RB, nx);
         f32x4 Ur[4];
         {
             const int c = 16 * w + m;
@@ -700,6 +716,7 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
         }
         lds_barrier();
         // ================= P7: the walk
+        if (cl + 1 < nch) load_row_g<RG>(p, h, t0 + 64, min(64, len - 64 * (cl + 1)), r, cb, nx);
         if (fix) {  // S <- (diag(d) - Kd^T W) S + Kd^T U and P <- (diag(d) - Kd^T W) P, sharing every A fragment
             f16x8 SB[4], PB[4];
 #pragma unroll
