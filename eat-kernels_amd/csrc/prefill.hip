@@ -112,6 +112,17 @@ __device__ __forceinline__ int pos64(int q) { return (q & 32) + pos32(q & 31); }
 // permuted by slot ^= cb >> 1.  The eight raw threads of a row then write 16-byte slots on distinct banks (unswizzled,
 // segments cb and cb + 4 sit 256 bytes apart and their writes conflict: 128 vs 55 cycles per wave instruction).
 __device__ __forceinline__ int swz(int c) { return c ^ (((c >> 5) & 3) << 2); }
+// hi + lo bf16 split of two fp32 values, each pair packed in one word (element 0 in the low half): hi = RNE(x),
+// lo = RNE(x - hi), one v_cvt_pk_bf16_f32 per pair
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void split_bf16x2(float x0, float x1, uint32_t& hi, uint32_t& lo) {
+    hi = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{x0, x1}, bf16x2));
+    const float h0 = __uint_as_float(hi << 16), h1 = __uint_as_float(hi & 0xffff0000u);
+    lo = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{x0 - h0, x1 - h1}, bf16x2));
+}
+__device__ __forceinline__ bf16x8 as_bf16x8(const uint32_t (&w)[4]) {
+    return __builtin_bit_cast(bf16x8, u32x4{w[0], w[1], w[2], w[3]});
+}
 // 2^x (v_exp_f32)
 __device__ __forceinline__ float exp2_(float x) { return __builtin_amdgcn_exp2f(x); }
 
@@ -518,27 +529,28 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
                 const int c0 = 32 * s + 8 * g;
-                bf16x8 kah, kal, qah, qal, kbh, kbl;
+                uint32_t kah[4], kal[4], qah[4], qal[4], kbh[4], kbl[4];  // bf16x8 fragments as 4 packed pairs
 #pragma unroll
                 for (int hf = 0; hf < 2; ++hf) {
                     const f32x4 ka = *reinterpret_cast<const f32x4*>(&sKA[i * RS32 + swz(c0 + 4 * hf)]);
                     const f32x4 qa = *reinterpret_cast<const f32x4*>(&sQA[i * RS32 + swz(c0 + 4 * hf)]);
                     const f32x4 kb = *reinterpret_cast<const f32x4*>(&sKB[i * RS32 + swz(c0 + 4 * hf)]);
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const int e = 4 * hf + j;
-                        const __bf16 a1 = (__bf16)ka[j], a2 = (__bf16)qa[j], a3 = (__bf16)kb[j];
-                        kah[e] = a1; kal[e] = (__bf16)(ka[j] - (float)a1);
-                        qah[e] = a2; qal[e] = (__bf16)(qa[j] - (float)a2);
-                        kbh[e] = a3; kbl[e] = (__bf16)(kb[j] - (float)a3);
+                    for (int j = 0; j < 2; ++j) {
+                        const int e = 2 * hf + j;
+                        split_bf16x2(ka[2 * j], ka[2 * j + 1], kah[e], kal[e]);
+                        split_bf16x2(qa[2 * j], qa[2 * j + 1], qah[e], qal[e]);
+                        split_bf16x2(kb[2 * j], kb[2 * j + 1], kbh[e], kbl[e]);
                     }
                 }
-                akk = mfma32bf(kah, kbh, akk);
-                akk = mfma32bf(kah, kbl, akk);
-                akk = mfma32bf(kal, kbh, akk);
-                aqk = mfma32bf(kbh, qah, aqk);  // transposed: lane (g, m) holds row 16 I + m, columns 16 I + 4 g .. + 3
-                aqk = mfma32bf(kbl, qah, aqk);
-                aqk = mfma32bf(kbh, qal, aqk);
+                const bf16x8 Kah = as_bf16x8(kah), Kal = as_bf16x8(kal), Qah = as_bf16x8(qah), Qal = as_bf16x8(qal);
+                const bf16x8 Kbh = as_bf16x8(kbh), Kbl = as_bf16x8(kbl);
+                akk = mfma32bf(Kah, Kbh, akk);
+                akk = mfma32bf(Kah, Kbl, akk);
+                akk = mfma32bf(Kal, Kbh, akk);
+                aqk = mfma32bf(Kbh, Qah, aqk);  // transposed: lane (g, m) holds row 16 I + m, columns 16 I + 4 g .. + 3
+                aqk = mfma32bf(Kbl, Qah, aqk);
+                aqk = mfma32bf(Kbh, Qal, aqk);
             }
             f32x4 lt;
             f16x4 aq;
