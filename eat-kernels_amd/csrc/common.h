@@ -30,6 +30,12 @@ __device__ __forceinline__ uint32_t f2bf(float x) {
     return (uint32_t)__builtin_bit_cast(uint16_t, b);
 }
 
+// two fp32 -> packed bf16 pair (x0 in the low half), round to nearest even: one v_cvt_pk_bf16_f32
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t f2bf2(float x0, float x1) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{x0, x1}, bf16x2_t));
+}
+
 // XCD-aware task order.  Workgroup b of a launch runs on XCD b % 8 (round-robin dispatch over the 8 XCDs of an
 // MI355X); giving each XCD a contiguous range of (sequence, head) tasks keeps the workgroups that touch neighbouring
 // data (neighbouring 64 KiB state blocks, or the row blocks of one state) on one XCD and its L2.

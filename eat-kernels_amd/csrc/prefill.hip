@@ -114,11 +114,10 @@ __device__ __forceinline__ int pos64(int q) { return (q & 32) + pos32(q & 31); }
 __device__ __forceinline__ int swz(int c) { return c ^ (((c >> 5) & 3) << 2); }
 // hi + lo bf16 split of two fp32 values, each pair packed in one word (element 0 in the low half): hi = RNE(x),
 // lo = RNE(x - hi), one v_cvt_pk_bf16_f32 per pair
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ void split_bf16x2(float x0, float x1, uint32_t& hi, uint32_t& lo) {
-    hi = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{x0, x1}, bf16x2));
+    hi = f2bf2(x0, x1);
     const float h0 = __uint_as_float(hi << 16), h1 = __uint_as_float(hi & 0xffff0000u);
-    lo = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{x0 - h0, x1 - h1}, bf16x2));
+    lo = f2bf2(x0 - h0, x1 - h1);
 }
 __device__ __forceinline__ bf16x8 as_bf16x8(const uint32_t (&w)[4]) {
     return __builtin_bit_cast(bf16x8, u32x4{w[0], w[1], w[2], w[3]});
@@ -460,6 +459,10 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
                 unpack16(a, qf);
                 unpack16(b, kf);
             }
+            if (NORM) {  // uniform: calls without in-kernel normalization skip the 32 multiplies by 1
+#pragma unroll
+                for (int c = 0; c < 16; ++c) { kf[c] *= rk; qf[c] *= rq; }
+            }
             const int I = r >> 4, mr = 16 * I + 7;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
@@ -470,10 +473,9 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
                     const int c = 4 * i + j;
                     const float d = a[j] - b[j];  // Gamma_r - Gamma_m (the segment offset cancels)
                     const float fi = exp2_(d), fj = exp2_(-d);
-                    const float kh = kf[c] * rk;
-                    kfi[c] = kh * fi;
-                    kfj[c] = kh * fj;
-                    qfi[c] = qf[c] * rq * fi;
+                    kfi[c] = kf[c] * fi;
+                    kfj[c] = kf[c] * fj;
+                    qfi[c] = qf[c] * fi;
                 }
             }
 #pragma unroll
@@ -843,8 +845,7 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
                     if (s <= (it >> 1))
                         acc = mfma32(VB[s], *reinterpret_cast<const f16x8*>(&sAq[(16 * it + m) * RS16S + 32 * s + 8 * g]),
                                      acc);
-                const u32x2 o = {f2bf(p.scale * acc[0]) | (f2bf(p.scale * acc[1]) << 16),
-                                 f2bf(p.scale * acc[2]) | (f2bf(p.scale * acc[3]) << 16)};
+                const u32x2 o = {f2bf2(p.scale * acc[0], p.scale * acc[1]), f2bf2(p.scale * acc[2], p.scale * acc[3])};
                 *reinterpret_cast<u32x2*>(lds + LDS_A + (16 * it + m) * (4 * RS32) + 64 * w + 8 * g) = o;
             }
 #pragma unroll
