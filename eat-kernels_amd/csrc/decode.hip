@@ -48,7 +48,7 @@ struct DecParams {
 __device__ __forceinline__ bool slot_ok(int64_t r, int lo, int64_t n) { return r >= lo && r < n; }
 
 // SINGLE: one token per sequence (plain decode), S = 1 known at compile time.
-template <bool SPEC, bool SINGLE>
+template <bool SPEC, bool SINGLE, bool NT>
 __global__ void __launch_bounds__(DC_THREADS) decode_kernel(DecParams p) {
     // dynamic LDS: conv weights [4][384] fp32 | conv + SiLU outputs [S][384] fp32 | bf16-rounded outputs [S][128] fp32
     // | per-half-wave sums of squares [S][16] fp32 | window [3 + S][384] bf16
@@ -194,10 +194,10 @@ __global__ void __launch_bounds__(DC_THREADS) decode_kernel(DecParams p) {
         if (SPEC) {
             const int64_t wr = __builtin_amdgcn_readlane(wr_l, t);
             const bool ok = slot_ok(wr, 1, p.ssm_slots);
-            store_state(wk, p.ssm + (ok ? wr : 0) * p.ssm_ss + (int64_t)h * D * D, st, ok);
+            store_state<NT>(wk, p.ssm + (ok ? wr : 0) * p.ssm_ss + (int64_t)h * D * D, st, ok);
         }
     }
-    if (!SPEC) store_state(wk, p.ssm + rd * p.ssm_ss + (int64_t)h * D * D, st);
+    if (!SPEC) store_state<NT>(wk, p.ssm + rd * p.ssm_ss + (int64_t)h * D * D, st);
     lds_barrier();
     // ---- gated RMSNorm of every token's 128 outputs: y = bf16(o) rsqrt(mean(bf16(o)^2) + eps) nw sigmoid(og)
 #pragma unroll
@@ -278,12 +278,12 @@ extern "C" int kda355_decode_launch(const KdaDecodeArgs* a, kda355_stream_t stre
     const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const size_t lds = ((size_t)(4 + a->S) * DC_CH + (size_t)a->S * (D + 16)) * sizeof(float) +
                        (size_t)(3 + a->S) * DC_CH * sizeof(uint16_t);
-    if (spec)
-        hipLaunchKernelGGL((decode_kernel<true, false>), dim3(a->B * a->H), dim3(DC_THREADS), lds, s, p);
-    else if (a->S == 1)
-        hipLaunchKernelGGL((decode_kernel<false, true>), dim3(a->B * a->H), dim3(DC_THREADS), lds, s, p);
-    else
-        hipLaunchKernelGGL((decode_kernel<false, false>), dim3(a->B * a->H), dim3(DC_THREADS), lds, s, p);
+    // streaming stores when the launch writes more state than the MALL holds (WK_STREAM_BYTES)
+    const bool nt = (long long)a->B * (spec ? a->S : 1) * a->H * D * D * 4 > WK_STREAM_BYTES;
+    void (*kernel)(DecParams) = spec ? (nt ? decode_kernel<true, false, true> : decode_kernel<true, false, false>)
+                                : a->S == 1 ? (nt ? decode_kernel<false, true, true> : decode_kernel<false, true, false>)
+                                            : (nt ? decode_kernel<false, false, true> : decode_kernel<false, false, false>);
+    hipLaunchKernelGGL(kernel, dim3(a->B * a->H), dim3(DC_THREADS), lds, s, p);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         set_error("decode: launch failed: %s", hipGetErrorString(e));

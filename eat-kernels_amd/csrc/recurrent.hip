@@ -41,7 +41,7 @@ __device__ __forceinline__ bool row_ok(int64_t r, int64_t lo, int64_t slots) { r
 // the final state written back, REC_PER_TOKEN the state after every token written (spec verify).
 enum { REC_SINGLE = 0, REC_MULTI = 1, REC_PER_TOKEN_MODE = 2 };
 
-template <bool RAW_GATE, bool RAW_BETA, bool NORM, int MODE>
+template <bool RAW_GATE, bool RAW_BETA, bool NORM, int MODE, bool NT>
 __global__ void __launch_bounds__(REC_THREADS) recurrent_kernel(RecParams p) {
     constexpr bool PER_TOKEN = MODE == REC_PER_TOKEN_MODE;
     // (sequence, head) of this workgroup, kept in SGPRs: buffer descriptors built from them must be wave-uniform
@@ -137,13 +137,14 @@ __global__ void __launch_bounds__(REC_THREADS) recurrent_kernel(RecParams p) {
         if (PER_TOKEN) {
             const int64_t wr = __builtin_amdgcn_readlane(wr_l, t);
             const bool ok = row_ok(wr, p.write_min, p.write_slots);
-            store_state(wk, p.write_pool + (ok ? wr : 0) * p.write_ss + (int64_t)h * D * D, st, ok);
+            store_state<NT>(wk, p.write_pool + (ok ? wr : 0) * p.write_ss + (int64_t)h * D * D, st, ok);
         }
     }
-    if (!PER_TOKEN) store_state(wk, p.read_pool + rd * p.read_ss + (int64_t)h * D * D, st);
+    if (!PER_TOKEN) store_state<NT>(wk, p.read_pool + rd * p.read_ss + (int64_t)h * D * D, st);
 }
 
 // Copy one (sequence, head) state: scratch[scratch_idx[n, a-1]] -> pool[pool_idx[n]].
+template <bool NT>
 __global__ void __launch_bounds__(WK_THREADS) spec_commit_kernel(KdaSpecCommitArgs a, bool slot0) {
     const int task = xcd_task(blockIdx.x, gridDim.x);
     const int n = __builtin_amdgcn_readfirstlane(task / a.H);
@@ -156,12 +157,17 @@ __global__ void __launch_bounds__(WK_THREADS) spec_commit_kernel(KdaSpecCommitAr
     const Walker wk(threadIdx.x);
     f32x4 buf[8];
     load_state(wk, a.scratch + sr * a.scratch_slot_stride + (int64_t)h * D * D, buf);
-    store_state(wk, a.pool + pr * a.pool_slot_stride + (int64_t)h * D * D, buf);
+    store_state<NT>(wk, a.pool + pr * a.pool_slot_stride + (int64_t)h * D * D, buf);
 }
 
+// streaming stores when the launch writes more state than the MALL holds (WK_STREAM_BYTES)
 template <bool RG, bool RB, bool NM, int MODE>
 hipError_t launch_rec(const RecParams& p, hipStream_t s) {
-    hipLaunchKernelGGL((recurrent_kernel<RG, RB, NM, MODE>), dim3(p.B * p.H), dim3(REC_THREADS), 0, s, p);
+    const long long written = (long long)p.B * (MODE == REC_PER_TOKEN_MODE ? p.S : 1) * p.H * D * D * 4;
+    if (written > WK_STREAM_BYTES)
+        hipLaunchKernelGGL((recurrent_kernel<RG, RB, NM, MODE, true>), dim3(p.B * p.H), dim3(REC_THREADS), 0, s, p);
+    else
+        hipLaunchKernelGGL((recurrent_kernel<RG, RB, NM, MODE, false>), dim3(p.B * p.H), dim3(REC_THREADS), 0, s, p);
     return hipGetLastError();
 }
 template <bool RG, bool RB, bool NM>
@@ -256,8 +262,12 @@ extern "C" int kda355_spec_commit_launch(const KdaSpecCommitArgs* a, kda355_stre
     KDA_CHECK_ARG(aligned(a->scratch, 16) && aligned(a->pool, 16) && a->scratch_slot_stride % 4 == 0 &&
                       a->pool_slot_stride % 4 == 0,
                   "spec_commit: pools must be 16-byte aligned");
-    hipLaunchKernelGGL(spec_commit_kernel, dim3(a->B * a->H), dim3(WK_THREADS), 0, reinterpret_cast<hipStream_t>(stream), *a,
-                       (a->flags & KDA355_REC_SLOT0_RESERVED) != 0);
+    const bool slot0 = (a->flags & KDA355_REC_SLOT0_RESERVED) != 0;
+    const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    if ((long long)a->B * a->H * D * D * 4 > WK_STREAM_BYTES)
+        hipLaunchKernelGGL(spec_commit_kernel<true>, dim3(a->B * a->H), dim3(WK_THREADS), 0, s, *a, slot0);
+    else
+        hipLaunchKernelGGL(spec_commit_kernel<false>, dim3(a->B * a->H), dim3(WK_THREADS), 0, s, *a, slot0);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         set_error("spec_commit: launch failed: %s", hipGetErrorString(e));

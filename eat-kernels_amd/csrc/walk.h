@@ -14,7 +14,12 @@ namespace kda355 {
 
 constexpr int WK_THREADS = 512;
 constexpr int WK_LOAD_AUX = 2;    // nt: streaming load
-constexpr int WK_STORE_AUX = 17;  // sc0 | sc1: system-scope store, written through the L2
+constexpr int WK_STORE_AUX = 17;     // sc0 | sc1: system-scope store, written through the L2
+constexpr int WK_STORE_AUX_NT = 18;  // sc1 | nt: streaming store
+// Store policy by the bytes of state a launch writes.  Write-through keeps the written states in the 256 MB MALL for
+// the next step's reads; beyond that size they cannot stay there, and streaming stores write faster (measured on
+// page pools: 537 MB of states per launch 214 -> 193 us, 268 MB 90 -> 107 us, so the switch sits between them).
+constexpr long long WK_STREAM_BYTES = 384ll << 20;
 
 // Sum over the 32 lanes of each half wave; every lane of the half receives the total.
 __device__ __forceinline__ float sum32(float x) {
@@ -61,14 +66,17 @@ __device__ __forceinline__ void state_ready(f32x4 (&st)[8]) {
 
 // valid = false stores nothing: the descriptor then covers 0 bytes and the hardware drops out-of-range buffer
 // stores.  Keeping the store instructions unconditional keeps the compiler's memory-counter waits exact (a store
-// under a branch makes it wait for every older access on the path without it).
+// under a branch makes it wait for every older access on the path without it).  NT selects the streaming policy at
+// compile time: a run-time branch between the two policies costs the single-token decode 7 % (the stores can no
+// longer start while the last rows are still being updated).
+template <bool NT = false>
 __device__ __forceinline__ void store_state(const Walker& wk, float* base, const f32x4 (&st)[8], bool valid = true) {
     const __amdgpu_buffer_rsrc_t rs =
         __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(base), (short)0, valid ? D * D * 4 : 0, 0x00020000);
 #pragma unroll
     for (int p = 0; p < 8; ++p)
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, st[p]), rs, wk.voff(), p * WK_ROW_STEP,
-                                               WK_STORE_AUX);
+                                               NT ? WK_STORE_AUX_NT : WK_STORE_AUX);
 }
 
 // A buffer descriptor over `bytes` bytes at a wave-uniform base (the per-token operand rows).
