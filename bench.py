@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """KDA on one MI355X: chunked prefill throughput (the headline), recurrent decode, speculative verify, long prefill.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs c1,c3,c4,d1,c2] [--cpu-seconds 10]
+    python bench.py [--gpus 1] [--steps 20] [--warmup 50] [--configs c1,c3,c4,d1,c2] [--cpu-seconds 10]
 
 Prints ONE JSON line on stdout.  `value` is the prefill throughput of configuration 1: the
 fla `chunk_kda` plain call over 8 varlen sequences (lengths U[256, 8192] from seed 1, 38,881 tokens), H = 32,
@@ -347,7 +347,9 @@ def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    # default W = 50: an idle MI355X needs a few tens of ms under load to reach its clocks (the first ~15 ms of
+    # config-1 calls run ~10 % slower); an explicit --warmup W is honoured as given
+    ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--configs", default="c1,c3,c4,d1,c2")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--calib-copy", action="store_true",
