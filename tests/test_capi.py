@@ -134,6 +134,33 @@ def test_prefill_plan_splits_long_sequences():
     assert (pl.num_pieces, pl.num_split) == (2, 1)
 
 
+def test_prefill_plan_schedules_both_checkpoint_kinds():
+    """Later pieces get compose tasks for the single checkpoint and for every-n rows alike (the launch's mode picks
+    one; a plan made without flags must still cover both): 8192 tokens in 8 pieces of 16 chunks, single checkpoint at
+    chunk 40 (inside piece 3), every-n rows every 8 chunks (row j is the state after 8 j chunks: rows 0..2 belong to
+    the first piece, which writes them itself; rows 3..15 fall in pieces 2..8)."""
+    import numpy as np
+    from kda355 import _lib
+    L = _lib.lib()
+    cu = np.array([0, 8192], np.int64)
+    ck = np.array([40 * 64], np.int32)
+    pin = _lib.KdaPrefillPlanIn()
+    pin.cu_seqlens, pin.ck_offsets = ctypes.c_void_p(cu.ctypes.data), ctypes.c_void_p(ck.ctypes.data)
+    pin.N, pin.H, pin.num_cus, pin.ck_every = 1, 2, 256, 8 * 64
+    pl = _lib.KdaPrefillPlan()
+    assert L.kda355_prefill_plan(ctypes.byref(pin), ctypes.byref(pl), None, 0) == 0
+    tab = np.zeros(pl.table_words, np.int32)
+    assert L.kda355_prefill_plan(ctypes.byref(pin), ctypes.byref(pl), ctypes.c_void_p(tab.ctypes.data), tab.size) == 0
+    assert (pl.num_pieces, pl.num_split) == (8, 1)
+    off_ckc, nck = tab[13], tab[14]                      # header: compose list offset and length
+    tasks = tab[off_ckc:off_ckc + 4 * nck].reshape(nck, 4)
+    kinds = tasks[:, 3].tolist()
+    assert kinds.count(1) == 1 and kinds.count(2) == 13 and nck == pl.num_ck_tasks == 14
+    assert tasks[tasks[:, 3] == 1, 0].tolist() == [0]    # the single checkpoint of sequence 0
+    assert sorted(tasks[tasks[:, 3] == 2, 0].tolist()) == list(range(3, 16))   # every-n rows in later pieces
+    assert pl.workspace_bytes == (3 * 8 + 2 * 14) * 2 * 65536 + 7 * 16 * 2 * 16384
+
+
 def test_decode_rejects_host_tensors():
     """The fused decode wrapper raises TypeError for CPU tensors (the reference validator's device rule,
     kda/mi350x/kda/decode/kernel_v13_a.py:705-707), before any device call."""
