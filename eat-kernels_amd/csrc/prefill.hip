@@ -1189,7 +1189,8 @@ extern "C" int kda355_prefill_plan(const KdaPrefillPlanIn* in, KdaPrefillPlan* p
     }
     // Pieces.  A workgroup walks one (piece, head) chain and a CU holds one such workgroup at a time; the chain list is
     // dispatched longest first.  Candidate cuts: every sequence longer than a piece length T is cut into
-    // ceil(nch / T) near-equal pieces of >= MIN_PIECE chunks, for T on a geometric ladder.  Each candidate is costed by
+    // ceil(nch / T) near-equal pieces of >= MIN_PIECE chunks, for T on a geometric ladder from a quarter of the
+    // balanced per-CU load.  Each candidate is costed by
     // list-scheduling its chains onto the CUs (every chunk costs one unit, later pieces as much as first ones), plus
     // the passes a split adds: the scan (~SCAN_UNITS chunk times) and the output fixup (~FIX_UNITS chunk times per
     // chunk-head of later pieces, spread over the chip).  The cheapest candidate wins; ties keep fewer pieces.  The
@@ -1207,37 +1208,47 @@ extern "C" int kda355_prefill_plan(const KdaPrefillPlanIn* in, KdaPrefillPlan* p
         if ((idle || 4 * (int64_t)maxc > 5 * avg) && maxc >= 2 * MIN_PIECE) {
             auto cut = [&](int n, int T) { return nch[n] > T ? std::max(1, std::min(nch[n] / MIN_PIECE, (nch[n] + T - 1) / T)) : 1; };
             std::vector<int> counts;
-            std::vector<int64_t> cusload;
-            auto cost = [&](int T) {
+            std::vector<int64_t> loads;
+            const int64_t total_units = nchunks * in->H;
+            double best = 0.0;
+            auto cost = [&](int T, bool first) {
                 counts.clear();
                 int64_t fixch = 0;
                 bool split = false;
+                int most = 0;
                 for (int n = 0; n < N; ++n) {
                     const int np = cut(n, T);
                     for (int pc = 0; pc < np; ++pc) {
                         const int c = nch[n] / np + (pc < nch[n] % np ? 1 : 0);
                         counts.push_back(c);
+                        most = std::max(most, c);
                         if (pc > 0) fixch += c;
                     }
                     split |= np > 1;
                 }
-                std::stable_sort(counts.begin(), counts.end(), std::greater<int>());
-                cusload.assign(num_cus, 0);  // min-heap of CU finish times (a zero-filled array is a valid heap)
+                const double extra = split ? SCAN_UNITS + FIX_UNITS * (double)fixch * in->H : 0.0;
+                // no schedule beats the longest piece or the perfect balance
+                const double bound = (double)std::max<int64_t>(most, (total_units + num_cus - 1) / num_cus) + extra;
+                if (!first && bound >= best) return bound;
+                std::sort(counts.begin(), counts.end(), std::greater<int>());
+                // list scheduling, longest first: each workgroup goes to the CU that frees up first
+                loads.assign(num_cus, 0);  // a min-heap of finish times (all zero: a valid heap)
                 int64_t span = 0;
                 for (int c : counts)
-                    for (int h = 0; h < in->H; ++h) {
-                        std::pop_heap(cusload.begin(), cusload.end(), std::greater<int64_t>());
-                        cusload.back() += c;
-                        span = std::max(span, cusload.back());
-                        std::push_heap(cusload.begin(), cusload.end(), std::greater<int64_t>());
+                    for (int hh = 0; hh < in->H; ++hh) {
+                        std::pop_heap(loads.begin(), loads.end(), std::greater<int64_t>());
+                        loads.back() += c;
+                        span = std::max(span, loads.back());
+                        std::push_heap(loads.begin(), loads.end(), std::greater<int64_t>());
                     }
-                return (double)span + (split ? SCAN_UNITS + FIX_UNITS * (double)fixch * in->H : 0.0);
+                return (double)span + extra;
             };
             int bestT = maxc;
-            double best = cost(maxc);
-            for (double t = MIN_PIECE; t < maxc; t *= 1.12) {
+            best = cost(maxc, true);
+            // pieces shorter than a quarter of the balanced load per CU only add fixup work: the ladder starts there
+            for (double t = std::max<double>(MIN_PIECE, (double)avg / 4); t < maxc; t *= 1.12) {
                 const int T = (int)t;
-                const double c = cost(T);
+                const double c = cost(T, false);
                 if (c < best - 1e-9) { best = c; bestT = T; }
             }
             for (int n = 0; n < N; ++n) npieces[n] = cut(n, bestT);

@@ -132,6 +132,13 @@ def test_prefill_plan_splits_long_sequences():
     assert pl.num_pieces == 0
     pl, _ = plan([2048, 500], 2, 256)                    # 32 chunks -> 2 pieces of 16
     assert (pl.num_pieces, pl.num_split) == (2, 1)
+    # the plan is made on the host for every serving step: a large batch with one long outlier stays cheap
+    import time
+    rng = np.random.default_rng(0)
+    lens = list(rng.integers(64, 2048, size=255)) + [65536]
+    t0 = time.perf_counter()
+    pl, _ = plan(lens, 32, 256)
+    assert pl.num_split == 1 and time.perf_counter() - t0 < 0.05
 
 
 def test_prefill_plan_schedules_both_checkpoint_kinds():
