@@ -16,6 +16,9 @@ The other configurations are reported beside it (never as `value`):
                layout at the configs[3] shape and at the reference's s8_h96_b32 spec-verify workload
   long_prefill configs[2]: one sequence of 131,072 tokens, H = 32, paged fp32 pool of 64 slots at a seeded slot,
                bf16 checkpoints every 4096 tokens into 32 seeded rows
+  serving      (opt-in, --configs ...,serving) the reference's own 13 chunked-prefill steps and 10 decode steps on the
+               vLLM page layout, each timed like the reference times them (single call after a 512 MiB cache flush,
+               median) beside the reference's published MI350X latency for that workload
 
 Roofline: prefill is bound by HBM at these shapes (arithmetic intensity ~120 FLOP/B, below the bf16 ridge of ~312),
 so `roofline` is the HBM fraction of the prefill launch: compulsory bytes (q, k, v, out bf16; g fp32; beta fp32;
@@ -259,12 +262,12 @@ def bench_c2(kda, torch, dev, steps, warmup):
                 mfma_frac=flops / (ms * 1e-3) / (MFMA_PEAK_TFLOPS * 1e12))
 
 
-def bench_fused_decode(kda, torch, dev, steps, warmup, H, B, S):
+def bench_fused_decode(kda, torch, dev, steps, warmup, H, B, S, flush=None, taps_total=None):
     """The vLLM-contract fused decode (`kda355.decode`) on the vLLM page layout (conv state then SSM state in one page
     per slot, pages padded; mixed_qkv / out_gate / beta as column slices of one input projection), graph replay."""
     dim, T = H * D, B * S
     spec = S > 1
-    taps = 2 + S if spec else 3
+    taps = taps_total or (2 + S if spec else 3)
     slots = 2 * B * S + 16
     conv_bytes = taps * 3 * dim * 2
     page = -(-(conv_bytes + H * D * D * 4 + 4096) // 256) * 256
@@ -297,10 +300,109 @@ def bench_fused_decode(kda, torch, dev, steps, warmup, H, B, S):
     gr = torch.cuda.CUDAGraph()
     with torch.cuda.graph(gr):
         call()
-    ms, _ = time_steps(gr.replay, steps * 5, warmup * 5, torch)
+    if flush is None:
+        ms, _ = time_steps(gr.replay, steps * 5, warmup * 5, torch)
+        us = ms * 1e3
+    else:  # single replays after a cache flush, median (the reference's serving measurement)
+        for _ in range(warmup):
+            gr.replay()
+        torch.cuda.synchronize()
+        us = time_flushed_median(gr.replay, steps, torch, flush)
     state_bytes = B * H * D * D * 4 * (1 + S)
     del raw, P
-    return dict(H=H, B=B, S=S, us=ms * 1e3, state_bytes=state_bytes)
+    return dict(H=H, B=B, S=S, us=us, state_bytes=state_bytes)
+
+
+# ------------------------------------------------------------------------------------------------ serving workloads
+# The reference's own serving workloads and its published MI350X latencies for them.  Shapes:
+# kda/mi350x/benchmark/eval_kda_mi350x.py:92-115 (prefill steps as (H, [(new tokens, has_initial_state, checkpoint
+# offset)]), decode steps as (H, B, S)); latencies (us, median of single calls after a cache flush):
+# kda/mi350x/docs/HANDOVER.md:456-478.  Timed here the same way: one call after zeroing 512 MiB, median.
+SERVING_PREFILL = {
+    "p12_loaded8k_0": (12, [(7808, 1, 7808), (128, 1, 0)], 80.22),
+    "p12_loaded8k_1": (12, [(3776, 1, 3584), (1280, 1, 896), (448, 1, 384), (2688, 1, 2688)], 74.76),
+    "p12_loaded8k_2": (12, [(7936, 1, 7232)], 80.84),
+    "p12_loaded16k_0": (12, [(5440, 1, 4992), (1920, 1, 1024), (8768, 0, 8192)], 130.36),
+    "p12_loaded16k_1": (12, [(3008, 1, 3008), (1536, 1, 1536), (256, 1, 64), (128, 0, 0), (1600, 1, 832), (640, 1, 0),
+                             (576, 1, 0), (512, 1, 0), (448, 1, 0), (2560, 1, 2560), (320, 1, 256), (4288, 1, 3712)],
+                        113.17),
+    "p12_loaded16k_2": (12, [(384, 1, 64), (320, 1, 128), (256, 1, 0), (7424, 1, 7104), (192, 1, 0), (256, 1, 128),
+                             (1344, 1, 1280), (1280, 1, 320), (704, 1, 128), (2944, 0, 2048), (1280, 0, 1024)], 124.26),
+    "p12_light8k_0": (12, [(5248, 1, 4608), (2944, 0, 2048)], 81.30),
+    "p12_light8k_1": (12, [(640, 1, 0), (704, 1, 0), (960, 1, 960)], 34.08),
+    "p12_light16k_0": (12, [(1600, 1, 640)], 36.74),
+    "p12_light16k_1": (12, [(1664, 1, 768)], 37.94),
+    "p96_loaded8k_0": (96, [(8192, 1, 7616)], 339.17),
+    "p96_loaded8k_1": (96, [(384, 1, 0), (1344, 1, 896), (3008, 0, 2048), (2176, 1, 2048), (320, 1, 0), (832, 0, 0)],
+                       352.25),
+    "p96_light8k_0": (96, [(704, 1, 320), (1216, 1, 960), (512, 1, 320)], 117.13),
+}
+SERVING_DECODE = {  # name: (H, B, S, reference us)
+    "s8_h12_b1": (12, 1, 8, 15.41), "s8_h12_b4": (12, 4, 8, 18.32), "s8_h12_b16": (12, 16, 8, 31.80),
+    "s8_h12_b32": (12, 32, 8, 54.48), "s8_h12_b64": (12, 64, 8, 94.29), "s8_h12_b128": (12, 128, 8, 176.01),
+    "d_h12_b64": (12, 64, 1, 28.58), "s8_h96_b1": (96, 1, 8, 23.00), "s8_h96_b8": (96, 8, 8, 91.96),
+    "s8_h96_b32": (96, 32, 8, 333.78),
+}
+SERVING_TAPS = 10  # conv taps per page: 2 + 8 speculative tokens (the reference's DSpark layout)
+
+
+def time_flushed_median(fn, reps, torch, flush):
+    ts = []
+    for _ in range(reps):
+        flush.zero_()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        fn()
+        b.record()
+        torch.cuda.synchronize()
+        ts.append(a.elapsed_time(b) * 1e3)
+    ts.sort()
+    return ts[len(ts) // 2]
+
+
+def bench_serving_prefill(kda, torch, dev, H, seqs, reps, flush, seed):
+    """One chunked-prefill step on the vLLM page layout through `kda355.prefill` (raw gates and beta in the kernel,
+    q/k normalized in the kernel, pool rows read when has_initial_state, final states and checkpoint rows written)."""
+    N, dim = len(seqs), H * D
+    lens = [s[0] for s in seqs]
+    T = sum(lens)
+    slots = 2 * N + 9
+    conv_bytes = SERVING_TAPS * 3 * dim * 2
+    page = -(-(conv_bytes + H * D * D * 4 + 4096) // 256) * 256
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    raw = torch.zeros(slots * page, dtype=torch.uint8, device=dev)
+    ssm = torch.as_strided(raw.view(torch.float32), (slots, H, D, D), (page // 4, D * D, D, 1), conv_bytes // 4)
+    ssm.copy_(torch.randn(ssm.shape, generator=gen, device=dev) * 0.05)
+    q, k, v, raw_g = (torch.randn(1, T, H, D, generator=gen, device=dev).bfloat16() for _ in range(4))
+    Wp = -(-(4 * dim + D + H) // 16) * 16
+    P = torch.randn(T, Wp, generator=gen, device=dev).bfloat16()
+    raw_beta = P[:, 4 * dim + D:4 * dim + D + H].unsqueeze(0)
+    A_log = torch.rand(H, generator=gen, device=dev) * 2 - 1
+    dt_bias = torch.randn(H * D, generator=gen, device=dev) * 0.5
+    cpu = torch.Generator().manual_seed(seed)
+    perm = (torch.randperm(slots - 1, generator=cpu) + 1).to(torch.int32)
+    idx = perm[:N].contiguous().to(dev)
+    ck_off = torch.tensor([s[2] for s in seqs], dtype=torch.int32)
+    ck_rows = torch.tensor([int(perm[N + n]) if s[2] > 0 else -1 for n, s in enumerate(seqs)], dtype=torch.int32)
+    has_init = torch.tensor([bool(s[1]) for s in seqs], device=dev)
+    cu_cpu = torch.tensor([0] + [sum(lens[:i + 1]) for i in range(N)], dtype=torch.int32)
+    cu = cu_cpu.to(dev)
+    big_out = torch.empty(1, 256 + T, H, D, dtype=torch.bfloat16, device=dev)
+    out = big_out[:, 256:]
+    meta = kda.prefill_prepare(cu_cpu, H, ck_off, ck_rows, device=dev)
+    ws = torch.empty(max(meta.workspace_bytes, 256), dtype=torch.uint8, device=dev)
+    ck_off_d, ck_rows_d = ck_off.to(dev), ck_rows.to(dev)
+
+    def call():
+        kda.prefill(q, k, v, raw_g, raw_beta, A_log, dt_bias, D ** -0.5, -5.0, ssm, idx, has_init, cu, out, ck_off_d,
+                    ck_rows_d, meta=meta, workspace=ws)
+
+    for _ in range(3):
+        call()
+    torch.cuda.synchronize()
+    us = time_flushed_median(call, reps, torch, flush)
+    del raw, P, big_out, ws
+    return dict(us=us, T=T, N=N, pieces=meta.split[0])
 
 
 # ------------------------------------------------------------------------------------------------ CPU baseline
@@ -423,6 +525,24 @@ def main():
                                  "ms_per_step": round(c2["ms"], 3), "tok_s": round(c2["tok_s"], 1),
                                  "hbm_frac": round(c2["hbm_frac"], 4), "mfma_frac": round(c2["mfma_frac"], 4)}
         log(f"c2: {c2['ms']:.3f} ms/step")
+    if "serving" in cfgs:  # opt-in: the reference's serving workloads beside its published MI350X latencies
+        rows = []
+        for i, (name, (H, seqs, ref)) in enumerate(SERVING_PREFILL.items()):
+            r = bench_serving_prefill(kda355, torch, dev, H, seqs, max(args.steps, 20), flush, 100 + i)
+            rows.append({"workload": name, "H": H, "N": r["N"], "T": r["T"], "pieces": r["pieces"],
+                         "us": round(r["us"], 2), "reference_mi350x_us": ref, "ratio": round(ref / r["us"], 3)})
+            log(f"serving {name}: {r['us']:.1f} us (reference MI350X {ref} us)")
+        for name, (H, B, S, ref) in SERVING_DECODE.items():
+            r = bench_fused_decode(kda355, torch, dev, max(args.steps, 20), 5, H, B, S, flush=flush,
+                                   taps_total=SERVING_TAPS)
+            rows.append({"workload": name, "H": H, "B": B, "S": S, "us": round(r["us"], 2),
+                         "reference_mi350x_us": ref, "ratio": round(ref / r["us"], 3)})
+            log(f"serving {name}: {r['us']:.1f} us (reference MI350X {ref} us)")
+        gm = lambda xs: math.exp(sum(math.log(x) for x in xs) / len(xs))  # noqa: E731
+        extra["serving"] = {"method": "single calls after a 512 MiB cache flush, median (eval_kda_mi350x.py:163-182)",
+                            "prefill_geomean_ratio": round(gm([x["ratio"] for x in rows if "N" in x]), 3),
+                            "decode_geomean_ratio": round(gm([x["ratio"] for x in rows if "B" in x]), 3),
+                            "rows": rows}
 
     cpu = None
     if args.cpu_seconds > 0:
