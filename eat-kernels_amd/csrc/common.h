@@ -45,6 +45,15 @@ __device__ __forceinline__ int xcd_task(int b, int total) {
     return x * q + (x < r ? x : r) + (b >> 3);
 }
 
+// A wave-uniform address taken through readfirstlane: the compiler may otherwise compute uniform 64-bit address
+// arithmetic in VGPRs (v_lshl_add_u64), and a buffer descriptor built from a VGPR base becomes a waterfall loop.
+__device__ __forceinline__ void* uniform_ptr(const void* p) {
+    const uint64_t a = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+    return reinterpret_cast<void*>(((uint64_t)hi << 32) | lo);
+}
+
 // DPP lane moves inside a row of 16 lanes (quad_perm / row_half_mirror / row_mirror).
 template <int CTRL>
 __device__ __forceinline__ float dpp(float x) {

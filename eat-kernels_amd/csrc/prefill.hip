@@ -898,13 +898,23 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
 // in fp32, P as the chunk kernel stores it ([k'][k]).  Row v of the result depends on row v of X alone, so one
 // workgroup of 256 threads takes a block of 16 rows (grid: entries x H x 8, the 8 blocks of one state on one XCD so
 // that P is fetched into one L2).  The product runs on fp32 MFMAs (16x16x4): wave w owns the columns 32 w .. 32 w + 31
-// as two 16-column tiles; MFMA step s covers k' = 32 (lane / 16) + s, so a lane's A values (X rows from LDS, row
-// stride 132 floats) are 4 consecutive floats per LDS read and its B values come from P in global memory (L2).
-// Result lane layout: rows 4 (lane / 16) + e of the block, column 32 w + 16 ct + lane % 16.
+// as two 16-column tiles, tile ct holding the columns 32 w + 2 j + ct (j = lane % 16), so that a lane's two B values
+// for one k' are one 8-byte load.  MFMA step s covers k' = 32 (lane / 16) + s; a lane's A values (X rows from LDS,
+// row stride 132 floats) are 4 consecutive floats per LDS read.  The B values and the L values of one composition
+// are loaded into registers ahead of it (ComposeOps), so the scan fetches the next piece's operands while it
+// composes the current one.  Result lane layout: rows 4 (lane / 16) + e of the block, columns 32 w + 2 j + {0, 1}.
 constexpr int SC_THREADS = 256;
 constexpr int SC_ROWS = 16;
 constexpr int SC_XS = 132;
-constexpr int SC_SMEM = SC_ROWS * SC_XS * 4;
+constexpr int SC_BUF = SC_ROWS * SC_XS;     // floats of one staged row block
+constexpr int SC_SMEM = 2 * SC_BUF * 4;     // two row blocks (the scan alternates between them)
+
+struct ComposeOps {
+    f32x2 b[32];  // P[32 kq + s][32 w + 2 j + {0, 1}], s = 0 .. 31
+    f32x2 l[4];   // L[4 kq + e][32 w + 2 j + {0, 1}], e = 0 .. 3
+};
+__device__ __forceinline__ int compose_col() { return 32 * (threadIdx.x >> 6) + 2 * (threadIdx.x & 15); }
+__device__ __forceinline__ int compose_row0() { return 4 * ((threadIdx.x & 63) >> 4); }
 
 // the 16 rows starting at X (row stride D) -> sX
 __device__ __forceinline__ void stage_X(const float* __restrict__ X, float* sX) {
@@ -914,23 +924,31 @@ __device__ __forceinline__ void stage_X(const float* __restrict__ X, float* sX) 
         *reinterpret_cast<f32x4*>(sX + rr * SC_XS + 4 * c4) = *reinterpret_cast<const f32x4*>(X + rr * D + 4 * c4);
     }
 }
-// acc[ct] = Lblk (the block's rows of L) + sX P on this lane's tile elements; sX staged and synced
-__device__ __forceinline__ void compose_rows(const float* sX, const float* __restrict__ P, const float* __restrict__ Lblk,
-                                             f32x4 (&acc)[2]) {
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, j = lane & 15, kq = lane >> 4;
-    const float* pc = P + (32 * kq) * D + 32 * w + j;
+// this lane's operands of one composition: P (a whole state, [k'][k]) and Lblk (the block's first row of L)
+__device__ __forceinline__ void fetch_ops(const float* __restrict__ P, const float* __restrict__ Lblk, ComposeOps& o) {
+    const int col = compose_col(), r0 = compose_row0();
+    const float* pc = P + (8 * r0) * D + col;  // row 32 kq
 #pragma unroll
-    for (int ct = 0; ct < 2; ++ct)
+    for (int s = 0; s < 32; ++s) o.b[s] = *reinterpret_cast<const f32x2*>(pc + s * D);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) acc[ct][e] = Lblk[(4 * kq + e) * D + 32 * w + 16 * ct + j];
+    for (int e = 0; e < 4; ++e) o.l[e] = *reinterpret_cast<const f32x2*>(Lblk + (r0 + e) * D + col);
+}
+// acc[ct][e] = out[4 kq + e][32 w + 2 j + ct]; sX staged and synced
+__device__ __forceinline__ void compose_ops(const float* sX, const ComposeOps& o, f32x4 (&acc)[2]) {
+    const int j = threadIdx.x & 15, kq = (threadIdx.x & 63) >> 4;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        acc[0][e] = o.l[e][0];
+        acc[1][e] = o.l[e][1];
+    }
 #pragma unroll
     for (int s4 = 0; s4 < 8; ++s4) {
         const f32x4 a = *reinterpret_cast<const f32x4*>(sX + j * SC_XS + 32 * kq + 4 * s4);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int s = 4 * s4 + e;
-            acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], pc[s * D], acc[0], 0, 0, 0);
-            acc[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], pc[s * D + 16], acc[1], 0, 0, 0);
+            acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], o.b[s][0], acc[0], 0, 0, 0);
+            acc[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], o.b[s][1], acc[1], 0, 0, 0);
         }
     }
 }
@@ -945,7 +963,10 @@ __device__ __forceinline__ void scan_task(int H, int& ei, int& h, int& rb) {
 
 // Split sequences: X_1 = the first piece's end state (stored by that piece), X_{p+1} = P_p X_p + S_loc(p) for the
 // later pieces p = 1 .. np-1; X_p is the start state of piece p, X_np the sequence's final state.  One workgroup per
-// (sequence, head, block of 16 state rows).
+// (sequence, head, block of 16 state rows).  X_p sits in LDS buffer (p - 1) % 2: step p reads one buffer and writes
+// the other, so one barrier per step orders both (a wave writes buffer p % 2 only after every wave has passed step
+// p's barrier, i.e. finished reading that buffer in step p - 1).  The barrier covers LDS only: the global stores of
+// the states are not waited for.
 __global__ void __launch_bounds__(SC_THREADS) scan_kernel(PfParams p, const int32_t* __restrict__ tab) {
     extern __shared__ __align__(16) unsigned char lds[];
     float* sX = reinterpret_cast<float*>(lds);
@@ -955,9 +976,8 @@ __global__ void __launch_bounds__(SC_THREADS) scan_kernel(PfParams p, const int3
     const int32_t* e = tab + tab[H_OFF_SCAN] + S_WORDS * si;
     const int n = e[S_SEQ], np = e[S_NP], slot0 = e[S_SLOT0];
     const int64_t ws_arr = (int64_t)tab[H_NSLOTS] * H * D * D;
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, j = lane & 15, kq = lane >> 4;
+    const int col = compose_col(), r0 = compose_row0();
     const int64_t blk = (int64_t)SC_ROWS * rb * D;  // the block's first element in a state
-    stage_X(p.ws + 2 * ws_arr + ((int64_t)(slot0 + 1) * H + h) * D * D + blk, sX);
     float* fin = nullptr;  // the final state's destination (same rules as the chunk walk)
     if (p.flags & KDA355_PF_POOL) {
         const int64_t row = p.state_idx[n];
@@ -965,21 +985,38 @@ __global__ void __launch_bounds__(SC_THREADS) scan_kernel(PfParams p, const int3
     } else {
         fin = p.final_state + ((int64_t)n * H + h) * D * D;
     }
-    for (int pc = 1; pc < np; ++pc) {
+    // piece pc's operands: P at array 1, S_loc at array 0 of the workspace
+    auto fetch = [&](int pc, ComposeOps& o) {
         const int64_t so = ((int64_t)(slot0 + pc) * H + h) * D * D;
-        __syncthreads();  // sX holds X_pc
+        fetch_ops(p.ws + ws_arr + so, p.ws + so + blk, o);
+    };
+    // step pc: X_{pc+1} = P_pc X_pc + S_loc(pc) from `cur`, fetching piece pc + 1's operands into `nxt` meanwhile.
+    // Every step issues the same memory operations (the last one fetches its own piece again, a missing final-state
+    // destination is a store descriptor of no records): with no operation under a branch, the wait for `cur` counts
+    // only the operations issued after it, and never waits for the prefetch.
+    auto step = [&](int pc, const ComposeOps& cur, ComposeOps& nxt) {
+        fetch(min(pc + 1, np - 1), nxt);
+        lds_barrier();  // X_pc is complete in its buffer
         f32x4 acc[2];
-        compose_rows(sX, p.ws + ws_arr + so, p.ws + so + blk, acc);
-        __syncthreads();  // every wave has read sX
-        float* dst = (pc + 1 < np) ? p.ws + 2 * ws_arr + ((int64_t)(slot0 + pc + 1) * H + h) * D * D : fin;
+        compose_ops(sX + ((pc - 1) & 1) * SC_BUF, cur, acc);
+        float* sN = sX + (pc & 1) * SC_BUF;
+        const float* dst = (pc + 1 < np) ? p.ws + 2 * ws_arr + ((int64_t)(slot0 + pc + 1) * H + h) * D * D : fin;
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            uniform_ptr(dst ? dst : p.ws), (short)0, dst ? D * D * 4 : 0, 0x00020000);
 #pragma unroll
-        for (int ct = 0; ct < 2; ++ct)
-#pragma unroll
-            for (int ee = 0; ee < 4; ++ee) {
-                const int rr = 4 * kq + ee, col = 32 * w + 16 * ct + j;
-                sX[rr * SC_XS + col] = acc[ct][ee];
-                if (dst) dst[blk + rr * D + col] = acc[ct][ee];
-            }
+        for (int ee = 0; ee < 4; ++ee) {
+            const f32x2 v = {acc[0][ee], acc[1][ee]};
+            *reinterpret_cast<f32x2*>(sN + (r0 + ee) * SC_XS + col) = v;
+            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, v), rs,
+                                                  (int)(blk + (r0 + ee) * D + col) * 4, 0, 0);
+        }
+    };
+    ComposeOps oa, ob;
+    fetch(1, oa);
+    stage_X(p.ws + 2 * ws_arr + ((int64_t)(slot0 + 1) * H + h) * D * D + blk, sX);
+    for (int pc = 1; pc < np; pc += 2) {
+        step(pc, oa, ob);
+        if (pc + 1 < np) step(pc + 1, ob, oa);
     }
 }
 
@@ -996,26 +1033,26 @@ __global__ void __launch_bounds__(SC_THREADS) ck_compose_kernel(PfParams p, cons
     if (e[K_KIND] != ck_mode) return;
     const int64_t ws_arr = (int64_t)tab[H_NSLOTS] * H * D * D;
     const float* ws_ck = p.ws + 3 * ws_arr;
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, j = lane & 15, kq = lane >> 4;
+    const int col = compose_col(), r0 = compose_row0();
     const int64_t blk = (int64_t)SC_ROWS * rb * D;
+    ComposeOps o;
+    fetch_ops(ws_ck + ((int64_t)(2 * e[K_WSSLOT] + 1) * H + h) * D * D,
+              ws_ck + ((int64_t)(2 * e[K_WSSLOT]) * H + h) * D * D + blk, o);
     stage_X(p.ws + 2 * ws_arr + ((int64_t)e[K_SSLOT] * H + h) * D * D + blk, sX);
-    __syncthreads();
+    lds_barrier();
     f32x4 acc[2];
-    compose_rows(sX, ws_ck + ((int64_t)(2 * e[K_WSSLOT] + 1) * H + h) * D * D,
-                 ws_ck + ((int64_t)(2 * e[K_WSSLOT]) * H + h) * D * D + blk, acc);
+    compose_ops(sX, o, acc);
     const int64_t rr = p.ck_idx[e[K_CKIDX]];
     if (rr < 0 || rr >= p.ck_slots) return;
     const int64_t off = rr * p.ck_ss + (int64_t)h * D * D + blk;
 #pragma unroll
-    for (int ct = 0; ct < 2; ++ct)
-#pragma unroll
-        for (int ee = 0; ee < 4; ++ee) {
-            const int64_t o = off + (4 * kq + ee) * D + 32 * w + 16 * ct + j;
-            if (p.ck_bf16)
-                reinterpret_cast<uint16_t*>(p.ck_pool)[o] = (uint16_t)f2bf(acc[ct][ee]);
-            else
-                reinterpret_cast<float*>(p.ck_pool)[o] = acc[ct][ee];
-        }
+    for (int ee = 0; ee < 4; ++ee) {
+        const int64_t o2 = off + (r0 + ee) * D + col;
+        if (p.ck_bf16)
+            *reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(p.ck_pool) + o2) = f2bf2(acc[0][ee], acc[1][ee]);
+        else
+            *reinterpret_cast<f32x2*>(reinterpret_cast<float*>(p.ck_pool) + o2) = f32x2{acc[0][ee], acc[1][ee]};
+    }
 }
 
 // The outputs of later pieces: O = partial (fp16, as the chunk kernel left it in `out`) + scale R S_start, stored as
@@ -1190,14 +1227,15 @@ extern "C" int kda355_prefill_plan(const KdaPrefillPlanIn* in, KdaPrefillPlan* p
     // Pieces.  A workgroup walks one (piece, head) chain and a CU holds one such workgroup at a time; the chain list is
     // dispatched longest first.  Candidate cuts: every sequence longer than a piece length T is cut into
     // ceil(nch / T) near-equal pieces of >= MIN_PIECE chunks, for T on a geometric ladder from a quarter of the
-    // balanced per-CU load.  Each candidate is costed by
-    // list-scheduling its chains onto the CUs (every chunk costs one unit, later pieces as much as first ones), plus
-    // the passes a split adds: the scan (~SCAN_UNITS chunk times) and the output fixup (~FIX_UNITS chunk times per
-    // chunk-head of later pieces, spread over the chip).  The cheapest candidate wins; ties keep fewer pieces.  The
-    // first piece of a split sequence runs from the true start state; later pieces run from S = 0, carry their
-    // transition and are completed by the scan, fixup and checkpoint-compose kernels.
-    constexpr int MIN_PIECE = 16;
-    constexpr double SCAN_UNITS = 4.0, FIX_UNITS = 0.0012;
+    // balanced per-CU load.  Each candidate is costed in chunk times (one chunk of one head on one CU, ~11 us) by
+    // list-scheduling its chains onto the CUs (later pieces cost as much per chunk as first ones), plus the passes a
+    // split adds: the scan, sequential over the pieces of a sequence (SCAN_BASE + STEP_UNITS per later piece of the
+    // most-cut sequence), and the output fixup (FIX_BASE + FIX_UNITS per chunk-head of later pieces, spread over the
+    // chip).  The cheapest candidate wins; ties keep fewer pieces.  The first piece of a split sequence runs from the
+    // true start state; later pieces run from S = 0, carry their transition and are completed by the scan, fixup and
+    // checkpoint-compose kernels.  Measured on MI355X: scan steps ~2.7 us, fixup ~11 ns per chunk-head.
+    constexpr int MIN_PIECE = 2;
+    constexpr double SCAN_BASE = 0.5, STEP_UNITS = 0.25, FIX_BASE = 0.5, FIX_UNITS = 0.0012;
     const int num_cus = in->num_cus > 0 ? in->num_cus : 256;
     std::vector<int> npieces(N, 1);
     if (nchunks > 0) {
@@ -1215,9 +1253,10 @@ extern "C" int kda355_prefill_plan(const KdaPrefillPlanIn* in, KdaPrefillPlan* p
                 counts.clear();
                 int64_t fixch = 0;
                 bool split = false;
-                int most = 0;
+                int most = 0, maxnp = 1;
                 for (int n = 0; n < N; ++n) {
                     const int np = cut(n, T);
+                    maxnp = std::max(maxnp, np);
                     for (int pc = 0; pc < np; ++pc) {
                         const int c = nch[n] / np + (pc < nch[n] % np ? 1 : 0);
                         counts.push_back(c);
@@ -1226,7 +1265,8 @@ extern "C" int kda355_prefill_plan(const KdaPrefillPlanIn* in, KdaPrefillPlan* p
                     }
                     split |= np > 1;
                 }
-                const double extra = split ? SCAN_UNITS + FIX_UNITS * (double)fixch * in->H : 0.0;
+                const double extra = split ? SCAN_BASE + STEP_UNITS * (maxnp - 1) + FIX_BASE + FIX_UNITS * (double)fixch * in->H
+                                           : 0.0;
                 // no schedule beats the longest piece or the perfect balance
                 const double bound = (double)std::max<int64_t>(most, (total_units + num_cus - 1) / num_cus) + extra;
                 if (!first && bound >= best) return bound;

@@ -37,14 +37,6 @@ struct Walker {
 };
 constexpr int WK_ROW_STEP = 16 * D * 4;
 
-// A wave-uniform address taken through readfirstlane: the compiler may otherwise compute uniform 64-bit address
-// arithmetic in VGPRs (v_lshl_add_u64), and a buffer descriptor built from a VGPR base becomes a waterfall loop.
-__device__ __forceinline__ void* uniform_ptr(const void* p) {
-    const uint64_t a = reinterpret_cast<uint64_t>(p);
-    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
-    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
-    return reinterpret_cast<void*>(((uint64_t)hi << 32) | lo);
-}
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t state_rsrc(const float* base) {
     return __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(base), (short)0, D * D * 4, 0x00020000);

@@ -63,30 +63,80 @@ def test_struct_layout_matches_header():
     assert [int(x) for x in sizes] == [ctypes.sizeof(m) for m in mirrors]
 
 
-def test_prefill_plan_host_only():
-    """The schedule is built on the host from the layout alone: chunk counts, every-n row counts, bad layouts."""
+def _plan(lens, H, cus, every=0, ck=None):
+    """kda355_prefill_plan over a layout of sequence lengths: (plan, table, the cu array the table refers to)."""
     import numpy as np
     from kda355 import _lib
     L = _lib.lib()
-    cu = np.array([0, 100, 100, 300, 4396], np.int64)
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
     pin = _lib.KdaPrefillPlanIn()
     pin.cu_seqlens = ctypes.c_void_p(cu.ctypes.data)
-    pin.N, pin.H, pin.ck_every = 4, 8, 128
-    pin.num_cus = 64                                     # 32 chains, 9 chunks per CU at balance: 64 > 1.25 x 9
+    if ck is not None:
+        ck = np.asarray(ck, np.int32)
+        pin.ck_offsets = ctypes.c_void_p(ck.ctypes.data)
+    pin.N, pin.H, pin.num_cus, pin.ck_every = len(lens), H, cus, every
     pl = _lib.KdaPrefillPlan()
     assert L.kda355_prefill_plan(ctypes.byref(pin), ctypes.byref(pl), None, 0) == 0
-    assert pl.num_chunks == 2 + 0 + 4 + 64 and pl.T == 4396 and pl.ck_rows == 1 + 0 + 2 + 32
-    # the 64-chunk sequence is cut into 4 pieces of 16 (the minimum piece); pieces 2..4 each keep one 16 KiB R tile
-    # per chunk and head, every piece a start / local-state / transition slot per head, and the every-2-chunk rows
-    # inside pieces 2..4 (chunks 18, 20, .., 62: 8 + 8 + 7) a (local state, transition) pair per head
-    assert (pl.num_pieces, pl.num_split, pl.num_chains, pl.num_fix_tasks, pl.num_ck_tasks) == (4, 1, 7, 24, 23)
-    assert L.kda355_prefill_workspace_bytes(ctypes.byref(pl)) == (3 * 4 + 2 * 23) * 8 * 65536 + 48 * 8 * 16384
-    pin.num_cus = 4                                      # 140 chunks per CU: nothing is split, no workspace
-    assert L.kda355_prefill_plan(ctypes.byref(pin), ctypes.byref(pl), None, 0) == 0
-    assert pl.num_pieces == 0 and L.kda355_prefill_workspace_bytes(ctypes.byref(pl)) == 0
     tab = np.zeros(pl.table_words, np.int32)
     assert L.kda355_prefill_plan(ctypes.byref(pin), ctypes.byref(pl), ctypes.c_void_p(tab.ctypes.data), tab.size) == 0
-    assert L.kda355_prefill_plan(ctypes.byref(pin), ctypes.byref(pl), ctypes.c_void_p(tab.ctypes.data), 3) == _lib.EINVAL
+    return pl, tab
+
+
+def _check_pieces(pl, tab, lens, H, every=0, ck_chunk=None):
+    """The invariants of a split plan, from its tables: every sequence's chunks are covered once, in order; a split
+    sequence is a first piece (flag 4: hands over its end state) followed by later pieces (flag 1: run from zero) of
+    >= 2 chunks; fixup tasks = one per group of <= 2 chunks of a later piece; compose tasks = one per checkpoint that
+    falls strictly inside a later piece (every-n row j: the state after j * every chunks, j * every < chunks of the
+    sequence; single: the state after ck_chunk[n] chunks); the workspace = (3 slots per piece + 2 per compose task)
+    states per head + one 16 KiB R tile per later-piece chunk and head."""
+    ch = tab[20:20 + 13 * pl.num_chains].reshape(-1, 13)
+    nch = [(x + 63) // 64 for x in lens]
+    fix = ck_rows = ck_single = r_chunks = 0
+    for n, c in enumerate(nch):
+        pieces = sorted((int(f), int(k), int(fl)) for s, k, _, _, _, _, f, fl, *_ in ch if s == n)
+        assert [f for f, _, _ in pieces] == list(np.cumsum([0] + [k for _, k, _ in pieces])[:-1])
+        assert sum(k for _, k, _ in pieces) == c
+        if len(pieces) == 1:
+            assert pieces[0][2] == 2                      # a whole sequence: writes its final state
+            continue
+        assert pieces[0][2] == 4 and all(fl == 1 for _, _, fl in pieces[1:])
+        assert all(k >= 2 for _, k, _ in pieces)
+        for f, k, _ in pieces[1:]:
+            fix += (k + 1) // 2
+            r_chunks += k
+            if every:
+                ck_rows += sum(1 for j in range(1, c + 1) if f < j * every <= f + k and j * every < c)
+            if ck_chunk is not None and f < ck_chunk[n] <= f + k:
+                ck_single += 1
+    split = [n for n in range(len(nch)) if sum(1 for r in ch if r[0] == n) > 1]
+    assert pl.num_split == len(split) and pl.num_pieces == sum(1 for r in ch if r[0] in split)
+    assert pl.num_fix_tasks == fix and pl.num_ck_tasks == ck_rows + ck_single
+    assert pl.workspace_bytes == ((3 * pl.num_pieces + 2 * pl.num_ck_tasks) * H * 65536 + r_chunks * H * 16384
+                                  if pl.num_pieces else 0)
+    return ch
+
+
+import numpy as np  # noqa: E402  (used by the plan helpers above)
+
+
+def test_prefill_plan_host_only():
+    """The schedule is built on the host from the layout alone: chunk counts, every-n row counts, bad layouts."""
+    from kda355 import _lib
+    L = _lib.lib()
+    lens = [100, 0, 200, 4296]
+    pl, tab = _plan(lens, 8, 64, every=128)              # 32 chains, 9 chunks per CU at balance on 64 CUs
+    assert pl.num_chunks == 2 + 0 + 4 + 68 and pl.T == 4596 and pl.ck_rows == 1 + 0 + 2 + 34
+    # the 68-chunk sequence (its last chunk 8 tokens) is cut into pieces; the others run whole
+    ch = _check_pieces(pl, tab, lens, 8, every=2)
+    assert pl.num_split == 1 and pl.num_pieces >= 4
+    assert L.kda355_prefill_workspace_bytes(ctypes.byref(pl)) == pl.workspace_bytes
+    pl, tab = _plan(lens, 8, 4, every=128)               # 140 chunks per CU: nothing is split, no workspace
+    assert pl.num_pieces == 0 and L.kda355_prefill_workspace_bytes(ctypes.byref(pl)) == 0
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    pin = _lib.KdaPrefillPlanIn()
+    pin.cu_seqlens, pin.N, pin.H, pin.num_cus, pin.ck_every = ctypes.c_void_p(cu.ctypes.data), 4, 8, 4, 128
+    small = np.zeros(3, np.int32)
+    assert L.kda355_prefill_plan(ctypes.byref(pin), ctypes.byref(pl), ctypes.c_void_p(small.ctypes.data), 3) == _lib.EINVAL
     bad = np.array([0, 10, 5], np.int64)
     pin.cu_seqlens, pin.N = ctypes.c_void_p(bad.ctypes.data), 2
     assert L.kda355_prefill_plan(ctypes.byref(pin), ctypes.byref(pl), None, 0) == _lib.EINVAL
@@ -96,76 +146,53 @@ def test_prefill_plan_host_only():
 
 
 def test_prefill_plan_splits_long_sequences():
-    """With idle CUs, long sequences are cut into pieces of >= 16 chunks; short ones and full chips are not split."""
-    import numpy as np
-    from kda355 import _lib
-    L = _lib.lib()
-
-    def plan(lens, H, cus):
-        cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
-        pin = _lib.KdaPrefillPlanIn()
-        pin.cu_seqlens = ctypes.c_void_p(cu.ctypes.data)
-        pin.N, pin.H, pin.num_cus = len(lens), H, cus
-        pl = _lib.KdaPrefillPlan()
-        assert L.kda355_prefill_plan(ctypes.byref(pin), ctypes.byref(pl), None, 0) == 0
-        tab = np.zeros(pl.table_words, np.int32)
-        assert L.kda355_prefill_plan(ctypes.byref(pin), ctypes.byref(pl), ctypes.c_void_p(tab.ctypes.data), tab.size) == 0
-        return pl, tab
-
-    pl, tab = plan([131072], 32, 256)                    # configuration 2: 2048 chunks x 32 heads on 256 CUs
+    """With idle CUs, long sequences are cut into pieces of >= 2 chunks; full chips are not split."""
+    pl, tab = _plan([131072], 32, 256)                   # configuration 2: 2048 chunks x 32 heads on 256 CUs
     assert (pl.num_pieces, pl.num_split, pl.num_chains, pl.num_fix_tasks) == (8, 1, 8, 7 * 256 // 2)
     assert pl.workspace_bytes == 3 * 8 * 32 * 128 * 128 * 4 + 7 * 256 * 32 * 64 * 128 * 2
     final = tab[20:20 + 13 * 8].reshape(8, 13)
     assert sorted(final[:, 6]) == list(range(0, 2048, 256)) and set(final[:, 1]) == {256}   # first chunk, count
     assert sorted(final[:, 7].tolist()) == [1] * 7 + [4]   # pieces 2..8 run from zero; piece 1 hands over its end
     lens1 = [4011, 4318, 6249, 7799, 532, 1400, 6787, 7785]   # configuration 1: 256 chains on 256 CUs
-    pl, tab = plan(lens1, 32, 256)
+    pl, tab = _plan(lens1, 32, 256)
     # 611 chunks x 32 heads = 77 per CU at balance, but the longest chain has 122 chunks: the long sequences are cut
-    # into pieces of >= 16 chunks, none longer than 64, covering every chunk once
-    counts = tab[20:20 + 13 * pl.num_chains].reshape(-1, 13)
-    assert pl.num_split >= 2 and pl.num_pieces > pl.num_split
-    assert counts[:, 1].max() <= 64 and counts[counts[:, 1] < 16, 1].tolist() in ([], [9]) and counts[:, 1].sum() == 611
-    assert list(counts[:, 1]) == sorted(counts[:, 1], reverse=True)                         # longest first
-    pl, _ = plan(lens1, 32, 64)                          # a quarter of the CUs: 306 chunks per CU, nothing is split
+    # into pieces, none longer than 64 chunks
+    counts = _check_pieces(pl, tab, lens1, 32)[:, 1]
+    assert pl.num_split >= 2 and pl.num_pieces > pl.num_split and counts.max() <= 64
+    assert list(counts) == sorted(counts, reverse=True)                         # longest first
+    pl, _ = _plan(lens1, 32, 64)                         # a quarter of the CUs: 306 chunks per CU, nothing is split
     assert pl.num_pieces == 0
-    pl, _ = plan([1000, 900], 2, 256)                    # 16 chunks: too short to split
+    pl, _ = _plan([64, 100], 2, 256)                     # 1 + 2 chunks: too short to split
     assert pl.num_pieces == 0
-    pl, _ = plan([2048, 500], 2, 256)                    # 32 chunks -> 2 pieces of 16
-    assert (pl.num_pieces, pl.num_split) == (2, 1)
+    for lens in ([2048, 500], [1000, 900], [8192]):      # few chains on an idle chip: cut into short pieces
+        pl, tab = _plan(lens, 2, 256)
+        _check_pieces(pl, tab, lens, 2)
+        assert pl.num_split == len([x for x in lens if x > 256]) and pl.num_pieces >= 2 * pl.num_split
     # the plan is made on the host for every serving step: a large batch with one long outlier stays cheap
     import time
     rng = np.random.default_rng(0)
     lens = list(rng.integers(64, 2048, size=255)) + [65536]
     t0 = time.perf_counter()
-    pl, _ = plan(lens, 32, 256)
+    pl, _ = _plan(lens, 32, 256)
     assert pl.num_split == 1 and time.perf_counter() - t0 < 0.05
 
 
 def test_prefill_plan_schedules_both_checkpoint_kinds():
     """Later pieces get compose tasks for the single checkpoint and for every-n rows alike (the launch's mode picks
-    one; a plan made without flags must still cover both): 8192 tokens in 8 pieces of 16 chunks, single checkpoint at
-    chunk 40 (inside piece 3), every-n rows every 8 chunks (row j is the state after 8 j chunks: rows 0..2 belong to
-    the first piece, which writes them itself; rows 3..15 fall in pieces 2..8)."""
-    import numpy as np
-    from kda355 import _lib
-    L = _lib.lib()
-    cu = np.array([0, 8192], np.int64)
-    ck = np.array([40 * 64], np.int32)
-    pin = _lib.KdaPrefillPlanIn()
-    pin.cu_seqlens, pin.ck_offsets = ctypes.c_void_p(cu.ctypes.data), ctypes.c_void_p(ck.ctypes.data)
-    pin.N, pin.H, pin.num_cus, pin.ck_every = 1, 2, 256, 8 * 64
-    pl = _lib.KdaPrefillPlan()
-    assert L.kda355_prefill_plan(ctypes.byref(pin), ctypes.byref(pl), None, 0) == 0
-    tab = np.zeros(pl.table_words, np.int32)
-    assert L.kda355_prefill_plan(ctypes.byref(pin), ctypes.byref(pl), ctypes.c_void_p(tab.ctypes.data), tab.size) == 0
-    assert (pl.num_pieces, pl.num_split) == (8, 1)
+    one; a plan made without flags must still cover both): 8192 tokens (128 chunks) on an idle chip, single
+    checkpoint at chunk 40, every-n rows every 8 chunks (row j is the state after 8 j chunks; rows inside the first
+    piece are written by that piece itself)."""
+    pl, tab = _plan([8192], 2, 256, every=8 * 64, ck=[40 * 64])
+    ch = _check_pieces(pl, tab, [8192], 2, every=8, ck_chunk=[40])
+    assert pl.num_split == 1
     off_ckc, nck = tab[13], tab[14]                      # header: compose list offset and length
     tasks = tab[off_ckc:off_ckc + 4 * nck].reshape(nck, 4)
     kinds = tasks[:, 3].tolist()
-    assert kinds.count(1) == 1 and kinds.count(2) == 13 and nck == pl.num_ck_tasks == 14
-    assert tasks[tasks[:, 3] == 1, 0].tolist() == [0]    # the single checkpoint of sequence 0
-    assert sorted(tasks[tasks[:, 3] == 2, 0].tolist()) == list(range(3, 16))   # every-n rows in later pieces
-    assert pl.workspace_bytes == (3 * 8 + 2 * 14) * 2 * 65536 + 7 * 16 * 2 * 16384
+    first_len = int(ch[ch[:, 6] == 0, 1][0])             # chunks of the first piece
+    inside = [j for j in range(1, 16) if 8 * j > first_len]
+    assert kinds.count(1) == (1 if 40 > first_len else 0) and kinds.count(2) == len(inside)
+    assert tasks[tasks[:, 3] == 1, 0].tolist() == ([0] if 40 > first_len else [])   # the single checkpoint of seq 0
+    assert sorted(tasks[tasks[:, 3] == 2, 0].tolist()) == inside                      # every-n rows in later pieces
 
 
 def test_decode_rejects_host_tensors():
