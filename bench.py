@@ -19,6 +19,9 @@ The other configurations are reported beside it (never as `value`):
   serving      (opt-in, --configs ...,serving) the reference's own 13 chunked-prefill steps and 10 decode steps on the
                vLLM page layout, each timed like the reference times them (single call after a 512 MiB cache flush,
                median) beside the reference's published MI350X latency for that workload
+  plain        (opt-in, --configs ...,plain) the reference's 10 phase-1 plain prefill workloads at H = 12 through
+               kda_prefill, timed like the reference (median of 50 flushed single calls, launch included) beside its
+               published MI350X latencies
 
 Roofline: prefill is bound by HBM at these shapes (arithmetic intensity ~120 FLOP/B, below the bf16 ridge of ~312),
 so `roofline` is the HBM fraction of the prefill launch: compulsory bytes (q, k, v, out bf16; g fp32; beta fp32;
@@ -344,6 +347,17 @@ SERVING_DECODE = {  # name: (H, B, S, reference us)
     "s8_h96_b32": (96, 32, 8, 333.78),
 }
 SERVING_TAPS = 10  # conv taps per page: 2 + 8 speculative tokens (the reference's DSpark layout)
+# The reference's phase-1 plain prefill workloads (kda_prefill: gates, beta sigmoid and q/k norms in the kernel,
+# contiguous initial / final states, H = 12) and its published MI350X latencies in ms (median of 50 calls, 256 MB
+# Infinity Cache flushed before each, launch from Python included): kda/mi350x_plain/bench.py:42-53 (lengths),
+# kda/mi350x_plain/README.md:34-45 (latencies).
+PLAIN_H = 12
+PLAIN_PREFILL = {
+    "p_1x1k": ([1024], 0.0302), "p_1x4k": ([4096], 0.0504), "p_1x16k": ([16384], 0.1522),
+    "p_1x64k": ([65536], 0.5331), "p_4x4k": ([4096] * 4, 0.1137), "p_8x2k": ([2048] * 8, 0.1041),
+    "p_16x1k": ([1024] * 16, 0.1025), "p_32x512": ([512] * 32, 0.1084), "p_64x128": ([128] * 64, 0.0666),
+    "p_mixed": ([8192, 1024, 777, 512, 256, 130, 64, 17], 0.1062),
+}
 
 
 def time_flushed_median(fn, reps, torch, flush):
@@ -403,6 +417,32 @@ def bench_serving_prefill(kda, torch, dev, H, seqs, reps, flush, seed):
     us = time_flushed_median(call, reps, torch, flush)
     del raw, P, big_out, ws
     return dict(us=us, T=T, N=N, pieces=meta.split[0])
+
+
+def bench_plain_prefill(kda, torch, dev, lens, reps, flush, seed):
+    """One plain `kda355.kda_prefill` call (the reference's phase-1 interface) on inputs drawn like
+    kda/mi350x_plain/bench.py:57-67; the plan is made once outside the timed region, like the reference's prepare()."""
+    H, N, T = PLAIN_H, len(lens), sum(lens)
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    rn = lambda *sh, sc=1.0: torch.randn(*sh, generator=gen, device=dev) * sc  # noqa: E731
+    q, k, v, raw_g = (rn(1, T, H, D).bfloat16() for _ in range(4))
+    raw_beta = rn(1, T, H).bfloat16()
+    A_log = torch.rand(H, generator=gen, device=dev) * 2 - 1
+    dt_bias = rn(H * D, sc=0.5)
+    state = rn(N, H, D, D, sc=0.05)
+    cu = torch.tensor([0] + [sum(lens[:i + 1]) for i in range(N)], dtype=torch.int32)
+    meta = kda.plan(cu, H, device=dev)
+    cu_d = cu.to(dev)
+
+    def call():
+        kda.kda_prefill(q, k, v, raw_g, raw_beta, A_log, dt_bias, state, cu_d, scale=D ** -0.5, lower_bound=-5.0,
+                        meta=meta)
+
+    for _ in range(5):
+        call()
+    torch.cuda.synchronize()
+    us = time_flushed_median(call, reps, torch, flush)
+    return dict(us=us, T=T, N=N, pieces=meta.plan.num_pieces)
 
 
 # ------------------------------------------------------------------------------------------------ CPU baseline
@@ -543,6 +583,19 @@ def main():
                             "prefill_geomean_ratio": round(gm([x["ratio"] for x in rows if "N" in x]), 3),
                             "decode_geomean_ratio": round(gm([x["ratio"] for x in rows if "B" in x]), 3),
                             "rows": rows}
+    if "plain" in cfgs:  # opt-in: the reference's phase-1 plain prefill workloads beside its published MI350X latencies
+        rows = []
+        for i, (name, (lens, ref)) in enumerate(PLAIN_PREFILL.items()):
+            r = bench_plain_prefill(kda355, torch, dev, lens, max(args.steps, 50), flush, 200 + i)
+            rows.append({"workload": name, "H": PLAIN_H, "N": r["N"], "T": r["T"], "pieces": r["pieces"],
+                         "ms": round(r["us"] * 1e-3, 4), "reference_mi350x_ms": ref,
+                         "ratio": round(ref / (r["us"] * 1e-3), 3)})
+            log(f"plain {name}: {r['us'] * 1e-3:.4f} ms (reference MI350X {ref} ms)")
+        gm = lambda xs: math.exp(sum(math.log(x) for x in xs) / len(xs))  # noqa: E731
+        extra["plain_prefill"] = {"method": "single calls after a 512 MiB cache flush, median of 50, launch from Python "
+                                            "included (kda/mi350x_plain/bench.py:120-138)",
+                                  "mean_ratio": round(sum(x["ratio"] for x in rows) / len(rows), 3),
+                                  "geomean_ratio": round(gm([x["ratio"] for x in rows]), 3), "rows": rows}
 
     cpu = None
     if args.cpu_seconds > 0:

@@ -312,22 +312,42 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
     const bool RB = (p.flags & KDA355_PF_RAW_BETA) != 0;
     const bool NORM = (p.flags & KDA355_PF_NORMALIZE_QK) != 0;
 
-    // ---- initial state (lane: v = 16w + m, k = 16dt + 4g + e)
+    // ---- prologue.  Loads are issued in the order they are needed and none sits under a branch (the memory counter
+    // completes in issue order, and a load on one path only makes the compiler wait for everything older): the first
+    // chunk's rows (P0), the gate's dt_bias (P0), then the initial state, first used by the first walk.
     int tid = threadIdx.x, lane = tid & 63, m = lane & 15, g = lane >> 4, r = tid >> 3, cb = tid & 7;
-    f32x4 S[8];
+    RawRow nx;
+    load_row<RG>(p, h, tstart, nch > 0 ? min(64, len) : 0, r, cb, RB, nx);  // an empty sequence loads nothing
+    const float dtb = RG ? p.dt_bias[h * D + (tid & (D - 1))] : 0.f;
+    // initial state (lane: v = 16w + m, k = 16dt + 4g + e), through a descriptor of no records when there is none
     const float* src = nullptr;
     int64_t row = -1;
     if (pool) row = p.state_idx[n];
     if (fix) {
         // a later piece's local run starts from zero
     } else if (pool) {
-        if (row >= 0 && row < p.state_slots && p.has_init[n]) src = p.state_pool + row * p.state_ss + (int64_t)h * D * D;
+        // has_initial_state[n] by a scalar read of its aligned word through the constant address space (read-only
+        // for the kernel; a uniform address there becomes s_load_dword, so no vector load has to be waited for)
+        const uintptr_t ha = reinterpret_cast<uintptr_t>(p.has_init + n);
+        typedef const __attribute__((address_space(4))) uint32_t cword_t;
+        const uint32_t hword = *reinterpret_cast<cword_t*>(ha & ~(uintptr_t)3);
+        const bool hinit = ((hword >> (8 * (ha & 3))) & 0xffu) != 0;
+        if (row >= 0 && row < p.state_slots && hinit) src = p.state_pool + row * p.state_ss + (int64_t)h * D * D;
     } else if (p.init_state) {
         src = p.init_state + ((int64_t)n * H + h) * D * D;
     }
+    f32x4 S[8];
+    {
+        // base and size taken through readfirstlane: a descriptor the compiler cannot see as wave-uniform becomes a
+        // waterfall loop
+        const int nrec = __builtin_amdgcn_readfirstlane(src ? D * D * 4 : 0);
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            uniform_ptr(src ? static_cast<const void*>(src) : static_cast<const void*>(p.q)), (short)0, nrec, 0x00020000);
+        const int voff = ((16 * w + m) * D + 4 * g) * 4;
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt)
-        S[dt] = src ? *reinterpret_cast<const f32x4*>(src + (16 * w + m) * D + 16 * dt + 4 * g) : f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int dt = 0; dt < 8; ++dt)
+            S[dt] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, voff + 64 * dt, 0, 0));
+    }
     f32x4 Pm[8];  // fix: the transition, P[k][k'] at (k = 16dt + 4g + e, k' = 16w + m); starts as the identity
     if (fix) {
 #pragma unroll
@@ -345,23 +365,20 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
             store_state(reinterpret_cast<float*>(p.ck_pool) + rr * p.ck_ss + (int64_t)h * D * D, S, w, g, m);
     };
     const int ck_row0 = chain[C_CKROW0];
-    if (ck_mode == 2 && every > 0 && nch > 0 && first == 0) ck_store(ck_idx[ck_row0]);
     const int ck_single = (ck_mode == 1) ? chain[C_CKSINGLE] : 0;
 
     // gate-in-kernel constants for this thread's 16 channels
     float Aexp = 0.f;
     if (RG) {
         Aexp = __expf(p.A_log[h]);
-        if (tid < D) sDT[tid] = p.dt_bias[h * D + tid];
+        if (tid < D) sDT[tid] = dtb;
     }
     // A_qk blocks (0,1) and (2,3) are read by the walk and never written by the Gram phase
     for (int e = tid; e < 2 * 16 * 16; e += PF_THREADS) {
         const int b = e >> 8, ii = (e >> 4) & 15, jj = e & 15;
         sAq[(32 * b + ii) * RS16S + 32 * b + pos32(16 + jj)] = (half_t)0.f;
     }
-
-    RawRow nx;
-    if (nch > 0) load_row<RG>(p, h, tstart, min(64, len), r, cb, RB, nx);
+    lds_barrier();  // sDT and the zeroed A_qk blocks are visible to every wave
 
     for (int cl = 0; cl < nch; ++cl) {
         // Lane indices are re-derived every chunk from an opaque copy so that the per-lane LDS addresses of all phases
@@ -375,14 +392,9 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
         cb = tid & 7;
         const int t0 = tstart + 64 * cl, L = min(64, len - 64 * cl);
         // ================= P0: this chunk's raw rows (prefetched during the previous chunk)
-        // The raw q, k, v go to LDS slots that only this thread reads back and later overwrites (q: first half of its
-        // q^ fi slot in region B, k: of its k^ fj slot in region C, v: the W area, which is free until P6), so the
-        // registers die here and the next chunk's loads reuse them without a loop-carried copy.
-        const int sl0 = 16 * (cb >> 1), sl1 = 16 * (1 ^ (cb >> 1));  // swizzled slots 0 and 1 of the segment
-        *reinterpret_cast<u32x4*>(lds + LDS_B + r * (4 * RS32) + 64 * cb + sl0) = nx.q[0];
-        *reinterpret_cast<u32x4*>(lds + LDS_B + r * (4 * RS32) + 64 * cb + sl1) = nx.q[1];
-        *reinterpret_cast<u32x4*>(lds + LDS_C + r * (4 * RS32) + 64 * cb + sl0) = nx.k[0];
-        *reinterpret_cast<u32x4*>(lds + LDS_C + r * (4 * RS32) + 64 * cb + sl1) = nx.k[1];
+        // The raw q and k stay in registers until P2 (the next chunk's q, k loads reuse them from P5 on); the raw v
+        // goes to an LDS slot that only this thread reads back (the W area, which is free until P6), so its registers
+        // die here and the next chunk's v loads reuse them without a loop-carried copy.
         *reinterpret_cast<u32x4*>(lds + LDS_W + r * (2 * RS16) + 32 * cb) = nx.v[0];
         *reinterpret_cast<u32x4*>(lds + LDS_W + r * (2 * RS16) + 32 * cb + 16) = nx.v[1];
         float gv[16];
@@ -451,11 +463,7 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
         {
             float qf[16], kf[16], qfi[16], kfj[16];
             {
-                const unsigned char* qs = lds + LDS_B + r * (4 * RS32) + 64 * cb;
-                const unsigned char* ks = lds + LDS_C + r * (4 * RS32) + 64 * cb;
-                const int sl0 = 16 * (cb >> 1), sl1 = 16 * (1 ^ (cb >> 1));
-                const u32x4 a[2] = {*reinterpret_cast<const u32x4*>(qs + sl0), *reinterpret_cast<const u32x4*>(qs + sl1)};
-                const u32x4 b[2] = {*reinterpret_cast<const u32x4*>(ks + sl0), *reinterpret_cast<const u32x4*>(ks + sl1)};
+                const u32x4 a[2] = {nx.q[0], nx.q[1]}, b[2] = {nx.k[0], nx.k[1]};
                 unpack16(a, qf);
                 unpack16(b, kf);
             }
@@ -644,6 +652,12 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
         }
         lds_barrier();
         // ================= P5: Q~, Kd^T, beta v into their walk layouts (raw threads)
+        // The initial state loads (issued in the prologue) complete here, before any next-chunk row is in flight: an
+        // empty use of S makes the compiler's wait for them fall at this point, where in every later chunk only the
+        // long-finished output stores are outstanding, instead of before each walk, where it would also wait for
+        // the prefetched rows.
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) asm volatile("" : "+v"(S[dt]));
         // the next chunk's q, k rows: issued here, consumed at the next P0 (their registers are free during P1..P4)
         if (cl + 1 < nch) load_row_qk(p, h, t0 + 64, min(64, len - 64 * (cl + 1)), r, cb, nx);
         float qfi[16], kfj[16], vf[16];
@@ -731,6 +745,9 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
         lds_barrier();
         // ================= P7: the walk
         if (cl + 1 < nch) load_row_g<RG>(p, h, t0 + 64, min(64, len - 64 * (cl + 1)), r, cb, nx);
+        // every-n row 0 is the state before the sequence's first token: stored before the first walk changes S (here
+        // rather than in the prologue, so that nothing before the first walk waits for the state loads)
+        if (cl == 0 && ck_mode == 2 && every > 0 && first == 0) ck_store(ck_idx[ck_row0]);
         if (fix) {  // S <- (diag(d) - Kd^T W) S + Kd^T U and P <- (diag(d) - Kd^T W) P, sharing every A fragment
             f16x8 SB[4], PB[4];
 #pragma unroll
