@@ -327,7 +327,8 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
         // a later piece's local run starts from zero
     } else if (pool) {
         // has_initial_state[n] by a scalar read of its aligned word through the constant address space (read-only
-        // for the kernel; a uniform address there becomes s_load_dword, so no vector load has to be waited for)
+        // for the kernel; a uniform address there becomes s_load_dword, so no vector load has to be waited for).
+        // The aligned word may cover bytes next to the flag but never leaves the flag's page.
         const uintptr_t ha = reinterpret_cast<uintptr_t>(p.has_init + n);
         typedef const __attribute__((address_space(4))) uint32_t cword_t;
         const uint32_t hword = *reinterpret_cast<cword_t*>(ha & ~(uintptr_t)3);
