@@ -1244,49 +1244,71 @@ extern "C" int kda355_prefill_plan(const KdaPrefillPlanIn* in, KdaPrefillPlan* p
     }
     // Pieces.  A workgroup walks one (piece, head) chain and a CU holds one such workgroup at a time; the chain list is
     // dispatched longest first.  Candidate cuts: every sequence longer than a piece length T is cut into
-    // ceil(nch / T) near-equal pieces of >= MIN_PIECE chunks, for T on a geometric ladder from a quarter of the
-    // balanced per-CU load.  Each candidate is costed in chunk times (one chunk of one head on one CU, ~11 us) by
+    // ceil(nch / T) near-equal pieces of >= MIN_PIECE chunks, or into pieces of T chunks followed by the remainder
+    // (which fills CUs the long pieces leave idle: 16 chunks on 3/4 of the CUs cut as 12 + 4), for T on a geometric
+    // ladder from a quarter of the balanced per-CU load.  Each candidate is costed in chunk times (one chunk of one head on one CU, ~11 us) by
     // list-scheduling its chains onto the CUs (later pieces cost as much per chunk as first ones), plus the passes a
     // split adds: the scan, sequential over the pieces of a sequence (SCAN_BASE + STEP_UNITS per later piece of the
-    // most-cut sequence), and the output fixup (FIX_BASE + FIX_UNITS per chunk-head of later pieces, spread over the
-    // chip).  The cheapest candidate wins; ties keep fewer pieces.  The first piece of a split sequence runs from the
+    // most-cut sequence, + SCAN_WG_UNITS per scan workgroup per CU: 8 per split sequence and head), and the output
+    // fixup (FIX_BASE + FIX_UNITS per chunk-head of later pieces, spread over the chip); every workgroup also pays a
+    // start-up of START_QUARTERS / 4 chunk times.  The cheapest candidate wins; ties keep fewer pieces.  The first piece of a split sequence runs from the
     // true start state; later pieces run from S = 0, carry their transition and are completed by the scan, fixup and
     // checkpoint-compose kernels.  Measured on MI355X: scan steps ~2.7 us, fixup ~11 ns per chunk-head.
     constexpr int MIN_PIECE = 2;
-    constexpr double SCAN_BASE = 0.5, STEP_UNITS = 0.25, FIX_BASE = 0.5, FIX_UNITS = 0.0012;
+    constexpr double SCAN_BASE = 0.5, STEP_UNITS = 0.25, SCAN_WG_UNITS = 0.25, FIX_BASE = 0.5, FIX_UNITS = 0.0012;
+    constexpr int64_t START_QUARTERS = 4;  // a workgroup's start-up (state, first rows): about one chunk time
     const int num_cus = in->num_cus > 0 ? in->num_cus : 256;
-    std::vector<int> npieces(N, 1);
+    // chunk counts of the pieces of a c-chunk sequence for piece length T: near-equal (mode 0), or T chunks each and
+    // the remainder last (mode 1; a remainder under MIN_PIECE joins the piece before it)
+    auto piece_lengths = [](int c, int T, int mode, std::vector<int>& out) {
+        out.clear();
+        if (c <= T || c < 2 * MIN_PIECE) {
+            out.push_back(c);
+        } else if (mode == 0) {
+            const int np = std::max(1, std::min(c / MIN_PIECE, (c + T - 1) / T));
+            for (int pc = 0; pc < np; ++pc) out.push_back(c / np + (pc < c % np ? 1 : 0));
+        } else {
+            int left = c;
+            while (left > T) { out.push_back(T); left -= T; }
+            if (left >= MIN_PIECE) out.push_back(left); else out.back() += left;
+        }
+    };
+    int cutT = 1 << 30, cutMode = 0;  // no cut unless the cost model finds one
     if (nchunks > 0) {
         int maxc = 0;
         for (int n = 0; n < N; ++n) maxc = std::max(maxc, nch[n]);
         const int64_t avg = std::max<int64_t>(1, (nchunks * in->H + num_cus - 1) / num_cus);
         const bool idle = (int64_t)N * in->H < num_cus;
         if ((idle || 4 * (int64_t)maxc > 5 * avg) && maxc >= 2 * MIN_PIECE) {
-            auto cut = [&](int n, int T) { return nch[n] > T ? std::max(1, std::min(nch[n] / MIN_PIECE, (nch[n] + T - 1) / T)) : 1; };
-            std::vector<int> counts;
+            std::vector<int> counts, lens;
             std::vector<int64_t> loads;
             const int64_t total_units = nchunks * in->H;
             double best = 0.0;
-            auto cost = [&](int T, bool first) {
+            auto cost = [&](int T, int mode, bool first) {
                 counts.clear();
                 int64_t fixch = 0;
-                bool split = false;
-                int most = 0, maxnp = 1;
+                int nsplit = 0, most = 0, maxnp = 1;
                 for (int n = 0; n < N; ++n) {
-                    const int np = cut(n, T);
+                    piece_lengths(nch[n], T, mode, lens);
+                    const int np = (int)lens.size();
                     maxnp = std::max(maxnp, np);
                     for (int pc = 0; pc < np; ++pc) {
-                        const int c = nch[n] / np + (pc < nch[n] % np ? 1 : 0);
+                        const int c = lens[pc];
                         counts.push_back(c);
                         most = std::max(most, c);
                         if (pc > 0) fixch += c;
                     }
-                    split |= np > 1;
+                    nsplit += np > 1;
                 }
-                const double extra = split ? SCAN_BASE + STEP_UNITS * (maxnp - 1) + FIX_BASE + FIX_UNITS * (double)fixch * in->H
-                                           : 0.0;
+                const double extra =
+                    nsplit ? SCAN_BASE + STEP_UNITS * (maxnp - 1) + SCAN_WG_UNITS * 8.0 * nsplit * in->H / num_cus +
+                                 FIX_BASE + FIX_UNITS * (double)fixch * in->H
+                           : 0.0;
+                // loads in quarter chunk times: a workgroup costs its chunks plus its start-up
+                const int64_t q_total = 4 * total_units + START_QUARTERS * (int64_t)counts.size() * in->H;
                 // no schedule beats the longest piece or the perfect balance
-                const double bound = (double)std::max<int64_t>(most, (total_units + num_cus - 1) / num_cus) + extra;
+                const double bound =
+                    0.25 * (double)std::max<int64_t>(4 * most + START_QUARTERS, (q_total + num_cus - 1) / num_cus) + extra;
                 if (!first && bound >= best) return bound;
                 std::sort(counts.begin(), counts.end(), std::greater<int>());
                 // list scheduling, longest first: each workgroup goes to the CU that frees up first
@@ -1295,21 +1317,21 @@ extern "C" int kda355_prefill_plan(const KdaPrefillPlanIn* in, KdaPrefillPlan* p
                 for (int c : counts)
                     for (int hh = 0; hh < in->H; ++hh) {
                         std::pop_heap(loads.begin(), loads.end(), std::greater<int64_t>());
-                        loads.back() += c;
+                        loads.back() += 4 * c + START_QUARTERS;
                         span = std::max(span, loads.back());
                         std::push_heap(loads.begin(), loads.end(), std::greater<int64_t>());
                     }
-                return (double)span + extra;
+                return 0.25 * (double)span + extra;
             };
-            int bestT = maxc;
-            best = cost(maxc, true);
+            best = cost(maxc, 0, true);
             // pieces shorter than a quarter of the balanced load per CU only add fixup work: the ladder starts there
             for (double t = std::max<double>(MIN_PIECE, (double)avg / 4); t < maxc; t *= 1.12) {
                 const int T = (int)t;
-                const double c = cost(T, false);
-                if (c < best - 1e-9) { best = c; bestT = T; }
+                for (int mode = 0; mode < 2; ++mode) {
+                    const double c = cost(T, mode, false);
+                    if (c < best - 1e-9) { best = c; cutT = T; cutMode = mode; }
+                }
             }
-            for (int n = 0; n < N; ++n) npieces[n] = cut(n, bestT);
         }
     }
     std::vector<int> ck_chunk(N, 0), ck_row0(N, 0);
@@ -1331,11 +1353,14 @@ extern "C" int kda355_prefill_plan(const KdaPrefillPlanIn* in, KdaPrefillPlan* p
     std::vector<Piece> pieces;
     std::vector<CkTask> cktasks;
     int nslots = 0, nsplit = 0, nrslots = 0, nfix = 0, nsplitpieces = 0;
+    std::vector<int> plens, npieces(N, 1);
     for (int n = 0; n < N; ++n) {
-        const int np = npieces[n];
+        piece_lengths(nch[n], cutT, cutMode, plens);
+        const int np = (int)plens.size();
+        npieces[n] = np;
         int f = 0;
         for (int pc = 0; pc < np; ++pc) {
-            const int c = nch[n] / np + (pc < nch[n] % np ? 1 : 0);
+            const int c = plens[pc];
             Piece P{n, f, c, np > 1 ? nslots + pc : 0, 0, 0, 0, 0};
             if (np == 1) {
                 P.flags = PIECE_LAST;

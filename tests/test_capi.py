@@ -156,9 +156,10 @@ def test_prefill_plan_splits_long_sequences():
     lens1 = [4011, 4318, 6249, 7799, 532, 1400, 6787, 7785]   # configuration 1: 256 chains on 256 CUs
     pl, tab = _plan(lens1, 32, 256)
     # 611 chunks x 32 heads = 77 per CU at balance, but the longest chain has 122 chunks: the long sequences are cut
-    # into pieces, none longer than 64 chunks
+    # into pieces (a cut may be T chunks followed by the remainder), and no piece is longer than the balanced load
+    # plus a quarter of it
     counts = _check_pieces(pl, tab, lens1, 32)[:, 1]
-    assert pl.num_split >= 2 and pl.num_pieces > pl.num_split and counts.max() <= 64
+    assert pl.num_split >= 2 and pl.num_pieces > pl.num_split and counts.max() <= 77 * 5 // 4
     assert list(counts) == sorted(counts, reverse=True)                         # longest first
     pl, _ = _plan(lens1, 32, 64)                         # a quarter of the CUs: 306 chunks per CU, nothing is split
     assert pl.num_pieces == 0
