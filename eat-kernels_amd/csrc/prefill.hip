@@ -1332,6 +1332,17 @@ extern "C" int kda355_prefill_plan(const KdaPrefillPlanIn* in, KdaPrefillPlan* p
                     if (c < best - 1e-9) { best = c; cutT = T; cutMode = mode; }
                 }
             }
+            // then piece lengths within one ladder step of the best (at most ~32 per cut style)
+            if (cutT < maxc) {
+                const int lo = std::max(MIN_PIECE, (int)(cutT / 1.12)), hi = std::min(maxc - 1, (int)(cutT * 1.12) + 1);
+                const int T0 = cutT, step = std::max(1, (hi - lo) / 32);
+                for (int T = lo; T <= hi; T += step)
+                    for (int mode = 0; mode < 2; ++mode) {
+                        if (T == T0) continue;
+                        const double c = cost(T, mode, false);
+                        if (c < best - 1e-9) { best = c; cutT = T; cutMode = mode; }
+                    }
+            }
         }
     }
     std::vector<int> ck_chunk(N, 0), ck_row0(N, 0);
