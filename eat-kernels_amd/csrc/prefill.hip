@@ -269,6 +269,25 @@ __device__ __forceinline__ void store_state_bf16(uint16_t* dst, const f32x4 (&S)
     }
 }
 
+// The operand of this lane tile (rows a = 16 w + m, columns b = 16 dt + 4 g + e of a [128][128] fp32 array) stored in
+// the scan's blocked order: element (a, b) at ((a / 4) * 128 + b) * 4 + a % 4, i.e. for every group of 4 rows, the
+// 4 values of each column contiguous and the columns in order.  A scan lane's 4 values of one column are then one
+// 16-byte load and neighbouring lanes (columns) read neighbouring 16 bytes.  Staged through LDS rows of RS32 floats:
+// every thread writes its tile row-major, one barrier, then every thread gathers 8 four-row column pieces.
+__device__ __forceinline__ void stage_state(float* stage, const f32x4 (&S)[8], int w, int g, int m) {
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) *reinterpret_cast<f32x4*>(stage + (16 * w + m) * RS32 + 16 * dt + 4 * g) = S[dt];
+}
+__device__ __forceinline__ void copy_staged_blocked(float* dst, const float* stage) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int i = threadIdx.x + PF_THREADS * j, a4 = i >> 7, b = i & 127;
+        const f32x4 v = {stage[(4 * a4) * RS32 + b], stage[(4 * a4 + 1) * RS32 + b], stage[(4 * a4 + 2) * RS32 + b],
+                         stage[(4 * a4 + 3) * RS32 + b]};
+        *reinterpret_cast<f32x4*>(dst + 4 * i) = v;
+    }
+}
+
 // The chunk walk with outputs, checkpoints and states.  P1 = true compiles in the pieces of split sequences: an entry
 // flagged PIECE_FIX starts from S = 0 and also carries its state transition P (S_end = P S_start + S_loc); its outputs
 // are partial (fp16, without the S_start term), and for every chunk it stores R = Q~ P + A_qk (-W P), the operand of
@@ -894,9 +913,15 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
         lds_barrier();
     }
     if (nch > 0) store_out_slot(p, h, tstart + 64 * (nch - 1), min(64, len - 64 * (nch - 1)), r, cb, lds);
-    if (fix) {  // the piece's local end state and transition (stored [k'][k])
-        store_state(ws_h, S, w, g, m);
-        store_state(ws_h + ws_arr, Pm, w, g, m);
+    if (fix) {  // the piece's local end state and transition, in the scan's blocked order (LDS is free after the loop)
+        float* st0 = reinterpret_cast<float*>(lds);
+        float* st1 = st0 + D * RS32;
+        lds_barrier();  // every thread has read its output slot
+        stage_state(st0, S, w, g, m);
+        stage_state(st1, Pm, w, g, m);
+        lds_barrier();
+        copy_staged_blocked(ws_h, st0);
+        copy_staged_blocked(ws_h + ws_arr, st1);
         return;
     }
     if (P1 && (pflags & PIECE_STORE_END)) {  // the first piece of a split sequence: the second piece's start state
@@ -979,13 +1004,59 @@ __device__ __forceinline__ void scan_task(int H, int& ei, int& h, int& rb) {
     h = eh - ei * H;
 }
 
+// The scan's operands: later pieces store their transition P and local end state S_loc in blocked order (element
+// (a, b) at ((a / 4) * 128 + b) * 4 + a % 4, a = the row of the row-major array: k' for P[k'][k], v for S_loc[v][k]), so
+// a lane's B values P[32 kq + 4 s4 .. + 3][col] are one 16-byte load each (eight per tile and step) and its L values
+// L[16 rb + 4 kq .. + 3][col] one more, with the 16 lanes of a row group reading 256 contiguous bytes.  The scan runs
+// 4 waves per workgroup, wave w on the two 16-column tiles 32 w + 16 ct + j: one register set of operands is 72 VGPRs;
+// three sets leave two workgroups per CU, which a scan of one or two steps over many sequences needs more than a
+// shorter step.
+constexpr int SCAN_THREADS = 256;
+struct ScanOps {
+    f32x4 b[2][8];  // b[ct][s4] = P[32 kq + 4 s4 .. + 3][32 w + 16 ct + j]
+    f32x4 l[2];     // l[ct] = L[16 rb + 4 kq .. + 3][32 w + 16 ct + j]
+};
+// Buffer loads: the lane part of the address is one VGPR, the 2 KiB steps between a lane's eight operand rows are
+// scalar offsets (a global load's immediate offset does not reach them, and 64-bit addresses per load cost VGPRs).
+__device__ __forceinline__ void fetch_scan(const float* PB, const float* LB, int rb, ScanOps& o) {
+    const int j = threadIdx.x & 15, kq = (threadIdx.x & 63) >> 4, w = threadIdx.x >> 6;
+    const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(PB), (short)0, D * D * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rl = __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(LB), (short)0, D * D * 4, 0x00020000);
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) {
+        const int col = 32 * w + 16 * ct + j;
+#pragma unroll
+        for (int s4 = 0; s4 < 8; ++s4)
+            o.b[ct][s4] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rp, (8 * kq * D + col) * 16,
+                                                                                          s4 * D * 16, 0));
+        o.l[ct] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rl, ((4 * rb + kq) * D + col) * 16, 0, 0));
+    }
+}
+// acc[ct][e] = out[4 kq + e][32 w + 16 ct + j]; sX staged and synced
+__device__ __forceinline__ void compose_scan(const float* sX, const ScanOps& o, f32x4 (&acc)[2]) {
+    const int j = threadIdx.x & 15, kq = (threadIdx.x & 63) >> 4;
+    acc[0] = o.l[0];
+    acc[1] = o.l[1];
+#pragma unroll
+    for (int s4 = 0; s4 < 8; ++s4) {
+        const f32x4 a = *reinterpret_cast<const f32x4*>(sX + j * SC_XS + 32 * kq + 4 * s4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], o.b[0][s4][e], acc[0], 0, 0, 0);
+            acc[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], o.b[1][s4][e], acc[1], 0, 0, 0);
+        }
+    }
+}
+
 // Split sequences: X_1 = the first piece's end state (stored by that piece), X_{p+1} = P_p X_p + S_loc(p) for the
 // later pieces p = 1 .. np-1; X_p is the start state of piece p, X_np the sequence's final state.  One workgroup per
 // (sequence, head, block of 16 state rows).  X_p sits in LDS buffer (p - 1) % 2: step p reads one buffer and writes
 // the other, so one barrier per step orders both (a wave writes buffer p % 2 only after every wave has passed step
 // p's barrier, i.e. finished reading that buffer in step p - 1).  The barrier covers LDS only: the global stores of
-// the states are not waited for.
-__global__ void __launch_bounds__(SC_THREADS) scan_kernel(PfParams p, const int32_t* __restrict__ tab) {
+// the states are not waited for.  A freshly written transition takes about two compositions to arrive, so each
+// piece's operands are fetched two steps ahead, into one of three register sets (refilled right after the step that
+// used it, behind that step's state stores, so that a wait for a store never waits for a prefetch).
+__global__ void __launch_bounds__(SCAN_THREADS) scan_kernel(PfParams p, const int32_t* __restrict__ tab) {
     extern __shared__ __align__(16) unsigned char lds[];
     float* sX = reinterpret_cast<float*>(lds);
     const int H = p.H;
@@ -994,7 +1065,7 @@ __global__ void __launch_bounds__(SC_THREADS) scan_kernel(PfParams p, const int3
     const int32_t* e = tab + tab[H_OFF_SCAN] + S_WORDS * si;
     const int n = e[S_SEQ], np = e[S_NP], slot0 = e[S_SLOT0];
     const int64_t ws_arr = (int64_t)tab[H_NSLOTS] * H * D * D;
-    const int col = compose_col(), r0 = compose_row0();
+    const int j = threadIdx.x & 15, kq = (threadIdx.x & 63) >> 4, w = threadIdx.x >> 6;
     const int64_t blk = (int64_t)SC_ROWS * rb * D;  // the block's first element in a state
     float* fin = nullptr;  // the final state's destination (same rules as the chunk walk)
     if (p.flags & KDA355_PF_POOL) {
@@ -1003,38 +1074,59 @@ __global__ void __launch_bounds__(SC_THREADS) scan_kernel(PfParams p, const int3
     } else {
         fin = p.final_state + ((int64_t)n * H + h) * D * D;
     }
-    // piece pc's operands: P at array 1, S_loc at array 0 of the workspace
-    auto fetch = [&](int pc, ComposeOps& o) {
+    // piece pc's operands: P at array 1, S_loc at array 0 of the workspace (both in blocked order)
+    auto fetch = [&](int pc, ScanOps& o) {
         const int64_t so = ((int64_t)(slot0 + pc) * H + h) * D * D;
-        fetch_ops(p.ws + ws_arr + so, p.ws + so + blk, o);
+        fetch_scan(p.ws + ws_arr + so, p.ws + so, rb, o);
     };
-    // step pc: X_{pc+1} = P_pc X_pc + S_loc(pc) from `cur`, fetching piece pc + 1's operands into `nxt` meanwhile.
-    // Every step issues the same memory operations (the last one fetches its own piece again, a missing final-state
-    // destination is a store descriptor of no records): with no operation under a branch, the wait for `cur` counts
-    // only the operations issued after it, and never waits for the prefetch.
-    auto step = [&](int pc, const ComposeOps& cur, ComposeOps& nxt) {
-        fetch(min(pc + 1, np - 1), nxt);
+    // step pc: X_{pc+1} = P_pc X_pc + S_loc(pc) from `o`, which then receives piece pc + 3's operands.  Every step
+    // issues the same memory operations, and the loop runs whole groups of three steps: fetches past the last piece
+    // repeat it, and a step past the last one (or a missing final-state destination) stores through a descriptor
+    // of no records.  With no operation under a branch, the wait for `o` counts only the operations issued after it.
+    auto step = [&](int pc, ScanOps& o) {
         lds_barrier();  // X_pc is complete in its buffer
         f32x4 acc[2];
-        compose_ops(sX + ((pc - 1) & 1) * SC_BUF, cur, acc);
+        compose_scan(sX + ((pc - 1) & 1) * SC_BUF, o, acc);
         float* sN = sX + (pc & 1) * SC_BUF;
-        const float* dst = (pc + 1 < np) ? p.ws + 2 * ws_arr + ((int64_t)(slot0 + pc + 1) * H + h) * D * D : fin;
+        const float* dst = (pc + 1 < np) ? p.ws + 2 * ws_arr + ((int64_t)(slot0 + pc + 1) * H + h) * D * D
+                                         : (pc + 1 == np ? fin : nullptr);
         const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
             uniform_ptr(dst ? dst : p.ws), (short)0, dst ? D * D * 4 : 0, 0x00020000);
 #pragma unroll
-        for (int ee = 0; ee < 4; ++ee) {
-            const f32x2 v = {acc[0][ee], acc[1][ee]};
-            *reinterpret_cast<f32x2*>(sN + (r0 + ee) * SC_XS + col) = v;
-            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, v), rs,
-                                                  (int)(blk + (r0 + ee) * D + col) * 4, 0, 0);
-        }
+        for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+            for (int ee = 0; ee < 4; ++ee) {
+                const int rr = 4 * kq + ee, col = 32 * w + 16 * ct + j;
+                sN[rr * SC_XS + col] = acc[ct][ee];
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[ct][ee]), rs, (int)(blk + rr * D + col) * 4, 0,
+                                                      0);
+            }
+        fetch(min(pc + 3, np - 1), o);
     };
-    ComposeOps oa, ob;
+    // X_1's 16 rows (one 16-byte piece per thread) are loaded first, then the first three pieces' operands; the
+    // LDS write of X_1 then waits for X_1 alone (the compiler barriers keep the loads in this order)
+    const float* X1 = p.ws + 2 * ws_arr + ((int64_t)(slot0 + 1) * H + h) * D * D + blk;
+    f32x4 x1[2];  // two 16-byte pieces per thread: piece i = threadIdx.x + 256 q -> row i / 32, columns 4 (i % 32)
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        const int i = threadIdx.x + SCAN_THREADS * q;
+        x1[q] = *reinterpret_cast<const f32x4*>(X1 + (i >> 5) * D + 4 * (i & 31));
+    }
+    asm volatile("" ::: "memory");
+    ScanOps oa, ob, oc;
     fetch(1, oa);
-    stage_X(p.ws + 2 * ws_arr + ((int64_t)(slot0 + 1) * H + h) * D * D + blk, sX);
-    for (int pc = 1; pc < np; pc += 2) {
-        step(pc, oa, ob);
-        if (pc + 1 < np) step(pc + 1, ob, oa);
+    fetch(min(2, np - 1), ob);
+    fetch(min(3, np - 1), oc);
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        const int i = threadIdx.x + SCAN_THREADS * q;
+        *reinterpret_cast<f32x4*>(sX + (i >> 5) * SC_XS + 4 * (i & 31)) = x1[q];
+    }
+    for (int pc = 1; pc < np; pc += 3) {
+        step(pc, oa);
+        step(pc + 1, ob);
+        step(pc + 2, oc);
     }
 }
 
@@ -1193,23 +1285,23 @@ hipError_t launch_chunk(const PfParams& p, int list_off, int entries, hipStream_
     return hipGetLastError();
 }
 template <typename K>
-hipError_t launch_composer(K kernel, const PfParams& p, int entries, hipStream_t s, bool& attr_set) {
+hipError_t launch_composer(K kernel, const PfParams& p, int entries, int threads, hipStream_t s, bool& attr_set) {
     if (!attr_set) {  // idempotent; a race only repeats the call
         const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, SC_SMEM);
         if (e != hipSuccess) return e;
         attr_set = true;
     }
-    hipLaunchKernelGGL(kernel, dim3(entries * p.H * (D / SC_ROWS)), dim3(SC_THREADS), SC_SMEM, s, p, p.tab);
+    hipLaunchKernelGGL(kernel, dim3(entries * p.H * (D / SC_ROWS)), dim3(threads), SC_SMEM, s, p, p.tab);
     return hipGetLastError();
 }
 hipError_t launch_scan(const PfParams& p, int entries, hipStream_t s) {
     static bool attr_set = false;
-    return launch_composer(scan_kernel, p, entries, s, attr_set);
+    return launch_composer(scan_kernel, p, entries, SCAN_THREADS, s, attr_set);
 }
 hipError_t launch_ck_compose(const PfParams& p, int entries, hipStream_t s) {
     static bool attr_set = false;
-    return launch_composer(ck_compose_kernel, p, entries, s, attr_set);
+    return launch_composer(ck_compose_kernel, p, entries, SC_THREADS, s, attr_set);
 }
 hipError_t launch_fixup(const PfParams& p, int entries, hipStream_t s) {
     hipLaunchKernelGGL(fixup_kernel, dim3(entries * p.H), dim3(FX_THREADS), FX_SMEM, s, p, p.tab);
@@ -1255,7 +1347,7 @@ extern "C" int kda355_prefill_plan(const KdaPrefillPlanIn* in, KdaPrefillPlan* p
     // true start state; later pieces run from S = 0, carry their transition and are completed by the scan, fixup and
     // checkpoint-compose kernels.  Measured on MI355X: scan steps ~2.7 us, fixup ~11 ns per chunk-head.
     constexpr int MIN_PIECE = 2;
-    constexpr double SCAN_BASE = 0.5, STEP_UNITS = 0.25, SCAN_WG_UNITS = 0.25, FIX_BASE = 0.5, FIX_UNITS = 0.0012;
+    constexpr double SCAN_BASE = 0.5, STEP_UNITS = 0.15, SCAN_WG_UNITS = 0.25, FIX_BASE = 0.5, FIX_UNITS = 0.0012;
     constexpr int64_t START_QUARTERS = 4;  // a workgroup's start-up (state, first rows): about one chunk time
     const int num_cus = in->num_cus > 0 ? in->num_cus : 256;
     // chunk counts of the pieces of a c-chunk sequence for piece length T: near-equal (mode 0), or T chunks each and
