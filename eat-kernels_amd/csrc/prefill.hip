@@ -287,6 +287,21 @@ __device__ __forceinline__ void copy_staged_blocked(float* dst, const float* sta
         *reinterpret_cast<f32x4*>(dst + 4 * i) = v;
     }
 }
+// A staged [128][128] fp32 array as the bf16 pair hi = RNE(x), lo = RNE(x - hi) (two arrays of 16384 bf16, lo after
+// hi), each in the order: element (a, b) at ((a / 8) * 128 + b) * 8 + a % 8, i.e. the 8 values of each column in one
+// group of 8 rows are 16 contiguous bytes, the operand of one lane of a bf16 16x16x32 MFMA.
+__device__ __forceinline__ void copy_staged_split(uint16_t* dst, const float* stage) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int i = threadIdx.x + PF_THREADS * j, a8 = i >> 7, b = i & 127;
+        uint32_t hi[4], lo[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            split_bf16x2(stage[(8 * a8 + 2 * r) * RS32 + b], stage[(8 * a8 + 2 * r + 1) * RS32 + b], hi[r], lo[r]);
+        *reinterpret_cast<u32x4*>(dst + 8 * i) = u32x4{hi[0], hi[1], hi[2], hi[3]};
+        *reinterpret_cast<u32x4*>(dst + D * D + 8 * i) = u32x4{lo[0], lo[1], lo[2], lo[3]};
+    }
+}
 
 // The chunk walk with outputs, checkpoints and states.  P1 = true compiles in the pieces of split sequences: an entry
 // flagged PIECE_FIX starts from S = 0 and also carries its state transition P (S_end = P S_start + S_loc); its outputs
@@ -913,7 +928,7 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
         lds_barrier();
     }
     if (nch > 0) store_out_slot(p, h, tstart + 64 * (nch - 1), min(64, len - 64 * (nch - 1)), r, cb, lds);
-    if (fix) {  // the piece's local end state and transition, in the scan's blocked order (LDS is free after the loop)
+    if (fix) {  // the piece's local end state (blocked order) and transition (bf16 pair) for the scan; LDS is free now
         float* st0 = reinterpret_cast<float*>(lds);
         float* st1 = st0 + D * RS32;
         lds_barrier();  // every thread has read its output slot
@@ -921,7 +936,7 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
         stage_state(st1, Pm, w, g, m);
         lds_barrier();
         copy_staged_blocked(ws_h, st0);
-        copy_staged_blocked(ws_h + ws_arr, st1);
+        copy_staged_split(reinterpret_cast<uint16_t*>(ws_h + ws_arr), st1);
         return;
     }
     if (P1 && (pflags & PIECE_STORE_END)) {  // the first piece of a split sequence: the second piece's start state
@@ -1004,20 +1019,27 @@ __device__ __forceinline__ void scan_task(int H, int& ei, int& h, int& rb) {
     h = eh - ei * H;
 }
 
-// The scan's operands: later pieces store their transition P and local end state S_loc in blocked order (element
-// (a, b) at ((a / 4) * 128 + b) * 4 + a % 4, a = the row of the row-major array: k' for P[k'][k], v for S_loc[v][k]), so
-// a lane's B values P[32 kq + 4 s4 .. + 3][col] are one 16-byte load each (eight per tile and step) and its L values
-// L[16 rb + 4 kq .. + 3][col] one more, with the 16 lanes of a row group reading 256 contiguous bytes.  The scan runs
-// 4 waves per workgroup, wave w on the two 16-column tiles 32 w + 16 ct + j: one register set of operands is 72 VGPRs;
-// three sets leave two workgroups per CU, which a scan of one or two steps over many sequences needs more than a
-// shorter step.
+// The scan's operands: a later piece stores its local end state S_loc in blocked order (element (a, b) at
+// ((a / 4) * 128 + b) * 4 + a % 4, a = v) and its transition P[k'][k] as the bf16 pair hi = RNE(x), lo = RNE(x - hi)
+// in groups of 8 rows (copy_staged_split).  The product X P runs on bf16 16x16x32 MFMAs as X_hi P_hi + X_hi P_lo +
+// X_lo P_hi: each pair carries 16 bits of mantissa and the dropped X_lo P_lo term is below 2^-16 of each product, at
+// a fifth of the MFMA cycles of fp32 16x16x4 MFMAs (which bound the step before).  4 waves per workgroup, wave w on
+// the two 16-column tiles 32 w + 16 ct + j; MFMA t covers k' = 32 t + 8 kq .. + 7 (kq = lane / 16, j = lane % 16),
+// so a lane's B values per MFMA are one 16-byte load of hi and one of lo, with the 16 lanes of a row group reading
+// 256 contiguous bytes, and its L values (rows 16 rb + 4 kq .. + 3 of S_loc) one more 16-byte load.  The running
+// state block X sits in LDS as the bf16 pair (16 hi rows, then 16 lo rows, SCAN_XS bf16 per row: the 16-byte A reads
+// of the 16 rows fall on distinct banks).  One register set of operands is 72 VGPRs; three sets leave two
+// workgroups per CU, which a scan of one or two steps over many sequences needs more than a shorter step.
 constexpr int SCAN_THREADS = 256;
+constexpr int SCAN_XS = 136;
+constexpr int SCAN_XBUF = 2 * SC_ROWS * SCAN_XS;  // bf16 of one staged block
+constexpr int SCAN_SMEM = 2 * SCAN_XBUF * 2;      // two blocks (the scan alternates between them)
 struct ScanOps {
-    f32x4 b[2][8];  // b[ct][s4] = P[32 kq + 4 s4 .. + 3][32 w + 16 ct + j]
+    u32x4 b[2][8];  // b[ct][2 t + {0: hi, 1: lo}] = P[32 t + 8 kq .. + 7][32 w + 16 ct + j]
     f32x4 l[2];     // l[ct] = L[16 rb + 4 kq .. + 3][32 w + 16 ct + j]
 };
-// Buffer loads: the lane part of the address is one VGPR, the 2 KiB steps between a lane's eight operand rows are
-// scalar offsets (a global load's immediate offset does not reach them, and 64-bit addresses per load cost VGPRs).
+// Buffer loads: the lane part of the address is one VGPR, the steps between a lane's operand groups are scalar
+// offsets (a global load's immediate offset does not reach them, and 64-bit addresses per load cost VGPRs).
 __device__ __forceinline__ void fetch_scan(const float* PB, const float* LB, int rb, ScanOps& o) {
     const int j = threadIdx.x & 15, kq = (threadIdx.x & 63) >> 4, w = threadIdx.x >> 6;
     const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(PB), (short)0, D * D * 4, 0x00020000);
@@ -1026,24 +1048,30 @@ __device__ __forceinline__ void fetch_scan(const float* PB, const float* LB, int
     for (int ct = 0; ct < 2; ++ct) {
         const int col = 32 * w + 16 * ct + j;
 #pragma unroll
-        for (int s4 = 0; s4 < 8; ++s4)
-            o.b[ct][s4] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rp, (8 * kq * D + col) * 16,
-                                                                                          s4 * D * 16, 0));
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int hl = 0; hl < 2; ++hl)
+                o.b[ct][2 * t + hl] = __builtin_bit_cast(
+                    u32x4, __builtin_amdgcn_raw_buffer_load_b128(rp, (kq * D + col) * 16, t * 4 * D * 16 + hl * D * D * 2, 0));
         o.l[ct] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rl, ((4 * rb + kq) * D + col) * 16, 0, 0));
     }
 }
-// acc[ct][e] = out[4 kq + e][32 w + 16 ct + j]; sX staged and synced
-__device__ __forceinline__ void compose_scan(const float* sX, const ScanOps& o, f32x4 (&acc)[2]) {
+// acc[ct][e] = out[4 kq + e][32 w + 16 ct + j]; sX (the bf16 pair block) staged and synced
+__device__ __forceinline__ void compose_scan(const uint16_t* sX, const ScanOps& o, f32x4 (&acc)[2]) {
     const int j = threadIdx.x & 15, kq = (threadIdx.x & 63) >> 4;
     acc[0] = o.l[0];
     acc[1] = o.l[1];
 #pragma unroll
-    for (int s4 = 0; s4 < 8; ++s4) {
-        const f32x4 a = *reinterpret_cast<const f32x4*>(sX + j * SC_XS + 32 * kq + 4 * s4);
+    for (int t = 0; t < 4; ++t) {
+        const bf16x8 ah = *reinterpret_cast<const bf16x8*>(sX + j * SCAN_XS + 32 * t + 8 * kq);
+        const bf16x8 al = *reinterpret_cast<const bf16x8*>(sX + (SC_ROWS + j) * SCAN_XS + 32 * t + 8 * kq);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], o.b[0][s4][e], acc[0], 0, 0, 0);
-            acc[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], o.b[1][s4][e], acc[1], 0, 0, 0);
+        for (int ct = 0; ct < 2; ++ct) {
+            const bf16x8 bh = __builtin_bit_cast(bf16x8, o.b[ct][2 * t]);
+            const bf16x8 bl = __builtin_bit_cast(bf16x8, o.b[ct][2 * t + 1]);
+            acc[ct] = mfma32bf(al, bh, acc[ct]);
+            acc[ct] = mfma32bf(ah, bl, acc[ct]);
+            acc[ct] = mfma32bf(ah, bh, acc[ct]);
         }
     }
 }
@@ -1058,7 +1086,7 @@ __device__ __forceinline__ void compose_scan(const float* sX, const ScanOps& o, 
 // used it, behind that step's state stores, so that a wait for a store never waits for a prefetch).
 __global__ void __launch_bounds__(SCAN_THREADS) scan_kernel(PfParams p, const int32_t* __restrict__ tab) {
     extern __shared__ __align__(16) unsigned char lds[];
-    float* sX = reinterpret_cast<float*>(lds);
+    uint16_t* sX = reinterpret_cast<uint16_t*>(lds);
     const int H = p.H;
     int si, h, rb;
     scan_task(H, si, h, rb);
@@ -1086,8 +1114,8 @@ __global__ void __launch_bounds__(SCAN_THREADS) scan_kernel(PfParams p, const in
     auto step = [&](int pc, ScanOps& o) {
         lds_barrier();  // X_pc is complete in its buffer
         f32x4 acc[2];
-        compose_scan(sX + ((pc - 1) & 1) * SC_BUF, o, acc);
-        float* sN = sX + (pc & 1) * SC_BUF;
+        compose_scan(sX + ((pc - 1) & 1) * SCAN_XBUF, o, acc);
+        uint16_t* sN = sX + (pc & 1) * SCAN_XBUF;
         const float* dst = (pc + 1 < np) ? p.ws + 2 * ws_arr + ((int64_t)(slot0 + pc + 1) * H + h) * D * D
                                          : (pc + 1 == np ? fin : nullptr);
         const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
@@ -1097,7 +1125,9 @@ __global__ void __launch_bounds__(SCAN_THREADS) scan_kernel(PfParams p, const in
 #pragma unroll
             for (int ee = 0; ee < 4; ++ee) {
                 const int rr = 4 * kq + ee, col = 32 * w + 16 * ct + j;
-                sN[rr * SC_XS + col] = acc[ct][ee];
+                const uint32_t hb = f2bf(acc[ct][ee]);
+                sN[rr * SCAN_XS + col] = (uint16_t)hb;
+                sN[(SC_ROWS + rr) * SCAN_XS + col] = (uint16_t)f2bf(acc[ct][ee] - bf2f(hb));
                 __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[ct][ee]), rs, (int)(blk + rr * D + col) * 4, 0,
                                                       0);
             }
@@ -1120,8 +1150,12 @@ __global__ void __launch_bounds__(SCAN_THREADS) scan_kernel(PfParams p, const in
     asm volatile("" ::: "memory");
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
-        const int i = threadIdx.x + SCAN_THREADS * q;
-        *reinterpret_cast<f32x4*>(sX + (i >> 5) * SC_XS + 4 * (i & 31)) = x1[q];
+        const int i = threadIdx.x + SCAN_THREADS * q, rr = i >> 5, c = 4 * (i & 31);
+        uint32_t h0, l0, h1, l1;
+        split_bf16x2(x1[q][0], x1[q][1], h0, l0);
+        split_bf16x2(x1[q][2], x1[q][3], h1, l1);
+        *reinterpret_cast<u32x2*>(sX + rr * SCAN_XS + c) = u32x2{h0, h1};
+        *reinterpret_cast<u32x2*>(sX + (SC_ROWS + rr) * SCAN_XS + c) = u32x2{l0, l1};
     }
     for (int pc = 1; pc < np; pc += 3) {
         step(pc, oa);
@@ -1285,23 +1319,24 @@ hipError_t launch_chunk(const PfParams& p, int list_off, int entries, hipStream_
     return hipGetLastError();
 }
 template <typename K>
-hipError_t launch_composer(K kernel, const PfParams& p, int entries, int threads, hipStream_t s, bool& attr_set) {
+hipError_t launch_composer(K kernel, const PfParams& p, int entries, int threads, int smem, hipStream_t s,
+                           bool& attr_set) {
     if (!attr_set) {  // idempotent; a race only repeats the call
         const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, SC_SMEM);
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, smem);
         if (e != hipSuccess) return e;
         attr_set = true;
     }
-    hipLaunchKernelGGL(kernel, dim3(entries * p.H * (D / SC_ROWS)), dim3(threads), SC_SMEM, s, p, p.tab);
+    hipLaunchKernelGGL(kernel, dim3(entries * p.H * (D / SC_ROWS)), dim3(threads), smem, s, p, p.tab);
     return hipGetLastError();
 }
 hipError_t launch_scan(const PfParams& p, int entries, hipStream_t s) {
     static bool attr_set = false;
-    return launch_composer(scan_kernel, p, entries, SCAN_THREADS, s, attr_set);
+    return launch_composer(scan_kernel, p, entries, SCAN_THREADS, SCAN_SMEM, s, attr_set);
 }
 hipError_t launch_ck_compose(const PfParams& p, int entries, hipStream_t s) {
     static bool attr_set = false;
-    return launch_composer(ck_compose_kernel, p, entries, SC_THREADS, s, attr_set);
+    return launch_composer(ck_compose_kernel, p, entries, SC_THREADS, SC_SMEM, s, attr_set);
 }
 hipError_t launch_fixup(const PfParams& p, int entries, hipStream_t s) {
     hipLaunchKernelGGL(fixup_kernel, dim3(entries * p.H), dim3(FX_THREADS), FX_SMEM, s, p, p.tab);

@@ -388,6 +388,36 @@ def test_split_matches_whole_walk():
     assert rel_frob(f32(f2), f32(f1)) <= STATE_TOL
 
 
+@pytest.mark.parametrize("gscale", [1.0, 0.01])
+def test_split_long_scan_matches_whole_walk(gscale):
+    """A chain of many pieces: the scan composes the final state through every piece's transition (bf16 hi/lo pair
+    products), so its rounding adds up over the pieces.  With the config gates (gscale 1) a piece's transition
+    underflows to zero within a chunk or two; gscale 0.01 (log-decay ~ -0.007 per token and channel) keeps every
+    transition and every start state live, which exercises the scan and the output fixup in full.  Outputs and final
+    states against the unsplit walk of the same call."""
+    kda = _kda()
+    H, lens = 2, [32768]
+    g = gen(72)
+    q, k, v, gg, beta = config_inputs(sum(lens), H, g)
+    q, k, v, gg, beta = (x[None].to(DEV) for x in (q, k, v, gg * gscale, beta))
+    h0 = (torch.randn(len(lens), H, D, D, generator=g) * 0.02).to(DEV)
+    cu = torch.tensor(_cu(lens))
+    whole = kda.plan(cu, H, device=DEV, num_cus=1)
+    split = kda.plan(cu, H, device=DEV, num_cus=256)
+    assert whole.split[0] == 0 and split.split[0] >= 32, f"expected a long chain of pieces, got {split.split}"
+    o1, f1 = kda.chunk_kda(q, k, v, gg, beta, initial_state=h0, meta=whole)
+    o2, f2 = kda.chunk_kda(q, k, v, gg, beta, initial_state=h0, meta=split)
+    torch.cuda.synchronize()
+    err = rel_frob(f32(f2), f32(f1))
+    a, b = f32(o2).astype(np.float64), f32(o1).astype(np.float64)
+    rms = math.sqrt(float((b * b).mean()))
+    ex = float(np.max(np.abs(a - b) - 2 * bf16_half_ulp(b))) / rms
+    _say(f"long scan gscale={gscale} pieces={split.split} final-state rel frob {err:.3e} output excess {ex:.3e} "
+         f"relL2 {rel_frob(a, b):.3e}")
+    assert err <= STATE_TOL
+    assert ex <= OUT_TOL, f"split vs whole output excess {ex:.3e} beyond one bf16 ulp"
+
+
 @pytest.mark.parametrize("ckdt", [torch.float32, torch.bfloat16])
 def test_split_pool_every_n_checkpoints(oracle, ckdt):
     """Split sequence with the B200 every-n rows into an explicit row table (configuration 2's form) on a paged pool:
