@@ -48,16 +48,24 @@ struct DecParams {
 __device__ __forceinline__ bool slot_ok(int64_t r, int lo, int64_t n) { return r >= lo && r < n; }
 
 // SINGLE: one token per sequence (plain decode), S = 1 known at compile time.
+// PRE (several tokens, launches below the streaming size): the state-independent per-token operands are formed for
+// every token before the walk, which shortens each token's step (the latency of a small launch is the tokens' steps
+// in series); launches that stream more state than the MALL holds are bound by HBM, and there the extra phase and
+// the higher occupancy its smaller register set allows measured 1-3 % slower, so they form them per token.
 template <bool SPEC, bool SINGLE, bool NT>
 __global__ void __launch_bounds__(DC_THREADS) decode_kernel(DecParams p) {
+    constexpr bool PRE = !SINGLE && !NT;
     // dynamic LDS: conv weights [4][384] fp32 | conv + SiLU outputs [S][384] fp32 | bf16-rounded outputs [S][128] fp32
-    // | per-half-wave sums of squares [S][16] fp32 | window [3 + S][384] bf16
+    // | per-half-wave sums of squares [S][16] fp32 | gate factors exp(g) [S][128] fp32 | (k.q, beta) [S][2] fp32 |
+    // window [3 + S][384] bf16
     extern __shared__ __align__(16) float dsm[];
     float* sCw = dsm;
     float* sX = sCw + 4 * DC_CH;
     float* sO = sX + p.S * DC_CH;
     float* sRed = sO + p.S * D;
-    uint16_t* sWin = reinterpret_cast<uint16_t*>(sRed + p.S * 16);
+    float* sDd = sRed + p.S * 16;
+    float* sKB = sDd + p.S * D;
+    uint16_t* sWin = reinterpret_cast<uint16_t*>(sKB + 2 * p.S);
 
     // (sequence, head) of this workgroup, kept in SGPRs: buffer descriptors built from them must be wave-uniform
     // values the compiler can see as such, or it wraps every buffer access in a waterfall loop
@@ -117,7 +125,18 @@ __global__ void __launch_bounds__(DC_THREADS) decode_kernel(DecParams p) {
         return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(
                                              row_rsrc(p.gate + ((int64_t)n * S + t) * p.gate_rs + h * D, D * 2), 8 * wk.c, 0, 0));
     };
-    u32x2 g_next = load_gate(0);
+    u32x2 g_next = PRE ? u32x2{0u, 0u} : load_gate(0);
+    // PRE: the gate words of the tokens this wave forms before the walk (t = w, w + 8; clamped), channels 2 l, 2 l + 1
+    const int l64 = tid & 63;
+    uint32_t gw2[2] = {0u, 0u};
+    f32x2 db2 = {0.f, 0.f};
+    if (PRE) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+            gw2[j] = *reinterpret_cast<const uint32_t*>(p.gate + ((int64_t)n * S + min(wk.w + 8 * j, S - 1)) * p.gate_rs +
+                                                        h * D + 2 * l64);
+        db2 = *reinterpret_cast<const f32x2*>(p.dt_bias + h * D + 2 * l64);
+    }
     // out_gate of the outputs this thread finishes after the walk: element i = tid + 512 k (token i / 128, row i % 128)
     constexpr int OG_PER = SINGLE ? 1 : (DC_MAX_S * D) / DC_THREADS;
     uint32_t ogv[OG_PER];
@@ -166,26 +185,58 @@ __global__ void __launch_bounds__(DC_THREADS) decode_kernel(DecParams p) {
         }
     }
     lds_barrier();  // sX complete
+    if (PRE) {
+        // the per-token operands that do not depend on the state, formed before the walk (wave w takes tokens w and
+        // w + 8): q and k normalized in place in sX, exp(g) of the 128 channels, k . q and sigmoid(beta)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int t = wk.w + 8 * j;
+            if (t < S) {  // wave-uniform
+                float* xq = sX + t * DC_CH;
+                f32x2 qx = *reinterpret_cast<const f32x2*>(xq + 2 * l64);
+                f32x2 kx = *reinterpret_cast<const f32x2*>(xq + D + 2 * l64);
+                const float rq = __frsqrt_rn(sum64(qx.x * qx.x + qx.y * qx.y) + 1e-6f);
+                const float rk = __frsqrt_rn(sum64(kx.x * kx.x + kx.y * kx.y) + 1e-6f);
+                qx *= rq;
+                kx *= rk;
+                *reinterpret_cast<f32x2*>(xq + 2 * l64) = qx;
+                *reinterpret_cast<f32x2*>(xq + D + 2 * l64) = kx;
+                const float kq = sum64(qx.x * kx.x + qx.y * kx.y);
+                const f32x2 dd = {__expf(p.lb * sigmoidf_(A * bf2f(gw2[j] & 0xffffu) + A * db2.x)),
+                                  __expf(p.lb * sigmoidf_(A * bf2f(gw2[j] >> 16) + A * db2.y))};
+                *reinterpret_cast<f32x2*>(sDd + t * D + 2 * l64) = dd;
+                if (l64 == 0) {
+                    sKB[2 * t] = kq;
+                    sKB[2 * t + 1] = sigmoidf_(bf2f(__builtin_amdgcn_readlane(beta_l, t) & 0xffffu));
+                }
+            }
+        }
+        lds_barrier();
+    }
     if (!SINGLE) state_ready(st);
 
     for (int t = 0; t < S; ++t) {
-        const u32x2 gcur = g_next;
-        g_next = load_gate(min(t + 1, S - 1));  // unconditional, issued before this token's state stores
         const float* xq = sX + t * DC_CH;
         const f32x4 q4 = *reinterpret_cast<const f32x4*>(xq + c0);
         const f32x4 k4 = *reinterpret_cast<const f32x4*>(xq + D + c0);
         float qq[4] = {q4.x, q4.y, q4.z, q4.w};
         float kk[4] = {k4.x, k4.y, k4.z, k4.w};
-        float dd[4];
-        {
+        float dd[4], o;
+        if (!PRE) {
+            const u32x2 gcur = g_next;
+            g_next = load_gate(min(t + 1, S - 1));  // unconditional, issued before this token's state stores
             const float rg[4] = {bf2f(gcur.x & 0xffffu), bf2f(gcur.x >> 16), bf2f(gcur.y & 0xffffu), bf2f(gcur.y >> 16)};
 #pragma unroll
             for (int c = 0; c < 4; ++c) dd[c] = __expf(p.lb * sigmoidf_(A * rg[c] + dbA[c]));
+            rsqrt_norm4(kk);  // x * rsqrt(sum x^2 + 1e-6)  (kda/mi350x/reference.py:159-160)
+            rsqrt_norm4(qq);
+            const float bt = sigmoidf_(bf2f(__builtin_amdgcn_readlane(beta_l, t) & 0xffffu));
+            o = walk_token(st, kk, qq, dd, xq[2 * D + v_src_row(wk)], bt, p.scale, wk.c);
+        } else {
+            const f32x4 d4 = *reinterpret_cast<const f32x4*>(sDd + t * D + c0);
+            dd[0] = d4.x; dd[1] = d4.y; dd[2] = d4.z; dd[3] = d4.w;
+            o = walk_token_kq(st, kk, qq, dd, xq[2 * D + v_src_row(wk)], sKB[2 * t + 1], sKB[2 * t], p.scale, wk.c);
         }
-        rsqrt_norm4(kk);  // x * rsqrt(sum x^2 + 1e-6)  (kda/mi350x/reference.py:159-160)
-        rsqrt_norm4(qq);
-        const float bt = sigmoidf_(bf2f(__builtin_amdgcn_readlane(beta_l, t) & 0xffffu));
-        const float o = walk_token(st, kk, qq, dd, xq[2 * D + v_src_row(wk)], bt, p.scale, wk.c);
         // bf16(o) of the lane's row and the half wave's sum of squares (lanes c < 8 hold the half's 8 rows)
         const float ob = bf2f(f2bf(o));
         const float ss = sum32(wk.c < 8 ? ob * ob : 0.f);
@@ -276,7 +327,7 @@ extern "C" int kda355_decode_launch(const KdaDecodeArgs* a, kda355_stream_t stre
     p.lb = a->lower_bound;
     p.scale = 0.08838834764831845f;  // 128^-1/2: the reference scales the normalized q
     const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    const size_t lds = ((size_t)(4 + a->S) * DC_CH + (size_t)a->S * (D + 16)) * sizeof(float) +
+    const size_t lds = ((size_t)(4 + a->S) * DC_CH + (size_t)a->S * (2 * D + 18)) * sizeof(float) +
                        (size_t)(3 + a->S) * DC_CH * sizeof(uint16_t);
     // streaming stores when the launch writes more state than the MALL holds (WK_STREAM_BYTES)
     const bool nt = (long long)a->B * (spec ? a->S : 1) * a->H * D * D * 4 > WK_STREAM_BYTES;

@@ -103,12 +103,13 @@ __device__ __forceinline__ int v_src_row(const Walker& wk) { return 16 * (wk.c &
 // row v_src_row() (each row's v is broadcast from it).  Every lane of a half wave computes its 8 rows' full sums; the
 // return value is o at row 16 c + 2 w + half (meaningful on lanes c < 8).  Rows are reduced in two groups of 4 to
 // keep few values live.
-__device__ __forceinline__ float walk_token(f32x4 (&st)[8], const float (&kk)[4], const float (&qq)[4],
-                                            const float (&dd)[4], float vsrc, float bt, float scale, int c) {
+// walk_token_kq: the same with k . q supplied by the caller (formed before the walk when the token's operands do not
+// depend on the state).
+__device__ __forceinline__ float walk_token_kq(f32x4 (&st)[8], const float (&kk)[4], const float (&qq)[4],
+                                               const float (&dd)[4], float vsrc, float bt, float kq, float scale, int c) {
     float vv[8];
     vv[0] = v_of_row<0>(vsrc); vv[1] = v_of_row<1>(vsrc); vv[2] = v_of_row<2>(vsrc); vv[3] = v_of_row<3>(vsrc);
     vv[4] = v_of_row<4>(vsrc); vv[5] = v_of_row<5>(vsrc); vv[6] = v_of_row<6>(vsrc); vv[7] = v_of_row<7>(vsrc);
-    const float kq = sum32(kk[0] * qq[0] + kk[1] * qq[1] + kk[2] * qq[2] + kk[3] * qq[3]);
     float osel = 0.f;
 #pragma unroll
     for (int g = 0; g < 2; ++g) {
@@ -132,6 +133,18 @@ __device__ __forceinline__ float walk_token(f32x4 (&st)[8], const float (&kk)[4]
         }
     }
     return osel;
+}
+__device__ __forceinline__ float walk_token(f32x4 (&st)[8], const float (&kk)[4], const float (&qq)[4],
+                                            const float (&dd)[4], float vsrc, float bt, float scale, int c) {
+    const float kq = sum32(kk[0] * qq[0] + kk[1] * qq[1] + kk[2] * qq[2] + kk[3] * qq[3]);
+    return walk_token_kq(st, kk, qq, dd, vsrc, bt, kq, scale, c);
+}
+
+// Sum over the 64 lanes of a wave, returned wave-uniform.
+__device__ __forceinline__ float sum64(float x) {
+    x = sum32(x);
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 0)) +
+           __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 32));
 }
 
 }  // namespace kda355

@@ -193,6 +193,12 @@ def test_spec_verify_s8(oracle):
     _run(oracle, B=6, S=8, H=2, seed=6, spec=True)
 
 
+def test_spec_verify_streaming_size(oracle):
+    """A launch that writes more state than the streaming threshold (8 x 8 x 96 states of 64 KiB = 403 MB > 384 MiB):
+    the kernel variant with streaming stores, which forms each token's operands inside the walk."""
+    _run(oracle, B=8, S=8, H=96, seed=12, spec=True, pages=False)
+
+
 def test_spec_verify_padding(oracle):
     """Padding write rows (skipped) and a sequence whose conv row idx[n, 0] is padding (dead: zero output)."""
     _run(oracle, B=6, S=4, H=2, seed=7, spec=True, pad=[(0, 3), (2, 1), (4, 0)])
