@@ -1040,10 +1040,12 @@ struct ScanOps {
 };
 // Buffer loads: the lane part of the address is one VGPR, the steps between a lane's operand groups are scalar
 // offsets (a global load's immediate offset does not reach them, and 64-bit addresses per load cost VGPRs).
-__device__ __forceinline__ void fetch_scan(const float* PB, const float* LB, int rb, ScanOps& o) {
+// live = false loads nothing (descriptors of no records: the loads return zeros and move no data).
+__device__ __forceinline__ void fetch_scan(const float* PB, const float* LB, int rb, bool live, ScanOps& o) {
     const int j = threadIdx.x & 15, kq = (threadIdx.x & 63) >> 4, w = threadIdx.x >> 6;
-    const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(PB), (short)0, D * D * 4, 0x00020000);
-    const __amdgpu_buffer_rsrc_t rl = __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(LB), (short)0, D * D * 4, 0x00020000);
+    const int nrec = __builtin_amdgcn_readfirstlane(live ? D * D * 4 : 0);
+    const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(PB), (short)0, nrec, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rl = __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(LB), (short)0, nrec, 0x00020000);
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct) {
         const int col = 32 * w + 16 * ct + j;
@@ -1084,6 +1086,9 @@ __device__ __forceinline__ void compose_scan(const uint16_t* sX, const ScanOps& 
 // the states are not waited for.  A freshly written transition takes about two compositions to arrive, so each
 // piece's operands are fetched two steps ahead, into one of three register sets (refilled right after the step that
 // used it, behind that step's state stores, so that a wait for a store never waits for a prefetch).
+// LEAN (every split sequence in at most 3 pieces, config 1's case): one register set, no fetch ahead; ~100 VGPRs fit
+// four workgroups per CU, so a launch of many short scans runs in one round.
+template <bool LEAN>
 __global__ void __launch_bounds__(SCAN_THREADS) scan_kernel(PfParams p, const int32_t* __restrict__ tab) {
     extern __shared__ __align__(16) unsigned char lds[];
     uint16_t* sX = reinterpret_cast<uint16_t*>(lds);
@@ -1104,13 +1109,14 @@ __global__ void __launch_bounds__(SCAN_THREADS) scan_kernel(PfParams p, const in
     }
     // piece pc's operands: P at array 1, S_loc at array 0 of the workspace (both in blocked order)
     auto fetch = [&](int pc, ScanOps& o) {
-        const int64_t so = ((int64_t)(slot0 + pc) * H + h) * D * D;
-        fetch_scan(p.ws + ws_arr + so, p.ws + so, rb, o);
+        const int64_t so = ((int64_t)(slot0 + min(pc, np - 1)) * H + h) * D * D;
+        fetch_scan(p.ws + ws_arr + so, p.ws + so, rb, pc < np, o);
     };
     // step pc: X_{pc+1} = P_pc X_pc + S_loc(pc) from `o`, which then receives piece pc + 3's operands.  Every step
     // issues the same memory operations, and the loop runs whole groups of three steps: fetches past the last piece
-    // repeat it, and a step past the last one (or a missing final-state destination) stores through a descriptor
-    // of no records.  With no operation under a branch, the wait for `o` counts only the operations issued after it.
+    // and the stores of a step past the last one (or of a missing final-state destination) go through descriptors
+    // of no records, so they move no data (a sequence in two pieces, config 1's case, loads one operand set, not
+    // three).  With no operation under a branch, the wait for `o` counts only the operations issued after it.
     auto step = [&](int pc, ScanOps& o) {
         lds_barrier();  // X_pc is complete in its buffer
         f32x4 acc[2];
@@ -1131,7 +1137,7 @@ __global__ void __launch_bounds__(SCAN_THREADS) scan_kernel(PfParams p, const in
                 __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[ct][ee]), rs, (int)(blk + rr * D + col) * 4, 0,
                                                       0);
             }
-        fetch(min(pc + 3, np - 1), o);
+        if constexpr (!LEAN) fetch(pc + 3, o);
     };
     // X_1's 16 rows (one 16-byte piece per thread) are loaded first, then the first three pieces' operands; the
     // LDS write of X_1 then waits for X_1 alone (the compiler barriers keep the loads in this order)
@@ -1143,10 +1149,30 @@ __global__ void __launch_bounds__(SCAN_THREADS) scan_kernel(PfParams p, const in
         x1[q] = *reinterpret_cast<const f32x4*>(X1 + (i >> 5) * D + 4 * (i & 31));
     }
     asm volatile("" ::: "memory");
+    if constexpr (LEAN) {
+        ScanOps oa;
+        fetch(1, oa);
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const int i = threadIdx.x + SCAN_THREADS * q, rr = i >> 5, c = 4 * (i & 31);
+            uint32_t h0, l0, h1, l1;
+            split_bf16x2(x1[q][0], x1[q][1], h0, l0);
+            split_bf16x2(x1[q][2], x1[q][3], h1, l1);
+            *reinterpret_cast<u32x2*>(sX + rr * SCAN_XS + c) = u32x2{h0, h1};
+            *reinterpret_cast<u32x2*>(sX + (SC_ROWS + rr) * SCAN_XS + c) = u32x2{l0, l1};
+        }
+        step(1, oa);
+        if (np == 3) {
+            fetch(2, oa);
+            step(2, oa);
+        }
+        return;
+    }
     ScanOps oa, ob, oc;
     fetch(1, oa);
-    fetch(min(2, np - 1), ob);
-    fetch(min(3, np - 1), oc);
+    fetch(2, ob);
+    fetch(3, oc);
     asm volatile("" ::: "memory");
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
@@ -1330,9 +1356,10 @@ hipError_t launch_composer(K kernel, const PfParams& p, int entries, int threads
     hipLaunchKernelGGL(kernel, dim3(entries * p.H * (D / SC_ROWS)), dim3(threads), smem, s, p, p.tab);
     return hipGetLastError();
 }
-hipError_t launch_scan(const PfParams& p, int entries, hipStream_t s) {
-    static bool attr_set = false;
-    return launch_composer(scan_kernel, p, entries, SCAN_THREADS, SCAN_SMEM, s, attr_set);
+hipError_t launch_scan(const PfParams& p, int entries, bool lean, hipStream_t s) {
+    static bool attr_set[2] = {false, false};
+    return lean ? launch_composer(scan_kernel<true>, p, entries, SCAN_THREADS, SCAN_SMEM, s, attr_set[1])
+                : launch_composer(scan_kernel<false>, p, entries, SCAN_THREADS, SCAN_SMEM, s, attr_set[0]);
 }
 hipError_t launch_ck_compose(const PfParams& p, int entries, hipStream_t s) {
     static bool attr_set = false;
@@ -1706,7 +1733,9 @@ extern "C" int kda355_prefill_launch(const KdaPrefillArgs* a, kda355_stream_t st
         // transitions), then the start / final states of the split sequences, the later pieces' outputs and their
         // checkpoints
         e = rg ? launch_chunk<true, true>(p, off_final, pl->num_chains, s) : launch_chunk<false, true>(p, off_final, pl->num_chains, s);
-        if (e == hipSuccess) e = launch_scan(p, pl->num_split, s);
+        // every split sequence has >= 2 pieces, so the most-cut one has at most num_pieces - 2 (num_split - 1)
+        const bool lean = pl->num_pieces - 2 * (pl->num_split - 1) <= 3;
+        if (e == hipSuccess) e = launch_scan(p, pl->num_split, lean, s);
         if (e == hipSuccess && pl->num_fix_tasks > 0) e = launch_fixup(p, pl->num_fix_tasks, s);
         if (e == hipSuccess && pl->num_ck_tasks > 0) e = launch_ck_compose(p, pl->num_ck_tasks, s);
     } else {

@@ -418,6 +418,32 @@ def test_split_long_scan_matches_whole_walk(gscale):
     assert ex <= OUT_TOL, f"split vs whole output excess {ex:.3e} beyond one bf16 ulp"
 
 
+def test_split_three_pieces_matches_whole_walk():
+    """A launch whose split sequences have at most 3 pieces takes the lean scan (one operand set, four workgroups per
+    CU): the reference's p96_loaded8k_0 shape (H = 96, one 8192-token sequence, planned as 52 + 52 + 24 chunks) with
+    slow decay, against the unsplit walk of the same call."""
+    kda = _kda()
+    H, lens = 96, [8192]
+    g = gen(73)
+    q, k, v, gg, beta = config_inputs(sum(lens), H, g)
+    q, k, v, gg, beta = (x[None].to(DEV) for x in (q, k, v, gg * 0.01, beta))
+    h0 = (torch.randn(len(lens), H, D, D, generator=g) * 0.02).to(DEV)
+    cu = torch.tensor(_cu(lens))
+    whole = kda.plan(cu, H, device=DEV, num_cus=1)
+    split = kda.plan(cu, H, device=DEV, num_cus=256)
+    assert whole.split[0] == 0 and split.split == (3, 1), f"expected 3 pieces, got {split.split}"
+    o1, f1 = kda.chunk_kda(q, k, v, gg, beta, initial_state=h0, meta=whole)
+    o2, f2 = kda.chunk_kda(q, k, v, gg, beta, initial_state=h0, meta=split)
+    torch.cuda.synchronize()
+    err = rel_frob(f32(f2), f32(f1))
+    a, b = f32(o2).astype(np.float64), f32(o1).astype(np.float64)
+    rms = math.sqrt(float((b * b).mean()))
+    ex = float(np.max(np.abs(a - b) - 2 * bf16_half_ulp(b))) / rms
+    _say(f"three pieces H={H} final-state rel frob {err:.3e} output excess {ex:.3e}")
+    assert err <= STATE_TOL
+    assert ex <= OUT_TOL
+
+
 @pytest.mark.parametrize("ckdt", [torch.float32, torch.bfloat16])
 def test_split_pool_every_n_checkpoints(oracle, ckdt):
     """Split sequence with the B200 every-n rows into an explicit row table (configuration 2's form) on a paged pool:
