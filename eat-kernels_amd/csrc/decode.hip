@@ -24,6 +24,7 @@ namespace {
 constexpr int DC_THREADS = WK_THREADS;
 constexpr int DC_MAX_S = 16;
 constexpr int DC_CH = 3 * D;  // conv channels of one head: q | k | v
+constexpr int64_t DC_SLICE_CUS = 256;  // a launch splits each state while the slices still fit one per CU (MI355X)
 
 struct DecParams {
     const uint16_t* x;        // mixed_qkv [T, 3 * dim] bf16, row stride x_rs
@@ -52,9 +53,16 @@ __device__ __forceinline__ bool slot_ok(int64_t r, int lo, int64_t n) { return r
 // every token before the walk, which shortens each token's step (the latency of a small launch is the tokens' steps
 // in series); launches that stream more state than the MALL holds are bound by HBM, and there the extra phase and
 // the higher occupancy its smaller register set allows measured 1-3 % slower, so they form them per token.
-template <bool SPEC, bool SINGLE, bool NT>
+//
+// NP < 8 (small launches): the state rows are split over 8 / NP workgroups per (sequence, head), slice vs holding
+// rows 16 NP vs .. 16 NP (vs + 1) - 1 (NP rows per lane), so a token's step is 8 / NP times shorter and 8 / NP times
+// more CUs walk.  Every slice forms the conv and the q / k / gate operands of all 128 channels (the walk needs every
+// key column); slice 0 commits the conv cache.  Each slice writes bf16(o) of its rows to `out`, and norm_kernel then
+// applies the gated RMSNorm over the 128 rows of every (token, head).
+template <bool SPEC, bool SINGLE, bool NT, int NP>
 __global__ void __launch_bounds__(DC_THREADS) decode_kernel(DecParams p) {
     constexpr bool PRE = !SINGLE && !NT;
+    constexpr int VS = 8 / NP;  // slices per (sequence, head)
     // dynamic LDS: conv weights [4][384] fp32 | conv + SiLU outputs [S][384] fp32 | bf16-rounded outputs [S][128] fp32
     // | per-half-wave sums of squares [S][16] fp32 | gate factors exp(g) [S][128] fp32 | (k.q, beta) [S][2] fp32 |
     // window [3 + S][384] bf16
@@ -70,8 +78,11 @@ __global__ void __launch_bounds__(DC_THREADS) decode_kernel(DecParams p) {
     // (sequence, head) of this workgroup, kept in SGPRs: buffer descriptors built from them must be wave-uniform
     // values the compiler can see as such, or it wraps every buffer access in a waterfall loop
     const int task = xcd_task(blockIdx.x, gridDim.x);
-    const int n = __builtin_amdgcn_readfirstlane(task / p.H);
-    const int h = __builtin_amdgcn_readfirstlane(task - n * p.H);
+    const int nh = __builtin_amdgcn_readfirstlane(task / VS);
+    const int vs = __builtin_amdgcn_readfirstlane(task - nh * VS);
+    const int n = __builtin_amdgcn_readfirstlane(nh / p.H);
+    const int h = __builtin_amdgcn_readfirstlane(nh - n * p.H);
+    const int row0 = 16 * NP * vs;  // the slice's first state row
     const int tid = threadIdx.x;
     const int S = SINGLE ? 1 : p.S, H = p.H;
     const int dim = H * D;
@@ -89,6 +100,7 @@ __global__ void __launch_bounds__(DC_THREADS) decode_kernel(DecParams p) {
     }
     const bool live = slot_ok(rd, 1, p.ssm_slots) && slot_ok(cs, 1, p.conv_slots);
     if (!live) {
+        if (vs != 0) return;
         for (int t = 0; t < S; ++t) {
             uint32_t* o32 = reinterpret_cast<uint32_t*>(p.out + ((int64_t)n * S + t) * p.out_rs + h * D);
             if (tid < D / 2) o32[tid] = 0u;
@@ -143,15 +155,17 @@ __global__ void __launch_bounds__(DC_THREADS) decode_kernel(DecParams p) {
 #pragma unroll
     for (int k = 0; k < OG_PER; ++k) {
         const int i = min(tid + k * DC_THREADS, S * D - 1);
-        ogv[k] = __builtin_amdgcn_raw_buffer_load_b16(row_rsrc(p.og + ((int64_t)n * S + (i >> 7)) * p.og_rs + h * D, D * 2),
-                                                      2 * (i & 127), 0, 0);
+        ogv[k] = NP < 8 ? 0u
+                        : __builtin_amdgcn_raw_buffer_load_b16(
+                              row_rsrc(p.og + ((int64_t)n * S + (i >> 7)) * p.og_rs + h * D, D * 2), 2 * (i & 127), 0, 0);
     }
     const float nw = p.nw[tid & (D - 1)];
     const float A = __expf(p.A_log[h]);
     const f32x4 db = *reinterpret_cast<const f32x4*>(p.dt_bias + h * D + c0);
     asm volatile("" ::: "memory");  // keep the loads above ahead of the state loads (completion is in issue order)
-    f32x4 st[8];
-    load_state(wk, p.ssm + rd * p.ssm_ss + (int64_t)h * D * D, st);
+    f32x4 st[NP];
+    const int64_t slice = (int64_t)h * D * D + (int64_t)row0 * D;  // the slice's first element in a pool row
+    load_state<NP>(wk, p.ssm + rd * p.ssm_ss + slice, st);
 
     // unconditional: threads past the end rewrite the last piece / quad with the same data
     *reinterpret_cast<u32x4*>(&sWin[min(tid, npieces - 1) * 8]) = wp0;
@@ -173,7 +187,7 @@ __global__ void __launch_bounds__(DC_THREADS) decode_kernel(DecParams p) {
         for (int tap = 0; tap < 4; ++tap) acc += bf2f(sWin[(t + tap) * DC_CH + c]) * sCw[tap * DC_CH + c];
         sX[i] = acc * sigmoidf_(acc);
     }
-    {
+    if (vs == 0) {
         // spec: taps [0, 2 + S) <- window[1 .. 3 + S);  plain: taps [0, 3) <- window[S .. S + 3)
         const int ntap = SPEC ? 2 + S : 3, first = SPEC ? 1 : S;
 #pragma unroll 1
@@ -214,6 +228,8 @@ __global__ void __launch_bounds__(DC_THREADS) decode_kernel(DecParams p) {
         lds_barrier();
     }
     if (!SINGLE) state_ready(st);
+    // v of the slice row this lane broadcasts (lanes with c % 8 >= NP repeat the last one)
+    const int vrow = row0 + 16 * min(wk.c & 7, NP - 1) + 2 * wk.w + wk.half;
 
     for (int t = 0; t < S; ++t) {
         const float* xq = sX + t * DC_CH;
@@ -231,24 +247,29 @@ __global__ void __launch_bounds__(DC_THREADS) decode_kernel(DecParams p) {
             rsqrt_norm4(kk);  // x * rsqrt(sum x^2 + 1e-6)  (kda/mi350x/reference.py:159-160)
             rsqrt_norm4(qq);
             const float bt = sigmoidf_(bf2f(__builtin_amdgcn_readlane(beta_l, t) & 0xffffu));
-            o = walk_token(st, kk, qq, dd, xq[2 * D + v_src_row(wk)], bt, p.scale, wk.c);
+            o = walk_token<NP>(st, kk, qq, dd, xq[2 * D + vrow], bt, p.scale, wk.c);
         } else {
             const f32x4 d4 = *reinterpret_cast<const f32x4*>(sDd + t * D + c0);
             dd[0] = d4.x; dd[1] = d4.y; dd[2] = d4.z; dd[3] = d4.w;
-            o = walk_token_kq(st, kk, qq, dd, xq[2 * D + v_src_row(wk)], sKB[2 * t + 1], sKB[2 * t], p.scale, wk.c);
+            o = walk_token_kq<NP>(st, kk, qq, dd, xq[2 * D + vrow], sKB[2 * t + 1], sKB[2 * t], p.scale, wk.c);
         }
-        // bf16(o) of the lane's row and the half wave's sum of squares (lanes c < 8 hold the half's 8 rows)
-        const float ob = bf2f(f2bf(o));
-        const float ss = sum32(wk.c < 8 ? ob * ob : 0.f);
-        if (wk.c < 8) sO[t * D + wk.row(wk.c)] = ob;
-        if (wk.c == 0) sRed[t * 16 + 2 * wk.w + wk.half] = ss;
+        if constexpr (NP == 8) {
+            // bf16(o) of the lane's row and the half wave's sum of squares (lanes c < 8 hold the half's 8 rows)
+            const float ob = bf2f(f2bf(o));
+            const float ss = sum32(wk.c < 8 ? ob * ob : 0.f);
+            if (wk.c < 8) sO[t * D + wk.row(wk.c)] = ob;
+            if (wk.c == 0) sRed[t * 16 + 2 * wk.w + wk.half] = ss;
+        } else {  // bf16(o) of the slice's rows straight to `out`; norm_kernel finishes them
+            if (wk.c < NP) p.out[((int64_t)n * S + t) * p.out_rs + h * D + row0 + wk.row(wk.c)] = (uint16_t)f2bf(o);
+        }
         if (SPEC) {
             const int64_t wr = __builtin_amdgcn_readlane(wr_l, t);
             const bool ok = slot_ok(wr, 1, p.ssm_slots);
-            store_state<NT>(wk, p.ssm + (ok ? wr : 0) * p.ssm_ss + (int64_t)h * D * D, st, ok);
+            store_state<NT, NP>(wk, p.ssm + (ok ? wr : 0) * p.ssm_ss + slice, st, ok);
         }
     }
-    if (!SPEC) store_state<NT>(wk, p.ssm + rd * p.ssm_ss + (int64_t)h * D * D, st);
+    if (!SPEC) store_state<NT, NP>(wk, p.ssm + rd * p.ssm_ss + slice, st);
+    if constexpr (NP < 8) return;
     lds_barrier();
     // ---- gated RMSNorm of every token's 128 outputs: y = bf16(o) rsqrt(mean(bf16(o)^2) + eps) nw sigmoid(og)
 #pragma unroll
@@ -265,6 +286,24 @@ __global__ void __launch_bounds__(DC_THREADS) decode_kernel(DecParams p) {
                                                   2 * (i & 127), 0, 0);
         }
     }
+}
+
+// The gated RMSNorm after a sliced decode: y = x rsqrt(mean(x^2) + eps) nw sigmoid(og) over the 128 values x = bf16(o)
+// of one (token, head) row of `out` (one wave per row, two values per lane), in place.  A dead sequence's rows are
+// zero and stay zero.
+constexpr int NM_THREADS = 256;
+__global__ void __launch_bounds__(NM_THREADS) norm_kernel(DecParams p, int rows) {
+    const int row = blockIdx.x * (NM_THREADS / 64) + (threadIdx.x >> 6);  // (token, head): token-major
+    if (row >= rows) return;  // wave-uniform
+    const int l = threadIdx.x & 63, t = row / p.H, h = row - t * p.H;
+    uint32_t* o = reinterpret_cast<uint32_t*>(p.out + (int64_t)t * p.out_rs + h * D) + l;
+    const uint32_t xo = *o;
+    const uint32_t og = *(reinterpret_cast<const uint32_t*>(p.og + (int64_t)t * p.og_rs + h * D) + l);
+    const f32x2 nw = *reinterpret_cast<const f32x2*>(p.nw + 2 * l);
+    const float x0 = bf2f(xo & 0xffffu), x1 = bf2f(xo >> 16);
+    const float rstd = __frsqrt_rn(sum64(x0 * x0 + x1 * x1) * (1.f / D) + p.eps);
+    *o = f2bf(x0 * rstd * nw.x * sigmoidf_(bf2f(og & 0xffffu))) |
+         (f2bf(x1 * rstd * nw.y * sigmoidf_(bf2f(og >> 16))) << 16);
 }
 
 bool aligned(const void* q, size_t a) { return (reinterpret_cast<uintptr_t>(q) % a) == 0; }
@@ -331,10 +370,23 @@ extern "C" int kda355_decode_launch(const KdaDecodeArgs* a, kda355_stream_t stre
                        (size_t)(3 + a->S) * DC_CH * sizeof(uint16_t);
     // streaming stores when the launch writes more state than the MALL holds (WK_STREAM_BYTES)
     const bool nt = (long long)a->B * (spec ? a->S : 1) * a->H * D * D * 4 > WK_STREAM_BYTES;
-    void (*kernel)(DecParams) = spec ? (nt ? decode_kernel<true, false, true> : decode_kernel<true, false, false>)
-                                : a->S == 1 ? (nt ? decode_kernel<false, true, true> : decode_kernel<false, true, false>)
-                                            : (nt ? decode_kernel<false, false, true> : decode_kernel<false, false, false>);
-    hipLaunchKernelGGL(kernel, dim3(a->B * a->H), dim3(DC_THREADS), lds, s, p);
+    // small launches split each state over 4 workgroups (32 rows each) while the slices fit one per CU, so that more
+    // CUs walk and each token's step is shorter; the gated RMSNorm then runs as a second kernel.  (Halves of 64 rows
+    // for launches of up to 128 pairs measured no faster than whole states: s8_h96_b1 27.5 against 27.1 us.)
+    const int64_t pairs = (int64_t)a->B * a->H;
+    const int np = (!nt && 4 * pairs <= DC_SLICE_CUS) ? 2 : 8;
+    void (*kernel)(DecParams) =
+        np == 2 ? (spec ? decode_kernel<true, false, false, 2>
+                        : a->S == 1 ? decode_kernel<false, true, false, 2> : decode_kernel<false, false, false, 2>)
+        : spec ? (nt ? decode_kernel<true, false, true, 8> : decode_kernel<true, false, false, 8>)
+        : a->S == 1 ? (nt ? decode_kernel<false, true, true, 8> : decode_kernel<false, true, false, 8>)
+                    : (nt ? decode_kernel<false, false, true, 8> : decode_kernel<false, false, false, 8>);
+    hipLaunchKernelGGL(kernel, dim3(a->B * a->H * (8 / np)), dim3(DC_THREADS), lds, s, p);
+    if (np < 8) {
+        const int rows = a->B * a->S * a->H;
+        hipLaunchKernelGGL(norm_kernel, dim3((rows + NM_THREADS / 64 - 1) / (NM_THREADS / 64)), dim3(NM_THREADS), 0, s, p,
+                           rows);
+    }
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         set_error("decode: launch failed: %s", hipGetErrorString(e));

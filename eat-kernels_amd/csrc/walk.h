@@ -42,18 +42,21 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t state_rsrc(const float* base) 
     return __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(base), (short)0, D * D * 4, 0x00020000);
 }
 
-__device__ __forceinline__ void load_state(const Walker& wk, const float* base, f32x4 (&st)[8]) {
+// NP < 8: the workgroup holds rows 0 .. 16 NP - 1 of the block at `base` (a slice of a state), NP rows per lane.
+template <int NP = 8>
+__device__ __forceinline__ void load_state(const Walker& wk, const float* base, f32x4 (&st)[NP]) {
     const __amdgpu_buffer_rsrc_t rs = state_rsrc(base);
 #pragma unroll
-    for (int p = 0; p < 8; ++p)
+    for (int p = 0; p < NP; ++p)
         st[p] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, wk.voff(), p * WK_ROW_STEP, WK_LOAD_AUX));
 }
 
 // Wait for the state loads here rather than at the state's first use inside a token loop: the compiler's wait
 // there would also run on every later iteration, where it drains that iteration's predecessor's state stores.
-__device__ __forceinline__ void state_ready(f32x4 (&st)[8]) {
+template <int NP = 8>
+__device__ __forceinline__ void state_ready(f32x4 (&st)[NP]) {
 #pragma unroll
-    for (int p = 0; p < 8; ++p) asm volatile("" : "+v"(st[p]));
+    for (int p = 0; p < NP; ++p) asm volatile("" : "+v"(st[p]));
 }
 
 // valid = false stores nothing: the descriptor then covers 0 bytes and the hardware drops out-of-range buffer
@@ -61,12 +64,12 @@ __device__ __forceinline__ void state_ready(f32x4 (&st)[8]) {
 // under a branch makes it wait for every older access on the path without it).  NT selects the streaming policy at
 // compile time: a run-time branch between the two policies costs the single-token decode 7 % (the stores can no
 // longer start while the last rows are still being updated).
-template <bool NT = false>
-__device__ __forceinline__ void store_state(const Walker& wk, float* base, const f32x4 (&st)[8], bool valid = true) {
+template <bool NT = false, int NP = 8>
+__device__ __forceinline__ void store_state(const Walker& wk, float* base, const f32x4 (&st)[NP], bool valid = true) {
     const __amdgpu_buffer_rsrc_t rs =
-        __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(base), (short)0, valid ? D * D * 4 : 0, 0x00020000);
+        __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(base), (short)0, valid ? 16 * NP * D * 4 : 0, 0x00020000);
 #pragma unroll
-    for (int p = 0; p < 8; ++p)
+    for (int p = 0; p < NP; ++p)
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, st[p]), rs, wk.voff(), p * WK_ROW_STEP,
                                                NT ? WK_STORE_AUX_NT : WK_STORE_AUX);
 }
@@ -98,46 +101,54 @@ __device__ __forceinline__ float v_of_row(float vsrc) {
 // Lane c's source row for v_of_row: 16 (c % 8) + 2 w + half.
 __device__ __forceinline__ int v_src_row(const Walker& wk) { return 16 * (wk.c & 7) + 2 * wk.w + wk.half; }
 
-// One token of the gated delta rule on this lane's 8 rows: S *= exp(g) along K; u = beta (v - S k); S += u k^T;
-// o = scale * (S_decayed q + u (k . q)) (= scale * S_new q).  dd = exp(g) of the lane's 4 key columns, vsrc = v at
-// row v_src_row() (each row's v is broadcast from it).  Every lane of a half wave computes its 8 rows' full sums; the
-// return value is o at row 16 c + 2 w + half (meaningful on lanes c < 8).  Rows are reduced in two groups of 4 to
-// keep few values live.
+// One token of the gated delta rule on this lane's NP rows (8: a whole state per workgroup; fewer: a slice of 16 NP
+// rows): S *= exp(g) along K; u = beta (v - S k); S += u k^T; o = scale * (S_decayed q + u (k . q)) (= scale * S_new q).
+// dd = exp(g) of the lane's 4 key columns, vsrc = v at row v_src_row() of the slice (each row's v is broadcast from
+// it; lanes with c % 8 >= NP hold any value).  Every lane of a half wave computes its rows' full sums; the return
+// value is o at row 16 c + 2 w + half (meaningful on lanes c < NP).  Rows are reduced in groups of 4 to keep few
+// values live.
 // walk_token_kq: the same with k . q supplied by the caller (formed before the walk when the token's operands do not
 // depend on the state).
-__device__ __forceinline__ float walk_token_kq(f32x4 (&st)[8], const float (&kk)[4], const float (&qq)[4],
+template <int NP = 8>
+__device__ __forceinline__ float walk_token_kq(f32x4 (&st)[NP], const float (&kk)[4], const float (&qq)[4],
                                                const float (&dd)[4], float vsrc, float bt, float kq, float scale, int c) {
-    float vv[8];
-    vv[0] = v_of_row<0>(vsrc); vv[1] = v_of_row<1>(vsrc); vv[2] = v_of_row<2>(vsrc); vv[3] = v_of_row<3>(vsrc);
-    vv[4] = v_of_row<4>(vsrc); vv[5] = v_of_row<5>(vsrc); vv[6] = v_of_row<6>(vsrc); vv[7] = v_of_row<7>(vsrc);
+    constexpr int GS = NP < 4 ? NP : 4;  // rows per group
+    float vv[NP];
+    vv[0] = v_of_row<0>(vsrc);
+    if constexpr (NP > 1) vv[1] = v_of_row<1>(vsrc);
+    if constexpr (NP > 2) { vv[2] = v_of_row<2>(vsrc); vv[3] = v_of_row<3>(vsrc); }
+    if constexpr (NP > 4) {
+        vv[4] = v_of_row<4>(vsrc); vv[5] = v_of_row<5>(vsrc); vv[6] = v_of_row<6>(vsrc); vv[7] = v_of_row<7>(vsrc);
+    }
     float osel = 0.f;
 #pragma unroll
-    for (int g = 0; g < 2; ++g) {
-        float ak[4], aq[4];
+    for (int g = 0; g < NP / GS; ++g) {
+        float ak[GS], aq[GS];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            f32x4& s = st[4 * g + i];
+        for (int i = 0; i < GS; ++i) {
+            f32x4& s = st[GS * g + i];
             s.x *= dd[0]; s.y *= dd[1]; s.z *= dd[2]; s.w *= dd[3];
             ak[i] = s.x * kk[0] + s.y * kk[1] + s.z * kk[2] + s.w * kk[3];
             aq[i] = s.x * qq[0] + s.y * qq[1] + s.z * qq[2] + s.w * qq[3];
         }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) { ak[i] = sum32(ak[i]); aq[i] = sum32(aq[i]); }
+        for (int i = 0; i < GS; ++i) { ak[i] = sum32(ak[i]); aq[i] = sum32(aq[i]); }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            f32x4& s = st[4 * g + i];
-            const float u = bt * (vv[4 * g + i] - ak[i]);
+        for (int i = 0; i < GS; ++i) {
+            f32x4& s = st[GS * g + i];
+            const float u = bt * (vv[GS * g + i] - ak[i]);
             const float o = scale * (aq[i] + u * kq);
-            osel = (c == 4 * g + i) ? o : osel;
+            osel = (c == GS * g + i) ? o : osel;
             s.x += u * kk[0]; s.y += u * kk[1]; s.z += u * kk[2]; s.w += u * kk[3];
         }
     }
     return osel;
 }
-__device__ __forceinline__ float walk_token(f32x4 (&st)[8], const float (&kk)[4], const float (&qq)[4],
+template <int NP = 8>
+__device__ __forceinline__ float walk_token(f32x4 (&st)[NP], const float (&kk)[4], const float (&qq)[4],
                                             const float (&dd)[4], float vsrc, float bt, float scale, int c) {
     const float kq = sum32(kk[0] * qq[0] + kk[1] * qq[1] + kk[2] * qq[2] + kk[3] * qq[3]);
-    return walk_token_kq(st, kk, qq, dd, vsrc, bt, kq, scale, c);
+    return walk_token_kq<NP>(st, kk, qq, dd, vsrc, bt, kq, scale, c);
 }
 
 // Sum over the 64 lanes of a wave, returned wave-uniform.

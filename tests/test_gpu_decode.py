@@ -199,6 +199,17 @@ def test_spec_verify_streaming_size(oracle):
     _run(oracle, B=8, S=8, H=96, seed=12, spec=True, pages=False)
 
 
+def test_spec_verify_whole_state_workgroups(oracle):
+    """A launch above the slicing size (9 x 32 = 288 > 64 (sequence, head) pairs): one workgroup per whole state and
+    the gated RMSNorm inside the decode kernel (the launches of at most 64 pairs above split each state over 4
+    workgroups of 32 rows and finish the norm in a second kernel)."""
+    _run(oracle, B=9, S=4, H=32, seed=13, spec=True, pages=False)
+
+
+def test_plain_decode_whole_state_workgroups(oracle):
+    _run(oracle, B=9, S=1, H=32, seed=14, spec=False)
+
+
 def test_spec_verify_padding(oracle):
     """Padding write rows (skipped) and a sequence whose conv row idx[n, 0] is padding (dead: zero output)."""
     _run(oracle, B=6, S=4, H=2, seed=7, spec=True, pad=[(0, 3), (2, 1), (4, 0)])
