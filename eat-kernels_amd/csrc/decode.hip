@@ -57,8 +57,9 @@ __device__ __forceinline__ bool slot_ok(int64_t r, int lo, int64_t n) { return r
 // NP < 8 (small launches): the state rows are split over 8 / NP workgroups per (sequence, head), slice vs holding
 // rows 16 NP vs .. 16 NP (vs + 1) - 1 (NP rows per lane), so a token's step is 8 / NP times shorter and 8 / NP times
 // more CUs walk.  Every slice forms the conv and the q / k / gate operands of all 128 channels (the walk needs every
-// key column); slice 0 commits the conv cache.  Each slice writes bf16(o) of its rows to `out`, and norm_kernel then
-// applies the gated RMSNorm over the 128 rows of every (token, head).
+// key column).  Each slice writes bf16(o) of its rows to `out`; finish_kernel then applies the gated RMSNorm over the 128
+// rows of every (token, head) and commits the conv cache (finish_kernel; a slice cannot commit: the other slices of
+// its state may not have read the window yet).
 template <bool SPEC, bool SINGLE, bool NT, int NP>
 __global__ void __launch_bounds__(DC_THREADS) decode_kernel(DecParams p) {
     constexpr bool PRE = !SINGLE && !NT;
@@ -187,7 +188,7 @@ __global__ void __launch_bounds__(DC_THREADS) decode_kernel(DecParams p) {
         for (int tap = 0; tap < 4; ++tap) acc += bf2f(sWin[(t + tap) * DC_CH + c]) * sCw[tap * DC_CH + c];
         sX[i] = acc * sigmoidf_(acc);
     }
-    if (vs == 0) {
+    if (NP == 8) {  // (sliced launches commit in finish_kernel, after every slice has read the window)
         // spec: taps [0, 2 + S) <- window[1 .. 3 + S);  plain: taps [0, 3) <- window[S .. S + 3)
         const int ntap = SPEC ? 2 + S : 3, first = SPEC ? 1 : S;
 #pragma unroll 1
@@ -259,7 +260,7 @@ __global__ void __launch_bounds__(DC_THREADS) decode_kernel(DecParams p) {
             const float ss = sum32(wk.c < 8 ? ob * ob : 0.f);
             if (wk.c < 8) sO[t * D + wk.row(wk.c)] = ob;
             if (wk.c == 0) sRed[t * 16 + 2 * wk.w + wk.half] = ss;
-        } else {  // bf16(o) of the slice's rows straight to `out`; norm_kernel finishes them
+        } else {  // bf16(o) of the slice's rows straight to `out`; finish_kernel finishes them
             if (wk.c < NP) p.out[((int64_t)n * S + t) * p.out_rs + h * D + row0 + wk.row(wk.c)] = (uint16_t)f2bf(o);
         }
         if (SPEC) {
@@ -288,12 +289,12 @@ __global__ void __launch_bounds__(DC_THREADS) decode_kernel(DecParams p) {
     }
 }
 
-// The gated RMSNorm after a sliced decode: y = x rsqrt(mean(x^2) + eps) nw sigmoid(og) over the 128 values x = bf16(o)
+// The gated RMSNorm after a sliced decode (finish_kernel): y = x rsqrt(mean(x^2) + eps) nw sigmoid(og) over the 128 values x = bf16(o)
 // of one (token, head) row of `out` (one wave per row, two values per lane), in place.  A dead sequence's rows are
 // zero and stay zero.
 constexpr int NM_THREADS = 256;
-__global__ void __launch_bounds__(NM_THREADS) norm_kernel(DecParams p, int rows) {
-    const int row = blockIdx.x * (NM_THREADS / 64) + (threadIdx.x >> 6);  // (token, head): token-major
+__device__ __forceinline__ void norm_rows(const DecParams& p, int blk, int rows) {
+    const int row = blk * (NM_THREADS / 64) + (threadIdx.x >> 6);  // (token, head): token-major
     if (row >= rows) return;  // wave-uniform
     const int l = threadIdx.x & 63, t = row / p.H, h = row - t * p.H;
     uint32_t* o = reinterpret_cast<uint32_t*>(p.out + (int64_t)t * p.out_rs + h * D) + l;
@@ -304,6 +305,59 @@ __global__ void __launch_bounds__(NM_THREADS) norm_kernel(DecParams p, int rows)
     const float rstd = __frsqrt_rn(sum64(x0 * x0 + x1 * x1) * (1.f / D) + p.eps);
     *o = f2bf(x0 * rstd * nw.x * sigmoidf_(bf2f(og & 0xffffu))) |
          (f2bf(x1 * rstd * nw.y * sigmoidf_(bf2f(og >> 16))) << 16);
+}
+
+// The conv cache commit of a sliced decode (finish_kernel), one workgroup per (sequence, head), with the slot and liveness rules of
+// decode_kernel: spec taps [0, 2 + S) <- window rows [1, 3 + S), plain taps [0, 3) <- window rows [S, S + 3), where
+// window row r < 3 is history tap start + r and row r >= 3 is input row r - 3.  Every piece is read before any is
+// written (the commit shifts the slot's own taps).
+constexpr int CC_THREADS = NM_THREADS;
+template <bool SPEC>
+__device__ __forceinline__ void conv_commit(const DecParams& p, int blk) {
+    const int n = blk / p.H, h = blk - n * p.H, S = p.S, dim = p.H * D;
+    int a = 1;
+    int64_t rd, cs;
+    if (SPEC) {
+        a = p.acc[n];
+        a = a < 1 ? 1 : (a > S ? S : a);
+        rd = p.idx[(int64_t)n * S + a - 1];
+        cs = p.idx[(int64_t)n * S];
+    } else {
+        rd = p.idx[n];
+        cs = rd;
+    }
+    if (!(slot_ok(rd, 1, p.ssm_slots) && slot_ok(cs, 1, p.conv_slots))) return;
+    const int start = SPEC ? a - 1 : 0, ntap = SPEC ? 2 + S : 3, first = SPEC ? 1 : S;
+    uint16_t* crow = p.conv + cs * p.conv_ss;
+    constexpr int PER = ((2 + DC_MAX_S) * (DC_CH / 8) + CC_THREADS - 1) / CC_THREADS;
+    const int npieces = ntap * (DC_CH / 8);
+    u32x4 v[PER];
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+        const int i = min((int)threadIdx.x + CC_THREADS * k, npieces - 1);
+        const int r = first + i / (DC_CH / 8), c8 = (i % (DC_CH / 8)) * 8;
+        const int64_t col = (int64_t)(c8 / D) * dim + h * D + c8 % D;
+        const uint16_t* src =
+            (r < 3) ? crow + (int64_t)(start + r) * p.conv_ts + col : p.x + ((int64_t)n * S + (r - 3)) * p.x_rs + col;
+        v[k] = *reinterpret_cast<const u32x4*>(src);
+    }
+    __syncthreads();  // every read is complete before the first write
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+        const int i = threadIdx.x + CC_THREADS * k;
+        if (i < npieces) {
+            const int r = i / (DC_CH / 8), c8 = (i % (DC_CH / 8)) * 8;
+            *reinterpret_cast<u32x4*>(crow + (int64_t)r * p.conv_ts + (int64_t)(c8 / D) * dim + h * D + c8 % D) = v[k];
+        }
+    }
+}
+// One launch after a sliced decode: workgroups [0, nnorm) run norm_rows, the rest commit one (sequence, head) each.
+template <bool SPEC>
+__global__ void __launch_bounds__(NM_THREADS) finish_kernel(DecParams p, int rows, int nnorm) {
+    if ((int)blockIdx.x < nnorm)
+        norm_rows(p, blockIdx.x, rows);
+    else
+        conv_commit<SPEC>(p, blockIdx.x - nnorm);
 }
 
 bool aligned(const void* q, size_t a) { return (reinterpret_cast<uintptr_t>(q) % a) == 0; }
@@ -383,9 +437,9 @@ extern "C" int kda355_decode_launch(const KdaDecodeArgs* a, kda355_stream_t stre
                     : (nt ? decode_kernel<false, false, true, 8> : decode_kernel<false, false, false, 8>);
     hipLaunchKernelGGL(kernel, dim3(a->B * a->H * (8 / np)), dim3(DC_THREADS), lds, s, p);
     if (np < 8) {
-        const int rows = a->B * a->S * a->H;
-        hipLaunchKernelGGL(norm_kernel, dim3((rows + NM_THREADS / 64 - 1) / (NM_THREADS / 64)), dim3(NM_THREADS), 0, s, p,
-                           rows);
+        const int rows = a->B * a->S * a->H, nnorm = (rows + NM_THREADS / 64 - 1) / (NM_THREADS / 64);
+        hipLaunchKernelGGL(spec ? finish_kernel<true> : finish_kernel<false>, dim3(nnorm + a->B * a->H), dim3(NM_THREADS),
+                           0, s, p, rows, nnorm);
     }
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
