@@ -1011,8 +1011,8 @@ __device__ __forceinline__ void compose_ops(const float* sX, const ComposeOps& o
     }
 }
 // (entry, head, row block) of this workgroup: XCD-contiguous order keeps an entry-head's 8 blocks on one XCD
-__device__ __forceinline__ void scan_task(int H, int& ei, int& h, int& rb) {
-    const int t = xcd_task(blockIdx.x, gridDim.x);
+__device__ __forceinline__ void scan_task(int H, int blk, int nblk, int& ei, int& h, int& rb) {
+    const int t = xcd_task(blk, nblk);
     rb = t & 7;
     const int eh = t >> 3;
     ei = eh / H;
@@ -1089,12 +1089,12 @@ __device__ __forceinline__ void compose_scan(const uint16_t* sX, const ScanOps& 
 // LEAN (every split sequence in at most 3 pieces, config 1's case): one register set, no fetch ahead; ~100 VGPRs fit
 // four workgroups per CU, so a launch of many short scans runs in one round.
 template <bool LEAN>
-__global__ void __launch_bounds__(SCAN_THREADS) scan_kernel(PfParams p, const int32_t* __restrict__ tab) {
-    extern __shared__ __align__(16) unsigned char lds[];
+__device__ __forceinline__ void scan_body(const PfParams& p, const int32_t* __restrict__ tab, unsigned char* lds, int wg,
+                                          int nwg) {
     uint16_t* sX = reinterpret_cast<uint16_t*>(lds);
     const int H = p.H;
     int si, h, rb;
-    scan_task(H, si, h, rb);
+    scan_task(H, wg, nwg, si, h, rb);
     const int32_t* e = tab + tab[H_OFF_SCAN] + S_WORDS * si;
     const int n = e[S_SEQ], np = e[S_NP], slot0 = e[S_SLOT0];
     const int64_t ws_arr = (int64_t)tab[H_NSLOTS] * H * D * D;
@@ -1189,6 +1189,11 @@ __global__ void __launch_bounds__(SCAN_THREADS) scan_kernel(PfParams p, const in
         step(pc + 2, oc);
     }
 }
+template <bool LEAN>
+__global__ void __launch_bounds__(SCAN_THREADS) scan_kernel(PfParams p, const int32_t* __restrict__ tab) {
+    extern __shared__ __align__(16) unsigned char lds[];
+    scan_body<LEAN>(p, tab, lds, (int)blockIdx.x, (int)gridDim.x);
+}
 
 // Checkpoints inside later pieces: row = P_c S_start + S_loc(c) (fp32), then stored like the chunk walk's checkpoints.
 // One workgroup per (task, head, block of 16 state rows); tasks of the checkpoint kind the launch does not use exit.
@@ -1197,7 +1202,7 @@ __global__ void __launch_bounds__(SC_THREADS) ck_compose_kernel(PfParams p, cons
     float* sX = reinterpret_cast<float*>(lds);
     const int H = p.H;
     int ti, h, rb;
-    scan_task(H, ti, h, rb);
+    scan_task(H, (int)blockIdx.x, (int)gridDim.x, ti, h, rb);
     const int32_t* e = tab + tab[H_OFF_CKC] + K_WORDS * ti;
     const int ck_mode = (p.flags & KDA355_PF_CK_EVERY) ? 2 : ((p.flags & KDA355_PF_CK_SINGLE) ? 1 : 0);
     if (e[K_KIND] != ck_mode) return;
@@ -1239,11 +1244,11 @@ constexpr int FX_GROUP = 2;  // measured: 2 chunks per group beats 1, 4 and 8 (s
 constexpr int FX_ROW = 17 * 16;        // bytes per fp16 state row in LDS
 constexpr int FX_SMEM = D * FX_ROW;
 __device__ __forceinline__ int fx_slot(int v, int s) { return v * FX_ROW + 16 * (s ^ (4 * (v >> 5))); }
-__global__ void __launch_bounds__(FX_THREADS) fixup_kernel(PfParams p, const int32_t* __restrict__ tab) {
-    extern __shared__ __align__(16) unsigned char lds[];
+__device__ __forceinline__ void fixup_body(const PfParams& p, const int32_t* __restrict__ tab, unsigned char* lds,
+                                           int blk) {
     const int H = p.H;
-    const int ti = blockIdx.x / H;
-    const int h = blockIdx.x - ti * H;
+    const int ti = blk / H;
+    const int h = blk - ti * H;
     const int32_t* e = tab + tab[H_OFF_FIX] + X_WORDS * ti;
     const int tstart = e[X_TSTART], L = e[X_LEN];
     const int64_t ws_arr = (int64_t)tab[H_NSLOTS] * H * D * D;
@@ -1330,6 +1335,19 @@ __global__ void __launch_bounds__(FX_THREADS) fixup_kernel(PfParams p, const int
         if (64 * (i + 2) >= L) break;
     }
 }
+__global__ void __launch_bounds__(FX_THREADS) fixup_kernel(PfParams p, const int32_t* __restrict__ tab) {
+    extern __shared__ __align__(16) unsigned char lds[];
+    fixup_body(p, tab, lds, (int)blockIdx.x);
+}
+// Every split sequence in 2 pieces (config 1): the fixups need only the first pieces' end states, which the chunk
+// kernel stored, so they run in one launch beside the (lean) scan: workgroups [0, nscan) scan, the rest fix up.
+__global__ void __launch_bounds__(FX_THREADS) scan_fix_kernel(PfParams p, const int32_t* __restrict__ tab, int nscan) {
+    extern __shared__ __align__(16) unsigned char lds[];
+    if ((int)blockIdx.x < nscan)
+        scan_body<true>(p, tab, lds, (int)blockIdx.x, nscan);
+    else
+        fixup_body(p, tab, lds, (int)blockIdx.x - nscan);
+}
 
 template <bool RG, bool P1>
 hipError_t launch_chunk(const PfParams& p, int list_off, int entries, hipStream_t s) {
@@ -1367,6 +1385,12 @@ hipError_t launch_ck_compose(const PfParams& p, int entries, hipStream_t s) {
 }
 hipError_t launch_fixup(const PfParams& p, int entries, hipStream_t s) {
     hipLaunchKernelGGL(fixup_kernel, dim3(entries * p.H), dim3(FX_THREADS), FX_SMEM, s, p, p.tab);
+    return hipGetLastError();
+}
+hipError_t launch_scan_fix(const PfParams& p, int scan_entries, int fix_entries, hipStream_t s) {
+    static_assert(SCAN_THREADS == FX_THREADS && SCAN_SMEM <= FX_SMEM, "scan_fix_kernel shares one launch shape");
+    const int nscan = scan_entries * p.H * (D / SC_ROWS);
+    hipLaunchKernelGGL(scan_fix_kernel, dim3(nscan + fix_entries * p.H), dim3(FX_THREADS), FX_SMEM, s, p, p.tab, nscan);
     return hipGetLastError();
 }
 
@@ -1735,8 +1759,12 @@ extern "C" int kda355_prefill_launch(const KdaPrefillArgs* a, kda355_stream_t st
         e = rg ? launch_chunk<true, true>(p, off_final, pl->num_chains, s) : launch_chunk<false, true>(p, off_final, pl->num_chains, s);
         // every split sequence has >= 2 pieces, so the most-cut one has at most num_pieces - 2 (num_split - 1)
         const bool lean = pl->num_pieces - 2 * (pl->num_split - 1) <= 3;
-        if (e == hipSuccess) e = launch_scan(p, pl->num_split, lean, s);
-        if (e == hipSuccess && pl->num_fix_tasks > 0) e = launch_fixup(p, pl->num_fix_tasks, s);
+        if (pl->num_pieces == 2 * pl->num_split && pl->num_fix_tasks > 0) {  // every split sequence in 2 pieces
+            if (e == hipSuccess) e = launch_scan_fix(p, pl->num_split, pl->num_fix_tasks, s);
+        } else {
+            if (e == hipSuccess) e = launch_scan(p, pl->num_split, lean, s);
+            if (e == hipSuccess && pl->num_fix_tasks > 0) e = launch_fixup(p, pl->num_fix_tasks, s);
+        }
         if (e == hipSuccess && pl->num_ck_tasks > 0) e = launch_ck_compose(p, pl->num_ck_tasks, s);
     } else {
         e = rg ? launch_chunk<true, false>(p, off_final, pl->num_chains, s) : launch_chunk<false, false>(p, off_final, pl->num_chains, s);
