@@ -299,12 +299,12 @@ __device__ __forceinline__ void norm_rows(const DecParams& p, int blk, int rows)
     const int l = threadIdx.x & 63, t = row / p.H, h = row - t * p.H;
     uint32_t* o = reinterpret_cast<uint32_t*>(p.out + (int64_t)t * p.out_rs + h * D) + l;
     const uint32_t xo = *o;
-    const uint32_t og = *(reinterpret_cast<const uint32_t*>(p.og + (int64_t)t * p.og_rs + h * D) + l);
-    const f32x2 nw = *reinterpret_cast<const f32x2*>(p.nw + 2 * l);
+    // out_gate and norm_weight element by element: the launch checks neither for more than their element alignment
+    const uint16_t* og = p.og + (int64_t)t * p.og_rs + h * D + 2 * l;
     const float x0 = bf2f(xo & 0xffffu), x1 = bf2f(xo >> 16);
     const float rstd = __frsqrt_rn(sum64(x0 * x0 + x1 * x1) * (1.f / D) + p.eps);
-    *o = f2bf(x0 * rstd * nw.x * sigmoidf_(bf2f(og & 0xffffu))) |
-         (f2bf(x1 * rstd * nw.y * sigmoidf_(bf2f(og >> 16))) << 16);
+    *o = f2bf(x0 * rstd * p.nw[2 * l] * sigmoidf_(bf2f(og[0]))) |
+         (f2bf(x1 * rstd * p.nw[2 * l + 1] * sigmoidf_(bf2f(og[1]))) << 16);
 }
 
 // The conv cache commit of a sliced decode (finish_kernel), one workgroup per (sequence, head), with the slot and liveness rules of
