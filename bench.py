@@ -618,7 +618,7 @@ def main():
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "algorithmic_bytes": c1["bytes"],
                      "kernel": "prefill launch: chunk_kernel (fused chunk-64 prefill, one workgroup per (piece, head)), "
-                               "then the scan and the output fixup (one scan_fix_kernel launch at this configuration) completing the split sequences",
+                               "then the scan and the output fixup (one tail_kernel launch at this configuration) completing the split sequences",
                      "mfma": {"achieved": round(tflops, 2), "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                               "frac": round(tflops / MFMA_PEAK_TFLOPS, 4), "flops": c1["flops"]}},
         "cpu_baseline": cpu,

@@ -1197,12 +1197,12 @@ __global__ void __launch_bounds__(SCAN_THREADS) scan_kernel(PfParams p, const in
 
 // Checkpoints inside later pieces: row = P_c S_start + S_loc(c) (fp32), then stored like the chunk walk's checkpoints.
 // One workgroup per (task, head, block of 16 state rows); tasks of the checkpoint kind the launch does not use exit.
-__global__ void __launch_bounds__(SC_THREADS) ck_compose_kernel(PfParams p, const int32_t* __restrict__ tab) {
-    extern __shared__ __align__(16) unsigned char lds[];
+__device__ __forceinline__ void ck_body(const PfParams& p, const int32_t* __restrict__ tab, unsigned char* lds, int wg,
+                                        int nwg) {
     float* sX = reinterpret_cast<float*>(lds);
     const int H = p.H;
     int ti, h, rb;
-    scan_task(H, (int)blockIdx.x, (int)gridDim.x, ti, h, rb);
+    scan_task(H, wg, nwg, ti, h, rb);
     const int32_t* e = tab + tab[H_OFF_CKC] + K_WORDS * ti;
     const int ck_mode = (p.flags & KDA355_PF_CK_EVERY) ? 2 : ((p.flags & KDA355_PF_CK_SINGLE) ? 1 : 0);
     if (e[K_KIND] != ck_mode) return;
@@ -1335,18 +1335,19 @@ __device__ __forceinline__ void fixup_body(const PfParams& p, const int32_t* __r
         if (64 * (i + 2) >= L) break;
     }
 }
-__global__ void __launch_bounds__(FX_THREADS) fixup_kernel(PfParams p, const int32_t* __restrict__ tab) {
+// The passes after the scan in one launch: workgroups [0, nscan) run the lean scan (nscan > 0 only when every split
+// sequence has 2 pieces, as in config 1: then the fixups and checkpoints need only the first pieces' end states,
+// which the chunk kernel stored), the next nfix the output fixup, the rest the checkpoint compose.  Fixups and
+// checkpoints are independent of each other: each reads start states and writes its own rows.
+__global__ void __launch_bounds__(FX_THREADS) tail_kernel(PfParams p, const int32_t* __restrict__ tab, int nscan, int nfix) {
     extern __shared__ __align__(16) unsigned char lds[];
-    fixup_body(p, tab, lds, (int)blockIdx.x);
-}
-// Every split sequence in 2 pieces (config 1): the fixups need only the first pieces' end states, which the chunk
-// kernel stored, so they run in one launch beside the (lean) scan: workgroups [0, nscan) scan, the rest fix up.
-__global__ void __launch_bounds__(FX_THREADS) scan_fix_kernel(PfParams p, const int32_t* __restrict__ tab, int nscan) {
-    extern __shared__ __align__(16) unsigned char lds[];
-    if ((int)blockIdx.x < nscan)
-        scan_body<true>(p, tab, lds, (int)blockIdx.x, nscan);
+    const int b = (int)blockIdx.x;
+    if (b < nscan)
+        scan_body<true>(p, tab, lds, b, nscan);
+    else if (b < nscan + nfix)
+        fixup_body(p, tab, lds, b - nscan);
     else
-        fixup_body(p, tab, lds, (int)blockIdx.x - nscan);
+        ck_body(p, tab, lds, b - nscan - nfix, (int)gridDim.x - nscan - nfix);
 }
 
 template <bool RG, bool P1>
@@ -1379,18 +1380,13 @@ hipError_t launch_scan(const PfParams& p, int entries, bool lean, hipStream_t s)
     return lean ? launch_composer(scan_kernel<true>, p, entries, SCAN_THREADS, SCAN_SMEM, s, attr_set[1])
                 : launch_composer(scan_kernel<false>, p, entries, SCAN_THREADS, SCAN_SMEM, s, attr_set[0]);
 }
-hipError_t launch_ck_compose(const PfParams& p, int entries, hipStream_t s) {
-    static bool attr_set = false;
-    return launch_composer(ck_compose_kernel, p, entries, SC_THREADS, SC_SMEM, s, attr_set);
-}
-hipError_t launch_fixup(const PfParams& p, int entries, hipStream_t s) {
-    hipLaunchKernelGGL(fixup_kernel, dim3(entries * p.H), dim3(FX_THREADS), FX_SMEM, s, p, p.tab);
-    return hipGetLastError();
-}
-hipError_t launch_scan_fix(const PfParams& p, int scan_entries, int fix_entries, hipStream_t s) {
-    static_assert(SCAN_THREADS == FX_THREADS && SCAN_SMEM <= FX_SMEM, "scan_fix_kernel shares one launch shape");
-    const int nscan = scan_entries * p.H * (D / SC_ROWS);
-    hipLaunchKernelGGL(scan_fix_kernel, dim3(nscan + fix_entries * p.H), dim3(FX_THREADS), FX_SMEM, s, p, p.tab, nscan);
+hipError_t launch_tail(const PfParams& p, int scan_entries, int fix_entries, int ck_entries, hipStream_t s) {
+    static_assert(SCAN_THREADS == FX_THREADS && SC_THREADS == FX_THREADS && SCAN_SMEM <= FX_SMEM && SC_SMEM <= FX_SMEM,
+                  "tail_kernel runs every pass in one launch shape");
+    const int nscan = scan_entries * p.H * (D / SC_ROWS), nfix = fix_entries * p.H;
+    const int nck = ck_entries * p.H * (D / SC_ROWS);
+    if (nscan + nfix + nck == 0) return hipSuccess;
+    hipLaunchKernelGGL(tail_kernel, dim3(nscan + nfix + nck), dim3(FX_THREADS), FX_SMEM, s, p, p.tab, nscan, nfix);
     return hipGetLastError();
 }
 
@@ -1759,13 +1755,12 @@ extern "C" int kda355_prefill_launch(const KdaPrefillArgs* a, kda355_stream_t st
         e = rg ? launch_chunk<true, true>(p, off_final, pl->num_chains, s) : launch_chunk<false, true>(p, off_final, pl->num_chains, s);
         // every split sequence has >= 2 pieces, so the most-cut one has at most num_pieces - 2 (num_split - 1)
         const bool lean = pl->num_pieces - 2 * (pl->num_split - 1) <= 3;
-        if (pl->num_pieces == 2 * pl->num_split && pl->num_fix_tasks > 0) {  // every split sequence in 2 pieces
-            if (e == hipSuccess) e = launch_scan_fix(p, pl->num_split, pl->num_fix_tasks, s);
+        if (pl->num_pieces == 2 * pl->num_split) {  // every split sequence in 2 pieces: the scan joins the tail launch
+            if (e == hipSuccess) e = launch_tail(p, pl->num_split, pl->num_fix_tasks, pl->num_ck_tasks, s);
         } else {
             if (e == hipSuccess) e = launch_scan(p, pl->num_split, lean, s);
-            if (e == hipSuccess && pl->num_fix_tasks > 0) e = launch_fixup(p, pl->num_fix_tasks, s);
+            if (e == hipSuccess) e = launch_tail(p, 0, pl->num_fix_tasks, pl->num_ck_tasks, s);
         }
-        if (e == hipSuccess && pl->num_ck_tasks > 0) e = launch_ck_compose(p, pl->num_ck_tasks, s);
     } else {
         e = rg ? launch_chunk<true, false>(p, off_final, pl->num_chains, s) : launch_chunk<false, false>(p, off_final, pl->num_chains, s);
     }
