@@ -289,14 +289,38 @@ __global__ void __launch_bounds__(DC_THREADS) decode_kernel(DecParams p) {
     }
 }
 
+// Read row, conv row and accepted length of sequence n under decode_kernel's slot rules; false for a dead sequence
+// (read or conv row is padding), whose output rows are zero.
+template <bool SPEC>
+__device__ __forceinline__ bool seq_slots(const DecParams& p, int n, int& a, int64_t& rd, int64_t& cs) {
+    a = 1;
+    if (SPEC) {
+        a = p.acc[n];
+        a = a < 1 ? 1 : (a > p.S ? p.S : a);
+        rd = p.idx[(int64_t)n * p.S + a - 1];
+        cs = p.idx[(int64_t)n * p.S];
+    } else {
+        rd = p.idx[n];
+        cs = rd;
+    }
+    return slot_ok(rd, 1, p.ssm_slots) && slot_ok(cs, 1, p.conv_slots);
+}
+
 // The gated RMSNorm after a sliced decode (finish_kernel): y = x rsqrt(mean(x^2) + eps) nw sigmoid(og) over the 128 values x = bf16(o)
-// of one (token, head) row of `out` (one wave per row, two values per lane), in place.  A dead sequence's rows are
-// zero and stay zero.
+// of one (token, head) row of `out` (one wave per row, two values per lane), in place.  A dead sequence's rows were
+// written as zeros by the slices and are left alone (rescaling them would turn a NaN out_gate or a negative weight
+// into NaN or -0).
 constexpr int NM_THREADS = 256;
+template <bool SPEC>
 __device__ __forceinline__ void norm_rows(const DecParams& p, int blk, int rows) {
     const int row = blk * (NM_THREADS / 64) + (threadIdx.x >> 6);  // (token, head): token-major
     if (row >= rows) return;  // wave-uniform
     const int l = threadIdx.x & 63, t = row / p.H, h = row - t * p.H;
+    {
+        int a;
+        int64_t rd, cs;
+        if (!seq_slots<SPEC>(p, t / p.S, a, rd, cs)) return;  // wave-uniform
+    }
     uint32_t* o = reinterpret_cast<uint32_t*>(p.out + (int64_t)t * p.out_rs + h * D) + l;
     const uint32_t xo = *o;
     // out_gate and norm_weight element by element: the launch checks neither for more than their element alignment
@@ -315,18 +339,9 @@ constexpr int CC_THREADS = NM_THREADS;
 template <bool SPEC>
 __device__ __forceinline__ void conv_commit(const DecParams& p, int blk) {
     const int n = blk / p.H, h = blk - n * p.H, S = p.S, dim = p.H * D;
-    int a = 1;
+    int a;
     int64_t rd, cs;
-    if (SPEC) {
-        a = p.acc[n];
-        a = a < 1 ? 1 : (a > S ? S : a);
-        rd = p.idx[(int64_t)n * S + a - 1];
-        cs = p.idx[(int64_t)n * S];
-    } else {
-        rd = p.idx[n];
-        cs = rd;
-    }
-    if (!(slot_ok(rd, 1, p.ssm_slots) && slot_ok(cs, 1, p.conv_slots))) return;
+    if (!seq_slots<SPEC>(p, n, a, rd, cs)) return;
     const int start = SPEC ? a - 1 : 0, ntap = SPEC ? 2 + S : 3, first = SPEC ? 1 : S;
     uint16_t* crow = p.conv + cs * p.conv_ss;
     constexpr int PER = ((2 + DC_MAX_S) * (DC_CH / 8) + CC_THREADS - 1) / CC_THREADS;
@@ -355,7 +370,7 @@ __device__ __forceinline__ void conv_commit(const DecParams& p, int blk) {
 template <bool SPEC>
 __global__ void __launch_bounds__(NM_THREADS) finish_kernel(DecParams p, int rows, int nnorm) {
     if ((int)blockIdx.x < nnorm)
-        norm_rows(p, blockIdx.x, rows);
+        norm_rows<SPEC>(p, blockIdx.x, rows);
     else
         conv_commit<SPEC>(p, blockIdx.x - nnorm);
 }

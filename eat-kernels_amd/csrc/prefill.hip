@@ -1690,6 +1690,11 @@ extern "C" int kda355_prefill_launch(const KdaPrefillArgs* a, kda355_stream_t st
     const uint32_t f = a->flags;
     KDA_CHECK_ARG(a->q && a->k && a->v && a->g && a->beta && a->out && a->tables, "prefill: a required pointer is null");
     KDA_CHECK_ARG(!(f & KDA355_PF_RAW_GATE) || (a->A_log && a->dt_bias), "prefill: raw gate needs A_log and dt_bias");
+    // the in-kernel gate keeps every log-decay in [lower_bound, 0]; the diagonal Gram blocks span e^{+-8 |g|} in bf16
+    // pairs, which holds for a per-token log-decay above -11 (a given g must satisfy the same: g >= -11)
+    KDA_CHECK_ARG(!(f & KDA355_PF_RAW_GATE) || a->lower_bound >= KDA355_MIN_LOG_DECAY,
+                  "prefill: lower_bound %g is below %g (the chunk kernel's decay range)", (double)a->lower_bound,
+                  (double)KDA355_MIN_LOG_DECAY);
     const bool pool = f & KDA355_PF_POOL;
     KDA_CHECK_ARG(pool ? (a->state_pool && a->state_idx && a->has_initial_state) : (a->final_state != nullptr),
                   "prefill: pool mode needs state_pool/state_idx/has_initial_state, contiguous mode final_state");
@@ -1770,3 +1775,4 @@ extern "C" int kda355_prefill_launch(const KdaPrefillArgs* a, kda355_stream_t st
     }
     return 0;
 }
+

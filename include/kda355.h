@@ -44,6 +44,10 @@ typedef struct ihipStream_t* kda355_stream_t; /* == hipStream_t */
 #define KDA355_ELAUNCH (-2)
 #define KDA355_HEAD_DIM 128
 #define KDA355_CHUNK 64
+/* Smallest per-token log-decay the chunked prefill accepts: its diagonal Gram blocks hold e^{+-8 g} over 8 tokens in
+   bf16 pairs.  Raw-gate launches (g = lower_bound * sigmoid(..) in [lower_bound, 0]) with lower_bound below it are
+   rejected; a given fp32 g must stay >= it. */
+#define KDA355_MIN_LOG_DECAY (-11.0f)
 
 /* ------------------------------------------------------------------------------------------------ recurrent */
 

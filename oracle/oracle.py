@@ -235,12 +235,14 @@ def recurrent(q, k, v, g, beta, pool, state_indices, num_accepted_tokens=None, s
       spec  (state_indices [B, S], num_accepted_tokens [B]): start from pool[state_indices[n, a-1]], write the
             state after token t to pool[state_indices[n, t]] when that slot is > 0.
     Slot 0 is the reserved padding slot: a sequence whose read slot is <= 0 is neither read nor written (its
-    output rows are zero).  Returns (out [B*S, H, 128] fp32, new_pool, written_rows)."""
+    output rows are zero).  normalize_qk uses the decode form x * rsqrt(sum x^2 + 1e-6) (reference.py:159-160, the
+    form of vLLM's fused_recurrent_kda with use_qk_l2norm_in_kernel), not the prefill clamp x / max(|x|, 1e-6);
+    scale multiplies q after it.  Returns (out [B*S, H, 128] fp32, new_pool, written_rows)."""
     if scale is None:
         scale = D ** -0.5
     q, k, v, g, beta = map(_f32, (q, k, v, g, beta))
     if normalize_qk:
-        q, k = l2norm_clamp(q), l2norm_clamp(k)
+        q, k = l2norm_rsqrt(q), l2norm_rsqrt(k)
     idx = np.asarray(state_indices, dtype=np.int64)
     spec = num_accepted_tokens is not None
     B = idx.shape[0]
@@ -275,7 +277,7 @@ def recurrent(q, k, v, g, beta, pool, state_indices, num_accepted_tokens=None, s
 
 
 def decode_full(mixed_qkv, conv_state, conv_weight, gate_in, beta_in, out_gate, A_log, dt_bias, norm_weight,
-                ssm_state, state_indices, num_accepted_tokens, norm_eps, lower_bound, precision=32):
+                ssm_state, state_indices, num_accepted_tokens, norm_eps, lower_bound, precision=32, aux=False):
     """reference.py:104-181 (fused conv1d + SiLU + KDA + gated RMSNorm decode / spec verify).
 
     mixed_qkv [T, 3*H*128] (bf16 values), conv_state [slots, taps, 3*H*128] (bf16 values), conv_weight
@@ -283,7 +285,9 @@ def decode_full(mixed_qkv, conv_state, conv_weight, gate_in, beta_in, out_gate, 
     norm_weight [128], ssm_state [slots, H, 128, 128].  Returns (out [T, H*128] bf16-rounded fp32, conv_new,
     ssm_new).  Rows <= 0 are padding: a sequence whose read row or conv row (idx[n, 0] in spec) is padding gets zero
     output and writes nothing (the reference kernel's slot rule, kda/mi350x/kda/decode/kda_v14_b.cu:1013-1042);
-    spec writes skip padding rows (reference.py:168-171)."""
+    spec writes skip padding rows (reference.py:168-171).  aux=True also returns (bf16(o) [T, H*128], the per-element
+    factor rstd * norm_weight * sigmoid(out_gate) [T, H*128]) of the gated RMSNorm, from which a checker can bound
+    what one step of the intermediate bf16(o) rounding moves each output element."""
     W = 4
     T, C = mixed_qkv.shape
     dim = C // 3
@@ -328,13 +332,18 @@ def decode_full(mixed_qkv, conv_state, conv_weight, gate_in, beta_in, out_gate, 
     ob = bf16_round(o)                                            # reference.py:172-175
     rstd = 1.0 / np.sqrt((ob * ob).mean(-1, keepdims=True) + np.float32(norm_eps))
     og = _f32(out_gate).reshape(T, H, D)
-    y = ob * rstd * _f32(norm_weight) * (1.0 / (1.0 + np.exp(-og)))
+    fac = rstd * _f32(norm_weight) * (1.0 / (1.0 + np.exp(-og)))
+    y = ob * fac
     out = bf16_round(y.reshape(T, dim))
     conv_new = np.array(conv_state, copy=True)
     ssm_new = np.array(ssm_state, copy=True)
+    ob = ob.reshape(T, dim)
+    fac = fac.reshape(T, dim)
     for n in range(B):
         if not live[n]:
             out[n * S:(n + 1) * S] = 0.0
+            ob[n * S:(n + 1) * S] = 0.0                           # no norm applies to a dead sequence's rows
+            fac[n * S:(n + 1) * S] = 0.0
             continue
         if spec:
             for t in range(S):
@@ -345,6 +354,8 @@ def decode_full(mixed_qkv, conv_state, conv_weight, gate_in, beta_in, out_gate, 
             ssm_new[read_slot[n]] = steps[n, S - 1]
             # reference.py:178-180 (taps [0, 3); more taps, which kernel_v13_a.py:711-712 accepts, stay as they are)
             conv_new[cslot[n], :W - 1] = window[n, -(W - 1):]
+    if aux:
+        return out, conv_new, ssm_new, (ob, fac)
     return out, conv_new, ssm_new
 
 

@@ -178,6 +178,62 @@ def test_prefill_plan_splits_long_sequences():
     assert pl.num_split == 1 and time.perf_counter() - t0 < 0.05
 
 
+# the reference eval's host gate layouts (kda/mi350x/benchmark/eval_kda_mi350x.py:98-112: (new tokens, has initial
+# state, checkpoint offset) per sequence)
+_GATE_LAYOUTS = {
+    "p12_loaded16k_1": (12, [(3008, 1, 3008), (1536, 1, 1536), (256, 1, 64), (128, 0, 0), (1600, 1, 832), (640, 1, 0),
+                             (576, 1, 0), (512, 1, 0), (448, 1, 0), (2560, 1, 2560), (320, 1, 256), (4288, 1, 3712)]),
+    "p96_loaded8k_1": (96, [(384, 1, 0), (1344, 1, 896), (3008, 0, 2048), (2176, 1, 2048), (320, 1, 0), (832, 0, 0)]),
+}
+
+
+def test_prepare_time_gate():
+    """prefill_prepare runs once per serving step on a new layout: the reference eval's bound is 1 ms + 5 us per
+    sequence, median over 5 fresh layouts (the lengths jittered by up to 64 tokens between neighbours, checkpoints at
+    multiples of 1024; eval_kda_mi350x.py:669-712).  The host plan alone is timed here (no device)."""
+    import statistics
+    import time
+    import kda355
+    for name, (H, seqs) in _GATE_LAYOUTS.items():
+        times = []
+        for j in range(5):
+            lens = [s[0] for s in seqs]
+            if len(lens) > 1:
+                a, b = j % len(lens), (j + 1) % len(lens)
+                d = min(64, lens[a] - 1)
+                lens[a] -= d
+                lens[b] += d
+            cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+            offs = np.array([(x // 1024) * 1024 if x >= 1024 else 0 for x in lens], np.int32)
+            t0 = time.perf_counter()
+            kda355.plan(cu, H, checkpoint_offsets=offs)
+            times.append((time.perf_counter() - t0) * 1e3)
+        limit = 1.0 + 0.005 * len(seqs)
+        assert statistics.median(times) <= limit, f"{name}: plan median {statistics.median(times):.3f} ms > {limit}"
+
+
+def test_prefill_rejects_lower_bound_below_decay_range():
+    """A raw-gate launch whose lower_bound is below KDA355_MIN_LOG_DECAY (-11) is rejected before any device call."""
+    from kda355 import _lib
+    L = _lib.lib()
+    pin = _lib.KdaPrefillPlanIn()
+    cu = np.array([0, 64], np.int64)
+    pin.cu_seqlens = ctypes.c_void_p(cu.ctypes.data)
+    pin.N, pin.H = 1, 1
+    pl = _lib.KdaPrefillPlan()
+    assert L.kda355_prefill_plan(ctypes.byref(pin), ctypes.byref(pl), None, 0) == 0
+    a = _lib.KdaPrefillArgs()
+    fake = ctypes.c_void_p(1 << 20)                      # never dereferenced: the arguments are rejected first
+    for f in ("q", "k", "v", "g", "beta", "A_log", "dt_bias", "out", "tables", "final_state"):
+        setattr(a, f, fake)
+    a.T, a.N, a.H = 64, 1, 1
+    a.flags = 2 | 4 | 1                                  # RAW_GATE | RAW_BETA | NORMALIZE_QK
+    a.plan = ctypes.pointer(pl)
+    a.lower_bound = -12.0
+    assert L.kda355_prefill_launch(ctypes.byref(a), None) == _lib.EINVAL
+    assert b"lower_bound" in L.kda355_last_error()
+
+
 def test_prefill_plan_schedules_both_checkpoint_kinds():
     """Later pieces get compose tasks for the single checkpoint and for every-n rows alike (the launch's mode picks
     one; a plan made without flags must still cover both): 8192 tokens (128 chunks) on an idle chip, single

@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import OUT_TOL, STATE_TOL, bf16_half_ulp, config_inputs, f32, gen, out_err, rel_frob
+from helpers import OUT_TOL, STATE_TOL, bf16_half_ulp, check_out, config_inputs, f32, gen, rel_frob
 
 pytestmark = pytest.mark.gpu
 D = 128
@@ -30,10 +30,8 @@ def _cu(lens):
     return np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
 
 
-def _check_out(got, ref, what):
-    ex, raw, rel = out_err(f32(got), ref)
-    assert ex <= OUT_TOL, f"{what}: output excess {ex:.3e} (raw {raw:.3e}, relL2 {rel:.3e})"
-    return ex
+def _check_out(got, ref, what, cu=None):
+    return check_out(got, ref, what, cu)
 
 
 def _plain_case(oracle, H, lens, seed, init=True, gscale=1.0, heads_checked=None):
@@ -53,7 +51,7 @@ def _plain_case(oracle, H, lens, seed, init=True, gscale=1.0, heads_checked=None
     sel = lambda x: np.ascontiguousarray(f32(x)[:, hs])  # noqa: E731
     ro, rf = oracle.prefill_plain(sel(q), sel(k), sel(v), sel(gg), sel(beta), _cu(lens),
                                   initial_state=None if h0 is None else sel(h0), precision=64)
-    _check_out(o[0][:, hs], ro, f"H={H} lens={lens[:6]}")
+    _check_out(o[0][:, hs], ro, f"H={H} lens={lens[:6]}", _cu(lens))
     got = f32(fin)[:, hs]
     for n in range(N):
         e = rel_frob(got[n], rf[n])
@@ -128,7 +126,7 @@ def test_kda_prefill_raw_gates(oracle, gates):
     torch.cuda.synchronize()
     qn, kn, vf, gl, bt = _oracle_gated(oracle, q, k, v, raw_g, raw_b, A_log, dt_bias)
     ro, rf, _ = oracle.chains(qn, kn, vf, gl, bt, _cu(lens), D ** -0.5, f32(h0), precision=64)
-    _check_out(o[0], ro, f"gates={gates}")
+    _check_out(o[0], ro, f"gates={gates}", _cu(lens))
     for n in range(len(lens)):
         assert rel_frob(f32(fin[n]), rf[n]) <= STATE_TOL, f"gates={gates} seq {n}"
 
@@ -184,7 +182,7 @@ def test_serving_pool_checkpoints_page_layout(oracle):
     ro, rnew = oracle.prefill_serving(f32(q), f32(k), f32(v), f32(raw_g), f32(raw_b), f32(A_log), f32(dt_bias), -5.0,
                                       D ** -0.5, pool0, sidx.numpy(), np.array(hinit, bool), _cu(lens),
                                       np.array(ck_off), cidx.numpy(), precision=64)
-    _check_out(out[0], ro, "serving")
+    _check_out(out[0], ro, "serving", _cu(lens))
     got = ssm.cpu().numpy()
     written = [int(s) for s in sidx] + [int(c) for c in cidx if c >= 0]
     for r in written:
@@ -261,7 +259,7 @@ def test_every_n_checkpoints_fp32_and_bf16(oracle, every):
     ro, rf, rows, starts = oracle.checkpoints_every_n(qn, kn, vf, gl, bt, _cu(lens), every, initial_state=S0,
                                                       normalize_qk=False, precision=64)
     assert list(starts) == list(ccs.numpy())
-    _check_out(got[torch.float32][0][0], ro, f"every={every}")
+    _check_out(got[torch.float32][0][0], ro, f"every={every}", _cu(lens))
     ck32 = f32(got[torch.float32][2])
     ck16 = f32(got[torch.bfloat16][2])
     for r in range(C):
@@ -316,7 +314,7 @@ def test_graph_capture_prefill(oracle):
         torch.cuda.synchronize()
         ro, rf = oracle.prefill_plain(f32(q), f32(k), f32(v), f32(gg), f32(beta), _cu(lens), initial_state=f32(init),
                                       precision=64)
-        _check_out(out[0], ro, f"replay {rep}")
+        _check_out(out[0], ro, f"replay {rep}", _cu(lens))
         for n in range(N):
             assert rel_frob(f32(fin[n]), rf[n]) <= STATE_TOL
 
@@ -357,7 +355,7 @@ def test_split_long_sequence_plain(oracle):
     torch.cuda.synchronize()
     ro, rf = oracle.prefill_plain(f32(q), f32(k), f32(v), f32(gg), f32(beta), _cu(lens), initial_state=f32(h0),
                                   precision=64)
-    _check_out(o[0], ro, "split plain")
+    _check_out(o[0], ro, "split plain", _cu(lens))
     for n in range(len(lens)):
         assert rel_frob(f32(fin[n]), rf[n]) <= STATE_TOL, f"split plain seq {n}"
 
@@ -469,7 +467,7 @@ def test_split_pool_every_n_checkpoints(oracle, ckdt):
     torch.cuda.synchronize()
     ro, rf, rrows, _ = oracle.checkpoints_every_n(f32(q), f32(k), f32(v), f32(gg), f32(beta), _cu(lens), every,
                                                  initial_state=f32(pool0)[slot.numpy()], precision=64)
-    _check_out(o[0], ro, "split every-n")
+    _check_out(o[0], ro, "split every-n", _cu(lens))
     assert rel_frob(f32(pool[3]), rf[0]) <= STATE_TOL
     untouched = [i for i in range(P) if i != 3]
     assert torch.equal(pool[untouched].cpu(), pool0[untouched]), "other pool slots changed"
@@ -520,7 +518,7 @@ def test_split_serving_single_checkpoints(oracle):
     ro, rnew = oracle.prefill_serving(f32(q), f32(k), f32(v), f32(raw_g), f32(raw_b), f32(A_log), f32(dt_bias), -5.0,
                                       D ** -0.5, pool0, sidx.numpy(), np.array(hinit, bool), _cu(lens),
                                       np.array(ck_off), cidx.numpy(), precision=64)
-    _check_out(out[0], ro, "split serving")
+    _check_out(out[0], ro, "split serving", _cu(lens))
     got = ssm.cpu().numpy()
     for r in [int(s) for s in sidx] + [int(c) for c in cidx]:
         e = rel_frob(got[r], rnew[r])

@@ -7,7 +7,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import OUT_TOL, STATE_TOL, config_inputs, f32, gen, out_err, rel_frob
+from helpers import STATE_TOL, check_out, config_inputs, f32, gen, rel_frob
 
 pytestmark = pytest.mark.gpu
 D = 128
@@ -22,12 +22,22 @@ def _say(msg):
     print(f"[case] {msg}", flush=True)
 
 
-def _run_case(oracle, B, S, H, slots, seed, spec, raw=False, pad_rows=(), graph=False):
+def _cu_tokens(B, S):
+    return np.arange(0, B * S + 1, S)
+
+
+def _run_case(oracle, B, S, H, slots, seed, spec, raw=False, pad_rows=(), graph=False, qk_norms=False):
     kda = _kda()
-    _say(f"recurrent B={B} S={S} H={H} slots={slots} spec={spec} raw={raw} pad={pad_rows} graph={graph} seed={seed}")
+    _say(f"recurrent B={B} S={S} H={H} slots={slots} spec={spec} raw={raw} pad={pad_rows} graph={graph} "
+         f"qk_norms={qk_norms} seed={seed}")
     g = gen(seed)
     T = B * S
     q, k, v, gg, beta = config_inputs(T, H, g)
+    if qk_norms:
+        # rows of norm 1e-3 .. 10 (log-uniform): the in-kernel x rsqrt(|x|^2 + 1e-6) is not the identity on them
+        for t in (q, k):
+            t.copy_((t.float() * torch.exp(torch.empty(T, H, 1).uniform_(np.log(1e-3), np.log(10.0),
+                                                                          generator=g))).bfloat16())
     pool = torch.randn(slots, H, D, D, generator=g) * 0.05
     perm = torch.randperm(slots - 1, generator=g)[: B * S] + 1
     idx = perm.view(B, S).to(torch.int32) if spec else perm[:B].to(torch.int32)
@@ -75,8 +85,7 @@ def _run_case(oracle, B, S, H, slots, seed, spec, raw=False, pad_rows=(), graph=
     ro, rpool, written = oracle.recurrent(f32(q), f32(k), f32(v), g_np, b_np, f32(pool), idx.numpy(),
                                           acc.numpy() if spec else None, precision=64)
     got_pool = dpool.cpu().numpy()
-    ex, rawe, rel = out_err(f32(out[0]), ro)
-    assert ex <= OUT_TOL, f"output excess {ex:.3e} (raw {rawe:.3e}, relL2 {rel:.3e})"
+    check_out(out[0], ro, f"recurrent B={B} S={S} H={H}", _cu_tokens(B, S))
     for r in sorted(set(written)):
         e = rel_frob(got_pool[r], rpool[r])
         assert e <= STATE_TOL, f"pool row {r}: relF {e:.3e}"
@@ -105,6 +114,13 @@ def test_spec_verify_padding_writes(oracle):
 def test_raw_gate_beta(oracle):
     _run_case(oracle, B=8, S=2, H=4, slots=32, seed=5, spec=True, raw=True)
     _run_case(oracle, B=8, S=1, H=4, slots=32, seed=6, spec=False, raw=True)
+
+
+def test_non_unit_qk_norms(oracle):
+    """q / k rows of norms 1e-3 .. 10: the decode form x rsqrt(|x|^2 + 1e-6) (reference.py:159-160) shrinks the small
+    ones below unit norm, which the oracle's decode form reproduces and the prefill clamp form would not."""
+    _run_case(oracle, B=16, S=1, H=4, slots=40, seed=8, spec=False, qk_norms=True)
+    _run_case(oracle, B=8, S=3, H=4, slots=40, seed=9, spec=True, qk_norms=True)
 
 
 def test_graph_capture_replay(oracle):
@@ -149,8 +165,7 @@ def test_graph_replay_new_indices_and_data(oracle):
         torch.cuda.synchronize()
         ro, rpool, written = oracle.recurrent(f32(q), f32(k), f32(v), f32(gg), f32(beta), f32(p0), ix.numpy(),
                                               precision=64)
-        ex, rawe, rel = out_err(f32(out[0]), ro)
-        assert ex <= OUT_TOL, f"replay {rep}: output excess {ex:.3e}"
+        check_out(out[0], ro, f"replay {rep}", _cu_tokens(B, 1))
         got = pool.cpu().numpy()
         for r in written:
             assert rel_frob(got[r], rpool[r]) <= STATE_TOL, f"replay {rep}: row {r}"
@@ -185,10 +200,9 @@ def test_spec_scratch_commit(oracle):
     # oracle: per-token states from the committed slot, then pool[slot] = state after token a-1
     S_in = f32(pool)[pslot.numpy()]
     from oracle import oracle as O
-    ro, steps = O.recurrent_core(O.l2norm_clamp(f32(q)), O.l2norm_clamp(f32(k)), f32(v), f32(gg), f32(beta), S_in,
+    ro, steps = O.recurrent_core(O.l2norm_rsqrt(f32(q)), O.l2norm_rsqrt(f32(k)), f32(v), f32(gg), f32(beta), S_in,
                                  D ** -0.5, precision=64)
-    ex, rawe, rel = out_err(f32(out[0]), ro)
-    assert ex <= OUT_TOL, f"output excess {ex:.3e}"
+    check_out(out[0], ro, "spec scratch", _cu_tokens(B, S))
     sc = scratch.cpu().numpy().reshape(B, S, H, D, D)
     for n in range(B):
         for t in range(S):

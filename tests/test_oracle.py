@@ -64,6 +64,27 @@ def test_norms(oracle):
     assert np.array_equal(oracle.l2norm_rsqrt(zero), zero)
 
 
+@pytest.mark.parametrize("c", [1e-3, 1e-7])
+def test_norm_forms_in_recurrences(oracle, c):
+    """One token, zero state, beta = 1, g = 0, q = k = c e_0: o = scale v (k^ . q^).  The prefill form
+    x / max(|x|, 1e-6) (reference.py:59-60) gives k^ . q^ = (c / max(c, 1e-6))^2; the decode form
+    x rsqrt(|x|^2 + 1e-6) (reference.py:159-160), which vLLM's fused_recurrent_kda and the decode kernels use, gives
+    c^2 / (c^2 + 1e-6).  At c = 1e-3 the two differ by 2x, so a recurrence on the wrong form fails."""
+    H, scale = 1, 0.25
+    x = np.zeros((1, H, D), np.float32)
+    x[..., 0] = c
+    v = np.random.default_rng(2).standard_normal((1, H, D)).astype(np.float32)
+    z = np.zeros((1, H, D), np.float32)
+    one = np.ones((1, H), np.float32)
+    pre = min(1.0, c / 1e-6) ** 2
+    dec = c * c / (c * c + 1e-6)
+    o_p, _ = oracle.prefill_plain(x, x, v, z, one, [0, 1], scale=scale, precision=64)
+    assert np.allclose(o_p, scale * v * pre, rtol=1e-5, atol=1e-12)
+    pool = np.zeros((2, H, D, D), np.float32)
+    o_d, _, _ = oracle.recurrent(x, x, v, z, one, pool, np.array([1]), scale=scale, precision=64)
+    assert np.allclose(o_d, scale * v * dec, rtol=1e-5, atol=1e-12)
+
+
 # ---------------------------------------------------------------------------------------------- recurrence pins
 @pytest.mark.parametrize("prec", [32, 64])
 def test_pure_decay_closed_form(oracle, prec):
@@ -398,7 +419,50 @@ def test_decode_full_conv_groups_taps_silu(oracle):
             assert np.allclose(got, expect(vt), rtol=1.6e-2, atol=1e-2), (spec, n)
 
 
-def test_config0_shapes(oracle):
+def test_decode_full_gated_rmsnorm(oracle):
+    """Gated RMSNorm pin (reference.py:172-175): y = bf16(o) rsqrt(mean(bf16(o)^2) + eps) norm_weight sigmoid(og).
+    The conv-orientation case above fixes o = SiLU(v_tap) / sqrt(128) (beta = 1, no decay, zero state, k^ . q^ = 1).
+    Here sigmoid(og) takes the exact values 1/2 (og = 0), 1 (og = 30) and ~0 (og = -30) across channels, the weight
+    is a per-channel ramp, and the history taps are small so that mean(o^2) ~ eps: dropping the gate or the weight,
+    moving eps outside the rsqrt or dropping it changes the result by >= 30 %."""
+    rng = np.random.default_rng(17)
+    H, slots, B = 1, 6, 3
+    dim = H * D
+    C = 3 * dim
+    w = np.zeros((3, 4, dim), np.float32)
+    w[0, 3] = 1.0
+    w[1, 3] = 1.0
+    w[2, 1] = 1.0                                             # v: window row 1 (history tap 1 in plain decode)
+    A_log = np.zeros(H, np.float32)
+    dt = np.zeros(dim, np.float32)
+    ssm = np.zeros((slots, H, D, D), np.float32)
+    conv = oracle.bf16_round((rng.standard_normal((slots, 3, C)) * 0.2).astype(np.float32))
+    x = oracle.bf16_round(rng.standard_normal((B, C)).astype(np.float32))
+    x[:, dim:2 * dim] = x[:, :dim]
+    gate_in = np.full((B, H, D), -100.0, np.float32)
+    beta_in = np.full((B, H), 30.0, np.float32)
+    og = np.tile(np.array([0.0, 30.0, -30.0, 0.0], np.float32), (B, dim // 4))
+    nw = np.linspace(0.25, 2.0, D).astype(np.float32)
+    idx = np.array([1, 3, 5])
+    sv = conv[idx, 1, 2 * dim:].astype(np.float64)
+    o = oracle.bf16_round(sv / (1.0 + np.exp(-sv)) / math.sqrt(D)).astype(np.float64)   # bf16(o)
+    ms = (o * o).mean(-1, keepdims=True)
+    eps = float(np.median(ms))
+    out, _, _, (ob, fac) = oracle.decode_full(x, conv, w, gate_in, beta_in, og, A_log, dt, nw, ssm, idx, None, eps,
+                                              -5.0, aux=True)
+    sig = 1.0 / (1.0 + np.exp(-og.astype(np.float64)))
+    expect = o / np.sqrt(ms + eps) * nw * sig
+    # the checker's view (bf16(o) and the per-element norm factor) matches the closed form as well
+    assert np.allclose(ob, o, rtol=8e-3, atol=0)
+    assert np.allclose(fac, nw * sig / np.sqrt(ms + eps), rtol=2e-2)
+    got = out.astype(np.float64)
+    scale = np.abs(expect).max()
+    assert np.allclose(got, expect, rtol=1.6e-2, atol=1e-2 * scale)
+    # the alternatives this must tell apart
+    for wrong in (o / np.sqrt(ms) * nw * sig, (o / np.sqrt(ms) + eps) * nw * sig, o / np.sqrt(ms + eps) * sig,
+                  o / np.sqrt(ms + eps) * nw):
+        assert np.abs(got - wrong).max() > 0.3 * scale
+
     """Config 0 (T = 1024, H = 4, zero initial state) runs and is finite; fp32 agrees with fp64."""
     q, k, v, gg, beta = config_inputs(1024, 4, gen(0))
     o32, f32_ = oracle.prefill_plain(f32(q), f32(k), f32(v), f32(gg), f32(beta), [0, 1024], precision=32)
