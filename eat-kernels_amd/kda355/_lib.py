@@ -113,6 +113,8 @@ def lib():
         L.kda355_prefill_workspace_bytes.restype = I64
         L.kda355_prefill_launch.argtypes = [ctypes.POINTER(KdaPrefillArgs), P]
         L.kda355_prefill_launch.restype = ctypes.c_int
+        L.kda355_prefill_launch_noalloc.argtypes = [ctypes.POINTER(KdaPrefillArgs), P]
+        L.kda355_prefill_launch_noalloc.restype = ctypes.c_int
         L.kda355_last_error.restype = ctypes.c_char_p
         L.kda355_version.restype = ctypes.c_int
         _lib = L
@@ -131,4 +133,8 @@ def check(rc: int, what: str):
 def exported_symbols():
     """Names declared in include/kda355.h that the library must export."""
     return ["kda355_recurrent_launch", "kda355_spec_commit_launch", "kda355_decode_launch", "kda355_prefill_plan",
-            "kda355_prefill_workspace_bytes", "kda355_prefill_launch", "kda355_last_error", "kda355_version"]
+            "kda355_prefill_workspace_bytes", "kda355_prefill_launch", "kda355_prefill_launch_noalloc",
+            "kda355_last_error", "kda355_version"]
+
+
+NOALLOC_SCRATCH_BYTES = 256 << 20  # KDA355_NOALLOC_SCRATCH_BYTES

@@ -143,7 +143,13 @@ def _launch(meta, q, k, v, gt, bt, out, flags, scale, lower_bound, A_log=None, d
         raise ValueError(f"kda355: meta was prepared for another layout (T/H {meta.T}/{meta.H} vs {T}/{H})")
     if meta.tables.device != dev:
         raise ValueError("kda355: meta was prepared for another device")
-    if workspace is None:
+    static = isinstance(workspace, str)
+    if static:
+        # kda355_prefill_launch_noalloc: the library's static device scratch, no allocation in the call
+        if workspace != "static":
+            raise ValueError("kda355: workspace must be a uint8 device tensor, None or 'static'")
+        workspace = None
+    elif workspace is None:
         workspace = torch.empty(max(meta.workspace_bytes, 256), dtype=torch.uint8, device=dev)
     elif workspace.numel() * workspace.element_size() < meta.workspace_bytes or workspace.device != dev:
         raise ValueError("kda355: workspace too small or on another device")
@@ -172,7 +178,10 @@ def _launch(meta, q, k, v, gt, bt, out, flags, scale, lower_bound, A_log=None, d
     a.flags = flags
     a.plan = ctypes.pointer(meta.plan)
     stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
-    _lib.check(_lib.lib().kda355_prefill_launch(ctypes.byref(a), stream), "prefill")
+    if static:
+        _lib.check(_lib.lib().kda355_prefill_launch_noalloc(ctypes.byref(a), stream), "prefill_noalloc")
+    else:
+        _lib.check(_lib.lib().kda355_prefill_launch(ctypes.byref(a), stream), "prefill")
 
 
 def _check_qkv(q, k, v):
@@ -297,7 +306,9 @@ def chunk_kda(q, k, v, g, beta, scale=None, initial_state=None, output_final_sta
     """fla chunk_kda plain call. q, k, v [1, T, H, 128] bf16; g [1, T, H, 128] (fp32 log-decay, or the raw gate with
     use_gate_in_kernel); beta [1, T, H] (fp32 activated, or logits with use_beta_sigmoid_in_kernel); initial_state
     [N, H, 128(V), 128(K)] fp32 or None; cu_seqlens [N+1] (None: one sequence).  meta: a plan(...) result for this
-    layout (skips the host read of cu_seqlens).  Returns (o [1, T, H, 128] bf16, final_state [N, H, 128, 128] fp32
+    layout (skips the host read of cu_seqlens).  workspace: a uint8 device tensor of >= meta.workspace_bytes, None
+    (allocated per call when the layout needs one), or "static" (kda355_prefill_launch_noalloc: the library's static
+    device scratch of 256 MiB, no allocation; calls on one GPU must not overlap).  Returns (o [1, T, H, 128] bf16, final_state [N, H, 128, 128] fp32
     or None).
 
     Serving keywords (the B200 contract, kda/b200/kda_b200.py:15-24):

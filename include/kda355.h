@@ -246,6 +246,18 @@ typedef struct KdaPrefillArgs {
 
 int kda355_prefill_launch(const KdaPrefillArgs* args, kda355_stream_t stream);
 
+/*
+ * kda355_prefill_launch without a caller workspace.  No counterpart in the reference: it is for callers that cannot
+ * allocate device memory (code under graph capture with no allocator at hand, tight serving loops, harnesses that
+ * forbid allocation).  args->workspace must be NULL; the workspace of split layouts comes from a static device array
+ * of KDA355_NOALLOC_SCRATCH_BYTES that every GPU the library runs on holds until the process ends, and a plan whose
+ * workspace_bytes exceeds it is rejected with KDA355_EINVAL (config-2-sized layouts need ~1 GB: use
+ * kda355_prefill_launch there).  The call allocates nothing.  Calls that overlap on one GPU share the array and
+ * race: serialize them (one stream).  Nothing in the array has to start at zero.
+ */
+#define KDA355_NOALLOC_SCRATCH_BYTES (256ull << 20)
+int kda355_prefill_launch_noalloc(const KdaPrefillArgs* args, kda355_stream_t stream);
+
 /* ------------------------------------------------------------------------------------------------ misc */
 
 /* Human-readable reason of the last KDA355_EINVAL / KDA355_ELAUNCH on the calling thread ("" if none). */
