@@ -4,6 +4,8 @@
     from kda355 import prefill_prepare, prefill                    # vLLM-ROCm Kimi serving prefill (paged pool)
     from kda355 import fused_recurrent_kda, spec_commit           # decode / speculative verify on a state pool
     from kda355 import decode                                      # vLLM-ROCm fused decode (conv + KDA + gated norm)
+    torch.ops.kda355.{fused_kda_decode, fused_kda_prefill, prefill, decode, fused_recurrent_kda, spec_commit}
+                                                                   # the same kernels as registered torch ops
 
 Every entry point runs the hand-written HIP kernels of libkda355.so (include/kda355.h).  There is no CPU or PyTorch
 fallback: calling on CPU tensors raises TypeError, and a missing library raises RuntimeError.
@@ -12,6 +14,7 @@ from ._lib import LIB_PATH, lib  # noqa: F401
 from .prefill import chunk_kda, kda_prefill, plan, prefill, prefill_prepare  # noqa: F401
 from .recurrent import fused_recurrent_kda, spec_commit  # noqa: F401
 from .decode import decode  # noqa: F401
+from . import ops  # noqa: F401  (registers torch.ops.kda355.*)
 
 __all__ = ["chunk_kda", "kda_prefill", "plan", "prefill", "prefill_prepare", "fused_recurrent_kda", "spec_commit", "decode",
            "lib", "LIB_PATH"]

@@ -46,6 +46,17 @@ def _slot_stride(t, per_slot):
 
 def decode(mixed_qkv, conv_state, conv_weight, gate, beta, out_gate, A_log, dt_bias, norm_weight, ssm_state,
            state_indices, num_accepted_tokens, cu_seqlens, norm_eps, lower_bound, out):
+    if not isinstance(cu_seqlens, torch.Tensor):
+        raise TypeError("kda355 decode: cu_seqlens must be a tensor")
+    return decode_batch(mixed_qkv, conv_state, conv_weight, gate, beta, out_gate, A_log, dt_bias, norm_weight,
+                        ssm_state, state_indices, num_accepted_tokens, cu_seqlens.numel() - 1, norm_eps, lower_bound,
+                        out)
+
+
+def decode_batch(mixed_qkv, conv_state, conv_weight, gate, beta, out_gate, A_log, dt_bias, norm_weight, ssm_state,
+                 state_indices, num_accepted_tokens, B, norm_eps, lower_bound, out):
+    """decode() with the batch size B given directly (only the length of cu_seqlens is ever used: every sequence has
+    the same S = T / B tokens)."""
     if not isinstance(mixed_qkv, torch.Tensor) or mixed_qkv.dim() != 2:
         raise ValueError("kda355 decode: mixed_qkv must be [T, 3 * H * 128]")
     dev = mixed_qkv.device
@@ -56,7 +67,7 @@ def decode(mixed_qkv, conv_state, conv_weight, gate, beta, out_gate, A_log, dt_b
         raise ValueError(f"kda355 decode: mixed_qkv width {C} is not 3 * H * 128")
     dim = C // 3
     H = dim // D
-    B = cu_seqlens.numel() - 1
+    B = int(B)
     spec = num_accepted_tokens is not None
     if B < 1 or T % B:
         raise ValueError(f"kda355 decode: T = {T} is not B x S for B = {B}")

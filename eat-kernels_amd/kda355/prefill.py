@@ -70,6 +70,32 @@ class PrefillMeta:
         """(pieces, split sequences): 0 pieces when no sequence is split."""
         return int(self.plan.num_pieces), int(self.plan.num_split)
 
+    def as_tensors(self):
+        """(plan, plan_table): the host plan as a CPU uint8 tensor (the KdaPrefillPlan bytes, then an int32 flag for
+        planned checkpoints and the sequence lengths as int64) and its device table -- the metadata tensors that the
+        torch.ops entry points take where vLLM's chunk op takes chunk_indices / chunk_offsets."""
+        head = bytes(self.plan) + np.array([int(self.any_ck), 0], np.int32).tobytes()
+        raw = head + np.ascontiguousarray(self.lens, np.int64).tobytes()
+        return torch.frombuffer(bytearray(raw), dtype=torch.uint8), self.tables
+
+    @classmethod
+    def from_tensors(cls, plan_bytes, plan_table):
+        """Inverse of as_tensors; checks that the pair belongs together as far as the bytes allow."""
+        n = ctypes.sizeof(_lib.KdaPrefillPlan)
+        if not isinstance(plan_bytes, torch.Tensor) or plan_bytes.dtype != torch.uint8 or plan_bytes.device.type != "cpu":
+            raise TypeError("kda355: plan must be the CPU uint8 tensor of PrefillMeta.as_tensors()")
+        if not isinstance(plan_table, torch.Tensor) or plan_table.dtype != torch.int32:
+            raise TypeError("kda355: plan_table must be the int32 table of PrefillMeta.as_tensors()")
+        raw = plan_bytes.contiguous().numpy().tobytes()
+        if len(raw) < n + 8:
+            raise ValueError("kda355: plan is too short to hold a prefill plan")
+        pl = _lib.KdaPrefillPlan.from_buffer_copy(raw[:n])
+        any_ck = int(np.frombuffer(raw[n:n + 4], np.int32)[0]) != 0
+        lens = np.frombuffer(raw[n + 8:], np.int64).copy()
+        if lens.size != pl.N or int(lens.sum()) != pl.T or plan_table.numel() != pl.table_words:
+            raise ValueError("kda355: plan and plan_table do not come from one PrefillMeta.as_tensors() call")
+        return cls(pl, plan_table, int(pl.H), int(pl.ck_every), any_ck, lens)
+
 
 def plan(cu_seqlens, num_heads, checkpoint_offsets=None, ck_every=0, device=None, num_cus=None):
     """Host-only schedule from the layout (never the data); one H2D copy of the table when device is a GPU.
