@@ -470,6 +470,21 @@ def cpu_baseline(inputs, lens, seconds, torch):
         if time.perf_counter() >= t_end or len(passes) >= 50:
             break
     med = sorted(passes)[len(passes) // 2]
+    # one thread on a bounded sample: the first sequence, all heads, the same recurrence
+    n0 = int(cun[1])
+    s_q, s_k = np.ascontiguousarray(qn[:n0]), np.ascontiguousarray(kn[:n0])
+    s_v, s_g, s_b = np.ascontiguousarray(vv[:n0]), np.ascontiguousarray(gg[:n0]), np.ascontiguousarray(bb[:n0])
+    s_cu, s_S0 = np.array([0, n0], np.int64), np.ascontiguousarray(S0[:1])
+    one = []
+    t_end = time.perf_counter() + seconds / 2
+    while True:
+        t0 = time.perf_counter()
+        qq, kk = O.l2norm_clamp(s_q), O.l2norm_clamp(s_k)
+        O.chains(qq, kk, s_v, s_g, s_b, s_cu, D ** -0.5, s_S0, precision=32, nthreads=1)
+        one.append(time.perf_counter() - t0)
+        if time.perf_counter() >= t_end or len(one) >= 20:
+            break
+    med1 = sorted(one)[len(one) // 2]
     model = ""
     try:
         for line in open("/proc/cpuinfo"):
@@ -481,7 +496,10 @@ def cpu_baseline(inputs, lens, seconds, torch):
     return {"value": T / med, "unit": "tok/s", "cores": threads, "kind": "port",
             "sample": f"the whole configuration-1 workload ({T} tokens x 32 heads, fp32 token recurrence of "
                       f"kda/mi350x/reference.py:85-91 restated in C, OpenMP over the 256 (sequence, head) chains), "
-                      f"{len(passes)} passes, median {med:.3f} s; host: {model}, nproc {os.cpu_count()}"}
+                      f"{len(passes)} passes, median {med:.3f} s; host: {model}, nproc {os.cpu_count()}",
+            "single_thread": {"value": n0 / med1, "unit": "tok/s", "cores": 1, "kind": "port",
+                              "sample": f"the first configuration-1 sequence ({n0} tokens x 32 heads), one thread, "
+                                        f"{len(one)} passes, median {med1:.3f} s"}}
 
 
 # ------------------------------------------------------------------------------------------------ main
