@@ -104,8 +104,8 @@ def _fused_kda_decode(x, weight, bias, conv_state, raw_g, raw_beta, A_log, dt_bi
         og2 = output_gate.view(T, H * D)
     except RuntimeError as e:
         raise ValueError(f"kda355 fused_kda_decode: out / output_gate must have dense rows ({e})") from None
-    _decode_batch(x, conv_state.transpose(1, 2), weight, raw_g[0], raw_beta[0], og2, A_log, dt_bias,
-                         norm_weight, state, state_indices, None, B, norm_eps, lower_bound, out2)
+    _decode_batch(x, conv_state.transpose(1, 2), weight, raw_g[0], raw_beta[0], og2, A_log, dt_bias, norm_weight,
+                  state, state_indices, None, B, norm_eps, lower_bound, out2)
 
 
 def _fused_kda_prefill(q, k, v, raw_g, raw_beta, A_log, dt_bias, out, cu_seqlens, scale, lower_bound,
@@ -117,7 +117,8 @@ def _fused_kda_prefill(q, k, v, raw_g, raw_beta, A_log, dt_bias, out, cu_seqlens
     sigmoid(beta) applied in the kernel.  State: either state_cache + state_indices + has_initial_state (read and
     written in place; initial_state / final_state must then be None) or the dense initial_state / final_state
     [N, H, 128, 128].  Checkpoints: checkpoint_offsets [N] (0 or a non-multiple of 64: none) into checkpoint_state,
-    at row checkpoint_state_indices[n] (< 0: none) or, without them, at row n."""
+    at row checkpoint_state_indices[n] (< 0: none) or, without them, at row n.  A given plan fixes the checkpoint
+    offsets (they are planned on the host): pass the plan made with the same offsets."""
     meta = _meta(plan, plan_table)
     dev, T, H = _prefill._check_qkv(q, k, v)
     ck = checkpoint_state is not None and checkpoint_offsets is not None
