@@ -312,8 +312,11 @@ def bench_fused_decode(kda, torch, dev, steps, warmup, H, B, S, flush=None, taps
         torch.cuda.synchronize()
         us = time_flushed_median(gr.replay, steps, torch, flush)
     state_bytes = B * H * D * D * 4 * (1 + S)
+    # per (sequence, head): the conv cache's 3 history taps read and its new taps written (3 x 384 bf16 each, 2 + S
+    # in spec mode), and per token the q|k|v row, gate, beta, out_gate and output
+    other_bytes = B * H * (3 * 768 + (2 + S if spec else 3) * 768 + S * (768 + 256 + 2 + 256 + 256))
     del raw, P
-    return dict(H=H, B=B, S=S, us=us, state_bytes=state_bytes)
+    return dict(H=H, B=B, S=S, us=us, state_bytes=state_bytes, other_bytes=other_bytes)
 
 
 # ------------------------------------------------------------------------------------------------ serving workloads
@@ -572,8 +575,10 @@ def main():
         for H, B, S, name in ((32, 256, 1, "configs[3] shape"), (96, 32, 8, "reference workload s8_h96_b32")):
             f = bench_fused_decode(kda355, torch, dev, args.steps, args.warmup, H, B, S)
             gbs = f["state_bytes"] / (f["us"] * 1e-6) / 1e9
+            all_gbs = (f["state_bytes"] + f["other_bytes"]) / (f["us"] * 1e-6) / 1e9
             rows.append({"workload": name, "H": H, "B": B, "S": S, "us_per_step": round(f["us"], 2),
-                         "state_GBs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)})
+                         "state_GBs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+                         "other_bytes": f["other_bytes"], "all_bytes_hbm_frac": round(all_gbs / HBM_PEAK_GBS, 4)})
             log(f"fused decode H={H} B={B} S={S}: {f['us']:.1f} us ({gbs:.0f} GB/s state traffic)")
         extra["fused_decode"] = {"config": "kda355.decode (vLLM contract: conv1d + SiLU, norms, gated delta rule, gated "
                                            "RMSNorm) on the vLLM page layout, HIP graph replay", "rows": rows}
