@@ -100,7 +100,7 @@ class PrefillMeta:
 def plan(cu_seqlens, num_heads, checkpoint_offsets=None, ck_every=0, device=None, num_cus=None):
     """Host-only schedule from the layout (never the data); one H2D copy of the table when device is a GPU.
     num_cus: CUs to fill (default: the device's); when the (sequence, head) chains alone leave CUs idle or the longest
-    chains would finish well after the rest, long sequences are split into pieces of >= 16 chunks (later pieces run
+    chains would finish well after the rest, long sequences are split into pieces of >= 2 chunks (later pieces run
     from a zero state carrying their transition; a scan and an output fixup complete them, with a workspace)."""
     cu = np.ascontiguousarray(torch.as_tensor(cu_seqlens).detach().cpu().numpy(), dtype=np.int64)
     N = cu.size - 1
@@ -120,11 +120,16 @@ def plan(cu_seqlens, num_heads, checkpoint_offsets=None, ck_every=0, device=None
     pin.num_cus = int(num_cus or 0)
     pl = _lib.KdaPrefillPlan()
     L = _lib.lib()
-    _lib.check(L.kda355_prefill_plan(ctypes.byref(pin), ctypes.byref(pl), None, 0), "prefill_plan")
-    tab = np.zeros(int(pl.table_words), np.int32)
-    _lib.check(L.kda355_prefill_plan(ctypes.byref(pin), ctypes.byref(pl), ctypes.c_void_p(tab.ctypes.data), tab.size),
-               "prefill_plan")
-    t = torch.from_numpy(tab)
+    # one planning pass in the common case: a table of this many words holds every layout up to a few hundred pieces;
+    # a larger one reports its size (table_words is set before the capacity check) and is planned again
+    cap = 8192 + 32 * (N + int(cu[-1]) // 64)
+    tab = np.zeros(cap, np.int32)
+    rc = L.kda355_prefill_plan(ctypes.byref(pin), ctypes.byref(pl), ctypes.c_void_p(tab.ctypes.data), cap)
+    if rc != 0 and int(pl.table_words) > cap:
+        tab = np.zeros(int(pl.table_words), np.int32)
+        rc = L.kda355_prefill_plan(ctypes.byref(pin), ctypes.byref(pl), ctypes.c_void_p(tab.ctypes.data), tab.size)
+    _lib.check(rc, "prefill_plan")
+    t = torch.from_numpy(tab[:int(pl.table_words)])
     if device is not None and torch.device(device).type == "cuda":
         t = t.to(device)
     any_ck = ck is not None and bool(np.any(ck > 0))
