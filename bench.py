@@ -22,6 +22,10 @@ The other configurations are reported beside it (never as `value`):
   plain        (opt-in, --configs ...,plain) the reference's 10 phase-1 plain prefill workloads at H = 12 through
                kda_prefill, timed like the reference (median of 50 flushed single calls, launch included) beside its
                published MI350X latencies
+  legacy       (opt-in, --configs ...,legacy) the reference eval's two phase-1 no-regression gates: the 10 plain
+               layouts through prefill() on a contiguous pool against recorded vLLM latencies, the 17 phase-1 decode
+               shapes on dense pools against recorded best-baseline latencies; metric mean(recorded / ours), beside
+               the reference's own readings of it
 
 Roofline: prefill is bound by HBM at these shapes (arithmetic intensity ~120 FLOP/B, below the bf16 ridge of ~312),
 so `roofline` is the HBM fraction of the prefill launch: compulsory bytes (q, k, v, out bf16; g fp32; beta fp32;
@@ -362,6 +366,26 @@ PLAIN_PREFILL = {
     "p_mixed": ([8192, 1024, 777, 512, 256, 130, 64, 17], 0.1062),
 }
 
+# The reference eval's phase-1 no-regression gates (kda/mi350x/benchmark/eval_kda_mi350x.py:979-1098): the 10 plain
+# prefill layouts through the serving prefill() with a contiguous state pool against recorded vLLM latencies (ms), and
+# the 17 phase-1 decode shapes (H, B, S) on dense pools against the recorded best-baseline latencies (us)
+# (kda/mi350x/workloads/legacy_{prefill,decode}_baseline_sota.json, MI350X).  The metric of each gate is
+# mean(recorded / ours); the reference's own readings are 2.808 (prefill) and 1.590 (decode)
+# (kda/mi350x/docs/HANDOVER.md:449-450).
+LEGACY_PREFILL_BASE_MS = {
+    "p_1x1k": 0.06292, "p_1x4k": 0.12216, "p_1x16k": 0.39876, "p_1x64k": 1.38945, "p_4x4k": 0.38048,
+    "p_8x2k": 0.33884, "p_16x1k": 0.31596, "p_32x512": 0.32024, "p_64x128": 0.19196, "p_mixed": 0.49144,
+}
+LEGACY_DECODE = {  # name: (H, B, S, recorded best-baseline us)
+    "d_k3_b1": (12, 1, 1, 16.28), "d_k3_b32": (12, 32, 1, 23.44), "d_k3_b128": (12, 128, 1, 54.44),
+    "s4_k3_b1": (12, 1, 4, 25.04), "s4_k3_b16": (12, 16, 4, 39.88), "s4_k3_b64": (12, 64, 4, 87.081),
+    "s8_k3_b1": (12, 1, 8, 32.48), "s8_k3_b16": (12, 16, 8, 58.361), "s8_k3_b64": (12, 64, 8, 147.521),
+    "d_glm16_b1": (16, 1, 1, 18.801), "d_glm16_b64": (16, 64, 1, 51.041), "d_glm16_b256": (16, 256, 1, 135.801),
+    "s6_glm16_b1": (16, 1, 6, 28.68), "s6_glm16_b16": (16, 16, 6, 53.681), "s6_glm16_b64": (16, 64, 6, 148.282),
+    "d_glm8_b128": (8, 128, 1, 51.48), "s6_glm8_b32": (8, 32, 6, 53.601),
+}
+LEGACY_REFERENCE_MEAN = {"prefill": 2.808, "decode": 1.590}
+
 
 def time_flushed_median(fn, reps, torch, flush):
     ts = []
@@ -420,6 +444,78 @@ def bench_serving_prefill(kda, torch, dev, H, seqs, reps, flush, seed):
     us = time_flushed_median(call, reps, torch, flush)
     del raw, P, big_out, ws
     return dict(us=us, T=T, N=N, pieces=meta.split[0])
+
+
+def bench_legacy_prefill(kda, torch, dev, lens, reps, flush):
+    """The phase-1 prefill gate's call: `kda355.prefill` on a contiguous state pool (sequence n in row n, every
+    sequence with an initial state), inputs drawn as eval_kda_mi350x.py:988-997 draws them (seed 0)."""
+    H, N, T = PLAIN_H, len(lens), sum(lens)
+    gen = torch.Generator(device=dev).manual_seed(0)
+    rn = lambda *sh, sc=1.0: torch.randn(*sh, generator=gen, device=dev) * sc  # noqa: E731
+    q, k, v, raw_g = rn(1, T, H, D).bfloat16(), rn(1, T, H, D).bfloat16(), rn(1, T, H, D).bfloat16(), rn(1, T, H, D).bfloat16()
+    raw_beta = rn(1, T, H).bfloat16()
+    A_log = torch.rand(H, generator=gen, device=dev) * 2 - 1
+    dt_bias = rn(H * D, sc=0.5)
+    pool = rn(N, H, D, D, sc=0.05)
+    cu_cpu = torch.tensor([0] + [sum(lens[:i + 1]) for i in range(N)], dtype=torch.int32)
+    cu = cu_cpu.to(dev)
+    si = torch.arange(N, dtype=torch.int32, device=dev)
+    hi = torch.ones(N, dtype=torch.bool, device=dev)
+    out = torch.empty(1, T, H, D, dtype=torch.bfloat16, device=dev)
+    meta = kda.prefill_prepare(cu_cpu, H, device=dev)
+    ws = torch.empty(max(meta.workspace_bytes, 256), dtype=torch.uint8, device=dev)
+
+    def call():
+        kda.prefill(q, k, v, raw_g, raw_beta, A_log, dt_bias, D ** -0.5, -5.0, pool, si, hi, cu, out, meta=meta,
+                    workspace=ws)
+
+    for _ in range(10):
+        call()
+    torch.cuda.synchronize()
+    us = time_flushed_median(call, reps, torch, flush)
+    del q, k, v, raw_g, pool, out, ws
+    return us
+
+
+def bench_legacy_decode(kda, torch, dev, name, H, B, S, reps, flush):
+    """The phase-1 decode gate's call: `kda355.decode` on dense pools, inputs drawn as eval_kda_mi350x.py:1045-1060
+    draws them (seed crc32(name)), captured in a HIP graph and replayed once per flushed measurement."""
+    import zlib
+    gen = torch.Generator(device=dev).manual_seed(zlib.crc32(name.encode()))
+    rn = lambda *sh, sc=1.0: torch.randn(*sh, generator=gen, device=dev) * sc  # noqa: E731
+    dim, T = H * D, B * S
+    taps = 3 if S == 1 else 2 + S
+    slots = 2 * B * S + 16
+    perm = torch.randperm(slots - 1, generator=gen, device=dev)[:B * S].int() + 1
+    si = perm if S == 1 else perm.view(B, S).contiguous()
+    acc = None if S == 1 else torch.randint(1, S + 1, (B,), generator=gen, device=dev, dtype=torch.int32)
+    mixed, conv = rn(T, 3 * dim).bfloat16(), rn(slots, taps, 3 * dim).bfloat16()
+    cw, gate, beta = rn(3, 4, dim, sc=0.4), rn(T, H, D).bfloat16(), rn(T, H).bfloat16()
+    og = rn(T, dim).bfloat16()
+    A_log = torch.rand(H, generator=gen, device=dev) * 2 - 1
+    dtb, nw, ssm = rn(dim, sc=0.5), 1 + rn(D, sc=0.1), rn(slots, H, D, D, sc=0.05)
+    cu = torch.arange(0, T + 1, S, dtype=torch.long, device=dev)
+    out = torch.empty(T, dim, dtype=torch.bfloat16, device=dev)
+
+    def call():
+        kda.decode(mixed, conv, cw, gate, beta, og, A_log, dtb, nw, ssm, si, acc, cu, 1e-5, -5.0, out)
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(3):
+            call()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr):
+        call()
+    for _ in range(5):
+        gr.replay()
+    torch.cuda.synchronize()
+    us = time_flushed_median(gr.replay, reps, torch, flush)
+    del gr, ssm, conv
+    return us
 
 
 def bench_plain_prefill(kda, torch, dev, lens, reps, flush, seed):
@@ -619,6 +715,26 @@ def main():
                                             "included (kda/mi350x_plain/bench.py:120-138)",
                                   "mean_ratio": round(sum(x["ratio"] for x in rows) / len(rows), 3),
                                   "geomean_ratio": round(gm([x["ratio"] for x in rows]), 3), "rows": rows}
+
+    if "legacy" in cfgs:  # opt-in: the reference eval's phase-1 no-regression gates, its metric mean(recorded / ours)
+        prows, drows = [], []
+        for name, base_ms in LEGACY_PREFILL_BASE_MS.items():
+            us = bench_legacy_prefill(kda355, torch, dev, PLAIN_PREFILL[name][0], max(args.steps, 50), flush)
+            prows.append({"workload": name, "us": round(us, 2), "recorded_vllm_us": round(base_ms * 1e3, 2),
+                          "vs_base": round(base_ms * 1e3 / us, 3)})
+            log(f"legacy prefill {name}: {us:.1f} us (recorded vLLM {base_ms * 1e3:.1f} us)")
+        for name, (H, B, S, base) in LEGACY_DECODE.items():
+            us = bench_legacy_decode(kda355, torch, dev, name, H, B, S, max(args.steps, 100), flush)
+            drows.append({"workload": name, "H": H, "B": B, "S": S, "us": round(us, 2), "recorded_best_baseline_us": base,
+                          "vs_base": round(base / us, 3)})
+            log(f"legacy decode {name}: {us:.2f} us (recorded best baseline {base} us)")
+        extra["legacy"] = {
+            "method": "the reference eval's phase-1 gates (eval_kda_mi350x.py:979-1098): single calls / graph replays "
+                      "after a 512 MiB cache flush, median; metric mean(recorded / ours)",
+            "prefill_mean_vs_base": round(sum(x["vs_base"] for x in prows) / len(prows), 3),
+            "decode_mean_vs_base": round(sum(x["vs_base"] for x in drows) / len(drows), 3),
+            "reference_mean_vs_base": LEGACY_REFERENCE_MEAN, "floors": {"prefill": 0.932, "decode": 1.5},
+            "prefill_rows": prows, "decode_rows": drows}
 
     cpu = None
     if args.cpu_seconds > 0:

@@ -25,6 +25,12 @@ constexpr int DC_THREADS = WK_THREADS;
 constexpr int DC_MAX_S = 16;
 constexpr int DC_CH = 3 * D;  // conv channels of one head: q | k | v
 constexpr int64_t DC_SLICE_CUS = 256;  // a launch splits each state while the slices still fit one per CU (MI355X)
+// Streaming stores from this many bytes of written state per launch.  Timed as the reference times decode (one graph
+// replay after a 512 MiB cache flush, which is also what a layer's decode sees in a model of many layers: its pool rows
+// were last touched a whole step earlier), streaming stores gain 1.5-3.5 % from 268 MB of writes up (d_glm16_b256
+// 117.6 -> 115.8 us, s6_glm16_b64 105 -> 101.6 us, s8_h12_b64 102.7 -> 100.5 us) and lose below (s8_h12_b32, 201 MB:
+// 56.6 -> 60.2 us; s8_h96_b1: 27.3 -> 33.1 us).
+constexpr long long DC_STREAM_BYTES = 256ll << 20;
 
 struct DecParams {
     const uint16_t* x;        // mixed_qkv [T, 3 * dim] bf16, row stride x_rs
@@ -437,16 +443,16 @@ extern "C" int kda355_decode_launch(const KdaDecodeArgs* a, kda355_stream_t stre
     const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const size_t lds = ((size_t)(4 + a->S) * DC_CH + (size_t)a->S * (2 * D + 18)) * sizeof(float) +
                        (size_t)(3 + a->S) * DC_CH * sizeof(uint16_t);
-    // streaming stores when the launch writes more state than the MALL holds (WK_STREAM_BYTES)
-    const bool nt = (long long)a->B * (spec ? a->S : 1) * a->H * D * D * 4 > WK_STREAM_BYTES;
-    // small launches split each state over 4 workgroups (32 rows each) while the slices fit one per CU, so that more
-    // CUs walk and each token's step is shorter; the gated RMSNorm then runs as a second kernel.  (Halves of 64 rows
-    // for launches of up to 128 pairs measured no faster than whole states: s8_h96_b1 27.5 against 27.1 us.)
+    const bool nt = (long long)a->B * (spec ? a->S : 1) * a->H * D * D * 4 >= DC_STREAM_BYTES;
+    // small multi-token launches split each state over 4 workgroups (32 rows each) while the slices fit one per CU, so
+    // that more CUs walk and each token's step is shorter; the gated RMSNorm then runs as a second kernel.  (Halves of
+    // 64 rows for launches of up to 128 pairs measured no faster than whole states: s8_h96_b1 27.5 against 27.1 us.)
+    // A single-token launch keeps whole states: its one step is short, and the second kernel cost more than slicing
+    // saved (d_k3_b1 17.0 -> 15.8 us, d_glm16_b1 17.0 -> 15.9 us unsliced).
     const int64_t pairs = (int64_t)a->B * a->H;
-    const int np = (!nt && 4 * pairs <= DC_SLICE_CUS) ? 2 : 8;
+    const int np = (!nt && a->S > 1 && 4 * pairs <= DC_SLICE_CUS) ? 2 : 8;
     void (*kernel)(DecParams) =
-        np == 2 ? (spec ? decode_kernel<true, false, false, 2>
-                        : a->S == 1 ? decode_kernel<false, true, false, 2> : decode_kernel<false, false, false, 2>)
+        np == 2 ? (spec ? decode_kernel<true, false, false, 2> : decode_kernel<false, false, false, 2>)
         : spec ? (nt ? decode_kernel<true, false, true, 8> : decode_kernel<true, false, false, 8>)
         : a->S == 1 ? (nt ? decode_kernel<false, true, true, 8> : decode_kernel<false, true, false, 8>)
                     : (nt ? decode_kernel<false, false, true, 8> : decode_kernel<false, false, false, 8>);

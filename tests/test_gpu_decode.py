@@ -198,10 +198,11 @@ def test_plain_decode_padding_slot(oracle):
 
 
 def test_sliced_decode_dead_rows_stay_zero(oracle):
-    """Launches of at most 64 (sequence, head) pairs split each state over 4 workgroups and finish the gated RMSNorm
-    in a second kernel.  Dead sequences (padding read or conv row) with NaN out_gate rows and negative norm weights:
-    their output rows stay +0, as in the whole-state path."""
-    _run(oracle, B=6, S=1, H=2, seed=15, spec=False, pad=[(1,), (4,)], hostile_dead=True)
+    """Multi-token launches of at most 64 (sequence, head) pairs split each state over 4 workgroups and finish the
+    gated RMSNorm in a second kernel.  Dead sequences (padding read or conv row) with NaN out_gate rows and negative
+    norm weights: their output rows stay +0, as in the whole-state path (single-token launches, below)."""
+    _run(oracle, B=6, S=2, H=2, seed=15, spec=False, pad=[(1,), (4,)], hostile_dead=True)
+    _run(oracle, B=6, S=1, H=2, seed=17, spec=False, pad=[(1,), (4,)], hostile_dead=True)
     _run(oracle, B=6, S=3, H=2, seed=16, spec=True, pad=[(2, 0), (3, 1)], hostile_dead=True)
 
 
