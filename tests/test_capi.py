@@ -266,3 +266,16 @@ def test_decode_rejects_host_tensors():
                       t(B, H, 128, dtype=torch.bfloat16), t(B, H, dtype=torch.bfloat16), t(B, dim, dtype=torch.bfloat16),
                       t(H), t(dim), t(128), t(4, H, 128, 128), t(B, dtype=torch.int32), None,
                       torch.arange(B + 1, dtype=torch.int32), 1e-5, -5.0, t(B, dim, dtype=torch.bfloat16))
+
+
+def test_unsupported_forms_raise_before_any_device_work():
+    """Forms the kernels do not implement raise ValueError up front (no fallback): the K-major state layout of fla's
+    chunk_kda (state_v_first=False) and the non-in-place final state of fused_recurrent_kda."""
+    import pytest
+    import torch
+    import kda355
+    x = torch.zeros(1, 4, 2, 128, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="value-first"):
+        kda355.chunk_kda(x, x, x, torch.zeros(1, 4, 2, 128), torch.zeros(1, 4, 2), state_v_first=False)
+    with pytest.raises(ValueError, match="in-place"):
+        kda355.fused_recurrent_kda(x, x, x, torch.zeros(1, 4, 2, 128), torch.zeros(1, 4, 2), inplace_final_state=False)

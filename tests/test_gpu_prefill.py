@@ -131,6 +131,37 @@ def test_kda_prefill_raw_gates(oracle, gates):
         assert rel_frob(f32(fin[n]), rf[n]) <= STATE_TOL, f"gates={gates} seq {n}"
 
 
+def test_chunk_kda_gate_and_beta_in_kernel(oracle):
+    """The fla keyword form of the in-kernel gate: chunk_kda(..., use_gate_in_kernel=True,
+    use_beta_sigmoid_in_kernel=True, A_log=, dt_bias=, lower_bound=) runs the kernel kda_prefill runs (bit for bit) and
+    matches the oracle; the gate may come in fp32 (converted to the kernel's bf16 raw form)."""
+    kda = _kda()
+    H, lens = 4, [700, 64, 129]
+    _say("chunk_kda gate and beta in the kernel")
+    g = gen(31)
+    T = sum(lens)
+    q, k, v, raw_g, raw_b, A_log, dt_bias = _raw_inputs(g, T, H)
+    h0 = torch.randn(len(lens), H, D, D, generator=g) * 0.25
+    cu = torch.tensor(_cu(lens), dtype=torch.int64).to(DEV)
+    args = (q[None].to(DEV), k[None].to(DEV), v[None].to(DEV))
+    o1, f1 = kda.chunk_kda(*args, raw_g[None].to(DEV), raw_b[None].to(DEV), initial_state=h0.to(DEV), cu_seqlens=cu,
+                           use_gate_in_kernel=True, use_beta_sigmoid_in_kernel=True, A_log=A_log.to(DEV),
+                           dt_bias=dt_bias.to(DEV), lower_bound=-5.0)
+    o2, f2 = kda.chunk_kda(*args, raw_g[None].float().to(DEV), raw_b[None].to(DEV), initial_state=h0.to(DEV),
+                           cu_seqlens=cu, use_gate_in_kernel=True, use_beta_sigmoid_in_kernel=True,
+                           A_log=A_log.to(DEV), dt_bias=dt_bias.to(DEV), lower_bound=-5.0)
+    o3, f3 = kda.kda_prefill(*args, raw_g[None].to(DEV), raw_b[None].to(DEV), A_log.to(DEV), dt_bias.to(DEV),
+                             h0.to(DEV), cu, lower_bound=-5.0)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o3) and torch.equal(f1, f3), "chunk_kda's keyword form and kda_prefill differ"
+    assert torch.equal(o1, o2) and torch.equal(f1, f2), "an fp32 raw gate holding bf16 values changed the result"
+    qn, kn, vf, gl, bt = _oracle_gated(oracle, q, k, v, raw_g, raw_b, A_log, dt_bias)
+    ro, rf, _ = oracle.chains(qn, kn, vf, gl, bt, _cu(lens), D ** -0.5, f32(h0), precision=64)
+    _check_out(o1[0], ro, "chunk_kda in-kernel gate", _cu(lens))
+    for n in range(len(lens)):
+        assert rel_frob(f32(f1[n]), rf[n]) <= STATE_TOL, f"seq {n}"
+
+
 def _pages(slots, H, taps, g):
     """vLLM hybrid page layout (kda/mi350x/CONTRACT.md:60-67): conv state then SSM state per padded page."""
     dim = H * D

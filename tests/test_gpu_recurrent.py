@@ -230,3 +230,46 @@ def test_errors_raise():
         kda.fused_recurrent_kda(q, q, q, gg, beta, initial_state=pool, cu_seqlens=cu, ssm_state_indices=idx[::2])
     with pytest.raises(TypeError):
         kda.fused_recurrent_kda(q, q, q, gg, beta, initial_state=pool, cu_seqlens=cu, ssm_state_indices=idx.cpu())
+
+
+@pytest.mark.parametrize("spec", [False, True])
+def test_slot0_live_when_not_reserved(oracle, spec):
+    """slot0_reserved=False makes slot 0 an ordinary pool row (read and written like any other); rows < 0 stay padding.
+    Checked against the oracle's reserved-slot-0 semantics on the pool shifted by one row (kernel slot s = oracle
+    slot s + 1, so the oracle's padding slot 0 is the kernel's -1)."""
+    kda = _kda()
+    B, S, H, slots = (6, 3, 2, 24) if spec else (8, 1, 2, 16)
+    _say(f"recurrent slot0 live spec={spec} B={B} S={S}")
+    g = gen(40 + spec)
+    T = B * S
+    q, k, v, gg, beta = config_inputs(T, H, g)
+    pool = torch.randn(slots, H, D, D, generator=g) * 0.05
+    perm = torch.randperm(slots, generator=g)[:B * S]
+    perm[perm == 0] = perm[0].item()
+    perm[0] = 0  # slot 0 is used
+    idx = perm.view(B, S).to(torch.int32) if spec else perm[:B].to(torch.int32)
+    if spec:
+        idx[B - 1, 1] = -1  # a padding write row
+    else:
+        idx[B - 1] = -1     # a padding sequence
+    acc = torch.randint(1, S + 1, (B,), generator=g, dtype=torch.int32) if spec else None
+    dev = torch.device("cuda", 0)
+    dpool = pool.to(dev)
+    cu = torch.arange(0, T + 1, S, dtype=torch.int32, device=dev)
+    out, _ = kda.fused_recurrent_kda(q[None].to(dev), k[None].to(dev), v[None].to(dev), gg[None].to(dev),
+                                     beta[None].to(dev), initial_state=dpool, cu_seqlens=cu,
+                                     ssm_state_indices=idx.to(dev),
+                                     num_accepted_tokens=acc.to(dev) if spec else None, slot0_reserved=False)
+    torch.cuda.synchronize()
+    pool_o = np.concatenate([np.zeros((1, H, D, D), np.float32), f32(pool)])
+    ro, rpool, written = oracle.recurrent(f32(q), f32(k), f32(v), f32(gg), f32(beta), pool_o, idx.numpy() + 1,
+                                          acc.numpy() if spec else None, precision=64)
+    assert 1 in set(written), "the oracle must write the kernel's slot 0 (its row 1)"
+    check_out(out[0], ro, f"recurrent slot0 live spec={spec}", _cu_tokens(B, S))
+    got = dpool.cpu().numpy()
+    for r in sorted(set(written)):
+        e = rel_frob(got[r - 1], rpool[r])
+        assert e <= STATE_TOL, f"pool row {r - 1}: relF {e:.3e}"
+    keep = np.ones(slots, bool)
+    keep[[r - 1 for r in set(written)]] = False
+    assert np.array_equal(got[keep], f32(pool)[keep]), "rows outside the written set changed"
