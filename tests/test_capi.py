@@ -279,3 +279,25 @@ def test_unsupported_forms_raise_before_any_device_work():
         kda355.chunk_kda(x, x, x, torch.zeros(1, 4, 2, 128), torch.zeros(1, 4, 2), state_v_first=False)
     with pytest.raises(ValueError, match="in-place"):
         kda355.fused_recurrent_kda(x, x, x, torch.zeros(1, 4, 2, 128), torch.zeros(1, 4, 2), inplace_final_state=False)
+
+
+def test_operator_helpers_report_the_design():
+    """The reference serving module's operator helpers (kernel.py:113-209) exist with its return shapes and report
+    what this build's design implies: no relay faults, no decode workspaces to heal, no range-guard switch."""
+    import warnings
+    import pytest
+    import kda355
+    h = kda355.prefill_health()
+    assert h["ok"] is True and h["faults"] == [] and set(h) == {"ok", "relay", "relay_state", "serial", "faults"}
+    d = kda355.decode_health(heal=True)
+    assert d["ok"] is True and d["ghost_events"] == 0
+    assert kda355.decode_warmup()["library"].endswith("libkda355.so")
+    prev = kda355.decode_cotenant_mode("lds_free")
+    assert kda355.decode_cotenant_mode(prev) == "lds_free"
+    with pytest.raises(ValueError):
+        kda355.decode_cotenant_mode("bogus")
+    assert kda355.prefill_range_guard() is False
+    with warnings.catch_warnings(record=True) as w:
+        warnings.simplefilter("always")
+        assert kda355.prefill_range_guard(True) is False
+    assert any(issubclass(x.category, RuntimeWarning) for x in w)
