@@ -57,7 +57,7 @@ constexpr int LDS_C = 68608;
 constexpr int LDS_W = 102400;
 constexpr int LDS_AQ = 119808;
 constexpr int LDS_AK = 129024;
-constexpr int LDS_UNUSED = 138240;  // 4352 bytes
+constexpr int LDS_GM = 138240;      // the gate cumsum's block middle rows 16 I + 7 [4][128] fp32 (2 KiB; 2304 bytes free)
 constexpr int LDS_F = 142592;
 constexpr int LDS_WT = 151808;
 constexpr int LDS_BETA = 153856;
@@ -325,6 +325,7 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
     float* sL = reinterpret_cast<float*>(lds + LDS_L);       // A_kk diagonal blocks, column-major [4][16][20]
     float* sF = reinterpret_cast<float*>(lds + LDS_F);       // per-channel factors [18][128]
     float* sWt = reinterpret_cast<float*>(lds + LDS_WT);     // segment totals of the gate cumsum [4][128]
+    float* sGM = reinterpret_cast<float*>(lds + LDS_GM);     // the cumsum's block middle rows 16 I + 7 [4][128]
     float* sBeta = reinterpret_cast<float*>(lds + LDS_BETA);
     float* sDT = reinterpret_cast<float*>(lds + LDS_DT);
 
@@ -492,12 +493,14 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
 #pragma unroll
             for (int i = 0; i < 16; ++i) sG[(16 * s + i) * RS32 + swz(c)] = x[i];
             sWt[s * 128 + c] = x[15];
+            sGM[s * 128 + c] = x[7];  // the factors' reference row of block s, kept apart so P2 can overwrite sG
         }
         lds_barrier();
-        // ================= P2: element factors (raw threads) and block factors (channel threads)
-        float kfi[16];
+        // ================= P2: element factors (raw threads) and block factors (channel threads).  The block middle
+        // rows and segment totals come from sGM / sWt, so each raw thread reads only its own gate row from sG and can
+        // overwrite that row with k^ fi in place (no other thread reads it in this phase).
         {
-            float qf[16], kf[16], qfi[16], kfj[16];
+            float qf[16], kf[16];
             {
                 const u32x4 a[2] = {nx.q[0], nx.q[1]}, b[2] = {nx.k[0], nx.k[1]};
                 unpack16(a, qf);
@@ -507,37 +510,36 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
 #pragma unroll
                 for (int c = 0; c < 16; ++c) { kf[c] *= rk; qf[c] *= rq; }
             }
-            const int I = r >> 4, mr = 16 * I + 7;
+            const int I = r >> 4;
+            // block i of the row: its gate values are read before its k^ fi overwrites them (one thread, in order)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const f32x4 a = *reinterpret_cast<const f32x4*>(&sG[r * RS32 + 16 * cb + 4 * (i ^ (cb >> 1))]);
-                const f32x4 b = *reinterpret_cast<const f32x4*>(&sG[mr * RS32 + 16 * cb + 4 * (i ^ (cb >> 1))]);
+                const int o = r * RS32 + 16 * cb + 4 * (i ^ (cb >> 1));
+                const f32x4 a = *reinterpret_cast<const f32x4*>(&sG[o]);
+                const f32x4 b = *reinterpret_cast<const f32x4*>(&sGM[I * 128 + 16 * cb + 4 * i]);
+                f32x4 kfi, kfj, qfi;
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     const int c = 4 * i + j;
                     const float d = a[j] - b[j];  // Gamma_r - Gamma_m (the segment offset cancels)
                     const float fi = exp2_(d), fj = exp2_(-d);
-                    kfi[c] = kf[c] * fi;
-                    kfj[c] = kf[c] * fj;
-                    qfi[c] = qf[c] * fi;
+                    kfi[j] = kf[c] * fi;
+                    kfj[j] = kf[c] * fj;
+                    qfi[j] = qf[c] * fi;
                 }
-            }
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                *reinterpret_cast<f32x4*>(&sQA[r * RS32 + 16 * cb + 4 * (i ^ (cb >> 1))]) =
-                    f32x4{qfi[4 * i], qfi[4 * i + 1], qfi[4 * i + 2], qfi[4 * i + 3]};
-                *reinterpret_cast<f32x4*>(&sKB[r * RS32 + 16 * cb + 4 * (i ^ (cb >> 1))]) =
-                    f32x4{kfj[4 * i], kfj[4 * i + 1], kfj[4 * i + 2], kfj[4 * i + 3]};
+                *reinterpret_cast<f32x4*>(&sQA[o]) = qfi;
+                *reinterpret_cast<f32x4*>(&sKB[o]) = kfj;
+                *reinterpret_cast<f32x4*>(&sKA[o]) = kfi;
             }
         }
         {
             const int c = tid & 127, qd = tid >> 7;
             const float o1 = sWt[c], o2 = o1 + sWt[128 + c], o3 = o2 + sWt[256 + c];
-            float gr[8];  // Gamma at rows 8w' + 7
+            float gr[8];  // Gamma at rows 8 i + 7: block middles (sGM) and segment ends (sWt), plus the earlier segments
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 const float off = (i < 2) ? 0.f : (i < 4) ? o1 : (i < 6) ? o2 : o3;
-                gr[i] = sG[(8 * i + 7) * RS32 + swz(c)] + off;
+                gr[i] = ((i & 1) ? sWt[(i >> 1) * 128 + c] : sGM[(i >> 1) * 128 + c]) + off;
             }
 #pragma unroll
             for (int f = 0; f < F_ROWS; ++f) {  // unrolled: gr[] is indexed by constants only (stays in registers)
@@ -561,12 +563,6 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
                 sF[f * 128 + c] = exp2_(x);
             }
         }
-        lds_barrier();
-        // ================= P3: k^ fi over the (now unused) gate rows
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            *reinterpret_cast<f32x4*>(&sKA[r * RS32 + 16 * cb + 4 * (i ^ (cb >> 1))]) =
-                f32x4{kfi[4 * i], kfi[4 * i + 1], kfi[4 * i + 2], kfi[4 * i + 3]};
         lds_barrier();
         // ================= P4: Gram tiles
         if (w < 4) {
