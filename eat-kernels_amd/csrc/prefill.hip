@@ -682,7 +682,9 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
                 }
             }
         }
-        lds_barrier();
+        // no barrier here: the reads below touch only the raw v staging and the thread's own q^ fi / k^ fj rows, which
+        // the Gram phase neither writes nor overwrites; the barrier before the layouts orders every Gram read of
+        // regions B and C before they are rewritten
         // ================= P5: Q~, Kd^T, beta v into their walk layouts (raw threads)
         // The initial state loads (issued in the prologue) complete here, before any next-chunk row is in flight: an
         // empty use of S makes the compiler's wait for them fall at this point, where in every later chunk only the
