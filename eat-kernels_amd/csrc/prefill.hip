@@ -316,10 +316,10 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
     float* sKA = sG;
     float* sQA = reinterpret_cast<float*>(lds + LDS_B);      // q^ fi
     half_t* sQt = reinterpret_cast<half_t*>(lds + LDS_B);    // Q~ (channels permuted)
-    half_t* sBV = reinterpret_cast<half_t*>(lds + LDS_BV);   // beta v
     float* sKB = reinterpret_cast<float*>(lds + LDS_C);      // k^ fj
     half_t* sKd = reinterpret_cast<half_t*>(lds + LDS_C);    // Kd^T (tokens permuted)
-    half_t* sW = reinterpret_cast<half_t*>(lds + LDS_W);     // W (channels permuted)
+    half_t* sW = reinterpret_cast<half_t*>(lds + LDS_BV);    // W (channels permuted), in region B's upper half
+    const uint16_t* sV = reinterpret_cast<const uint16_t*>(lds + LDS_W);  // this chunk's raw v rows (bf16)
     half_t* sAq = reinterpret_cast<half_t*>(lds + LDS_AQ);   // A_qk (columns permuted)
     half_t* sAk = reinterpret_cast<half_t*>(lds + LDS_AK);   // -A_kk off-diagonal blocks, T_II diagonal blocks
     float* sL = reinterpret_cast<float*>(lds + LDS_L);       // A_kk diagonal blocks, column-major [4][16][20]
@@ -694,12 +694,7 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
         for (int dt = 0; dt < 8; ++dt) asm volatile("" : "+v"(S[dt]));
         // the next chunk's q, k rows: issued here, consumed at the next P0 (their registers are free during P1..P4)
         if (cl + 1 < nch) load_row_qk(p, h, t0 + 64, min(64, len - 64 * (cl + 1)), r, cb, nx);
-        float qfi[16], kfj[16], vf[16];
-        {
-            const u32x4* vs = reinterpret_cast<const u32x4*>(lds + LDS_W + r * (2 * RS16) + 32 * cb);
-            const u32x4 a[2] = {vs[0], vs[1]};
-            unpack16(a, vf);
-        }
+        float qfi[16], kfj[16];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const f32x4 a = *reinterpret_cast<const f32x4*>(&sQA[r * RS32 + 16 * cb + 4 * (i ^ (cb >> 1))]);
@@ -727,16 +722,10 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
                 const float y = sF[(F_Y + I) * 128 + 16 * cb + e];
                 sKd[(16 * cb + (e ^ cb)) * RS16S + pr] = (half_t)(kfj[e] * y);
             }
-            const float b = sBeta[r];
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                f16x8 o;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) o[e] = (half_t)(b * vf[8 * i + e]);
-                *reinterpret_cast<f16x8*>(&sBV[r * RS16 + 16 * cb + 8 * i]) = o;
-            }
         }
-        lds_barrier();
+        // no barrier here: the solve reads k^ fi (region A), the raw v rows, -A_kk / T_II, the factors and beta, none
+        // of which the layouts above write; it writes W into region B's upper half, whose last reader (the operand
+        // reads before the layouts) passed the barrier above.  The walk reads the layouts after the solve's barrier.
         // ================= P6: W and U by block forward substitution (wave w: channel / value tile w)
         if (cl + 1 < nch) load_row_vb(p, h, t0 + 64, min(64, len - 64 * (cl + 1)), r, cb, RB, nx);
         f32x4 Ur[4];
@@ -751,7 +740,7 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
                 for (int e = 0; e < 4; ++e) {
                     const int rw = 16 * I + 4 * g + e;
                     aw[e] = sBeta[rw] * sKA[rw * RS32 + swz(c)] * xI;
-                    au[e] = (float)sBV[rw * RS16 + c];
+                    au[e] = sBeta[rw] * bf2f(sV[rw * RS16 + c]);  // beta v straight from the raw v row
                 }
 #pragma unroll
                 for (int J = 0; J < I; ++J) {
