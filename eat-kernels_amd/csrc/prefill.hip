@@ -242,17 +242,6 @@ __device__ __forceinline__ void unpack16(const u32x4 (&w)[2], float (&f)[16]) {
         }
 }
 
-// The staged output row slice of raw thread (r, cb): 16 bf16 values in the first half of its 64-byte slot of region A.
-__device__ __forceinline__ void store_out_slot(const PfParams& p, int h, int t0, int L, int r, int cb,
-                                               const unsigned char* lds) {
-    if (r < L) {
-        const u32x4* so = reinterpret_cast<const u32x4*>(lds + r * 528 + 64 * cb);
-        u32x4* dst = reinterpret_cast<u32x4*>(p.out + ((int64_t)t0 + r) * p.out_rs + (int64_t)h * D + 16 * cb);
-        dst[0] = so[0];
-        dst[1] = so[1];
-    }
-}
-
 // V-major state rows of this lane: v = 16w + m, k = 16dt + 4g .. + 3
 __device__ __forceinline__ void store_state(float* dst, const f32x4 (&S)[8], int w, int g, int m) {
     float* row = dst + (16 * w + m) * D + 4 * g;
@@ -466,21 +455,11 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
             rq = __builtin_amdgcn_rcpf(fmaxf(sqrtf(sq), 1e-6f));
             rk = __builtin_amdgcn_rcpf(fmaxf(sqrtf(sk), 1e-6f));
         }
-        // The previous chunk's staged output is read from this thread's slot before the gate overwrites it and is
-        // stored after every prefetched register was consumed and before the next loads are issued, so no wait for
-        // the prefetch ever covers the stores.
-        const u32x4 o0 = *reinterpret_cast<const u32x4*>(lds + r * 528 + 64 * cb);
-        const u32x4 o1 = *reinterpret_cast<const u32x4*>(lds + r * 528 + 64 * cb + 16);
 #pragma unroll
         for (int i = 0; i < 4; ++i)
             *reinterpret_cast<f32x4*>(&sG[r * RS32 + 16 * cb + 4 * (i ^ (cb >> 1))]) =
                 f32x4{gv[4 * i], gv[4 * i + 1], gv[4 * i + 2], gv[4 * i + 3]};
         if (cb == 0) sBeta[r] = bt;
-        if (cl > 0) {  // the previous chunk was a full one
-            u32x4* dst = reinterpret_cast<u32x4*>(p.out + ((int64_t)t0 - 64 + r) * p.out_rs + (int64_t)h * D + 16 * cb);
-            dst[0] = o0;
-            dst[1] = o1;
-        }
         lds_barrier();
         // ================= P1: gate cumsum inside 16-row segments
         {
@@ -805,7 +784,7 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
                     WB[s][e] = (half_t)Wp[2 * s][e];
                     WB[s][4 + e] = (half_t)Wp[2 * s + 1][e];
                 }
-            // partial O^T = S^T Q~^T + V'^T A_qk^T (staged as fp16) and R^T = P^T Q~^T + W'^T A_qk^T (to the workspace),
+            // partial O^T = S^T Q~^T + V'^T A_qk^T (fp16, to `out`) and R^T = P^T Q~^T + W'^T A_qk^T (to the workspace),
             // transposed tiles sharing the Q~ and A_qk fragments: lane (g, m) holds token 16 it + m, columns
             // 16 w + 4 g .. + 3
             half_t* rdst = ws_r + ((int64_t)(chain[C_RBASE] + cl) * H + h) * (64 * D) + 16 * w + 4 * g;
@@ -828,7 +807,9 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
                 f16x4 o, rr;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) { o[e] = (half_t)(p.scale * acc[e]); rr[e] = (half_t)acr[e]; }
-                *reinterpret_cast<f16x4*>(lds + LDS_A + (16 * it + m) * (4 * RS32) + 64 * w + 8 * g) = o;
+                if (16 * it + m < L)
+                    *reinterpret_cast<f16x4*>(p.out + ((int64_t)t0 + 16 * it + m) * p.out_rs + (int64_t)h * D + 16 * w +
+                                              4 * g) = o;
                 *reinterpret_cast<f16x4*>(rdst + (16 * it + m) * D) = rr;
             }
 #pragma unroll
@@ -871,9 +852,8 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
                     VB[s][4 + e] = (half_t)Vp[2 * s + 1][e];
                 }
             // O^T = S^T Q~^T + V'^T A_qk^T: the same fragments with the MFMA operands swapped give the transposed tile, so
-            // lane (g, m) holds token 16 it + m, values 16 w + 4 g .. + 3 and stages them with one 8-byte store.  O is
-            // staged in region A: token tk, value v at byte tk * 528 + 64 (v / 16) + 2 (v % 16) -- the first half of the
-            // 64-byte slot the raw thread (tk, v / 16) later fills with its gate values
+            // lane (g, m) holds token 16 it + m, values 16 w + 4 g .. + 3 and stores them to `out` with one 8-byte store
+            // (the 8 waves' 32-byte pieces of a token row meet in the L2)
 #pragma unroll
             for (int it = 0; it < 4; ++it) {
                 f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -886,7 +866,9 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
                         acc = mfma32(VB[s], *reinterpret_cast<const f16x8*>(&sAq[(16 * it + m) * RS16S + 32 * s + 8 * g]),
                                      acc);
                 const u32x2 o = {f2bf2(p.scale * acc[0], p.scale * acc[1]), f2bf2(p.scale * acc[2], p.scale * acc[3])};
-                *reinterpret_cast<u32x2*>(lds + LDS_A + (16 * it + m) * (4 * RS32) + 64 * w + 8 * g) = o;
+                if (16 * it + m < L)
+                    *reinterpret_cast<u32x2*>(p.out + ((int64_t)t0 + 16 * it + m) * p.out_rs + (int64_t)h * D + 16 * w +
+                                              4 * g) = o;
             }
 #pragma unroll
             for (int dt = 0; dt < 8; ++dt) {
@@ -913,13 +895,14 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
             if (ck_mode == 1 && cs == ck_single) ck_store(ck_idx[n]);
             if (ck_mode == 2 && every > 0 && cs % every == 0 && cs < seqch) ck_store(ck_idx[ck_row0 + cs / every]);
         }
-        lds_barrier();
+        // no barrier here: the walk writes no LDS (its outputs go straight to `out`) and reads none of what the next
+        // chunk's raw-row phase writes (raw v rows, gate rows, beta); the barrier after that phase orders everything
+        // the walk reads before the cumsum and factors overwrite it
     }
-    if (nch > 0) store_out_slot(p, h, tstart + 64 * (nch - 1), min(64, len - 64 * (nch - 1)), r, cb, lds);
     if (fix) {  // the piece's local end state (blocked order) and transition (bf16 pair) for the scan; LDS is free now
         float* st0 = reinterpret_cast<float*>(lds);
         float* st1 = st0 + D * RS32;
-        lds_barrier();  // every thread has read its output slot
+        lds_barrier();  // every wave has finished the walk's LDS reads
         stage_state(st0, S, w, g, m);
         stage_state(st1, Pm, w, g, m);
         lds_barrier();
