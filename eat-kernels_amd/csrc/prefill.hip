@@ -330,9 +330,10 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
     const bool fix = P1 && (pflags & PIECE_FIX);
     const int every = tab[H_EVERY];
     const int64_t ws_arr = (int64_t)tab[H_NSLOTS] * H * D * D;  // floats per workspace array
+    const int64_t ck_words = (int64_t)tab[H_NCKSLOTS];
     float* ws_h = p.ws + ((int64_t)slot * H + h) * D * D;        // this piece-head in array 0 (+ ws_arr: 1, 2)
     float* ws_ck = p.ws + 3 * ws_arr;                            // checkpoint (S_loc, P) pairs
-    half_t* ws_r = reinterpret_cast<half_t*>(ws_ck + (int64_t)tab[H_NCKSLOTS] * 2 * H * D * D);  // R operands
+    half_t* ws_r = reinterpret_cast<half_t*>(ws_ck + ck_words * 2 * H * D * D);  // R operands
     const bool pool = (p.flags & KDA355_PF_POOL) != 0;
     const bool RB = (p.flags & KDA355_PF_RAW_BETA) != 0;
     const bool NORM = (p.flags & KDA355_PF_NORMALIZE_QK) != 0;
@@ -341,22 +342,37 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
     // completes in issue order, and a load on one path only makes the compiler wait for everything older): the first
     // chunk's rows (P0), the gate's dt_bias (P0), then the initial state, first used by the first walk.
     int tid = threadIdx.x, lane = tid & 63, m = lane & 15, g = lane >> 4, r = tid >> 3, cb = tid & 7;
+    // The prologue's memory reads are issued in two dependent rounds: first what depends on the launch alone (the
+    // table header, the chain entry, the gate's dt_bias, which is therefore waited for without waiting for the rows),
+    // then what depends on the chain entry (the first chunk's rows, the pool row and its has_initial_state flag); the
+    // initial state is issued last and only waited for before the first walk.  Every table word the loop uses is read
+    // here (empty asm operands pin the reads in the first round), so the first LDS barrier has no scalar read left to
+    // wait for.
+    typedef const __attribute__((address_space(4))) float cfloat_t;
+    const float dtb = RG ? p.dt_bias[h * D + (tid & (D - 1))] : 0.f;
+    const float alog = RG ? *reinterpret_cast<cfloat_t*>(reinterpret_cast<uintptr_t>(p.A_log + h)) : 0.f;
+    const int ck_row0 = chain[C_CKROW0], ck_single_raw = chain[C_CKSINGLE];
+    asm volatile("" ::"s"(every), "s"(ws_arr), "s"(ck_row0), "s"(ck_single_raw), "s"(ck_words), "s"(alog), "s"(p.ws));
     RawRow nx;
     load_row<RG>(p, h, tstart, nch > 0 ? min(64, len) : 0, r, cb, RB, nx);  // an empty sequence loads nothing
-    const float dtb = RG ? p.dt_bias[h * D + (tid & (D - 1))] : 0.f;
     // initial state (lane: v = 16w + m, k = 16dt + 4g + e), through a descriptor of no records when there is none
     const float* src = nullptr;
     int64_t row = -1;
-    if (pool) row = p.state_idx[n];
+    uint32_t hword = 0;
+    const uintptr_t ha = reinterpret_cast<uintptr_t>(p.has_init + n);
+    if (pool) {
+        // the pool row and has_initial_state[n] in one round: the flag by a scalar read of its aligned word through
+        // the constant address space (read-only for the kernel; a uniform address there becomes s_load_dword, so no
+        // vector load has to be waited for).  The aligned word may cover bytes next to the flag but never leaves the
+        // flag's page.
+        typedef const __attribute__((address_space(4))) uint32_t cword_t;
+        typedef const __attribute__((address_space(4))) int32_t cint_t;
+        row = *reinterpret_cast<cint_t*>(reinterpret_cast<uintptr_t>(p.state_idx + n));
+        hword = *reinterpret_cast<cword_t*>(ha & ~(uintptr_t)3);
+    }
     if (fix) {
         // a later piece's local run starts from zero
     } else if (pool) {
-        // has_initial_state[n] by a scalar read of its aligned word through the constant address space (read-only
-        // for the kernel; a uniform address there becomes s_load_dword, so no vector load has to be waited for).
-        // The aligned word may cover bytes next to the flag but never leaves the flag's page.
-        const uintptr_t ha = reinterpret_cast<uintptr_t>(p.has_init + n);
-        typedef const __attribute__((address_space(4))) uint32_t cword_t;
-        const uint32_t hword = *reinterpret_cast<cword_t*>(ha & ~(uintptr_t)3);
         const bool hinit = ((hword >> (8 * (ha & 3))) & 0xffu) != 0;
         if (row >= 0 && row < p.state_slots && hinit) src = p.state_pool + row * p.state_ss + (int64_t)h * D * D;
     } else if (p.init_state) {
@@ -390,13 +406,12 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
         else
             store_state(reinterpret_cast<float*>(p.ck_pool) + rr * p.ck_ss + (int64_t)h * D * D, S, w, g, m);
     };
-    const int ck_row0 = chain[C_CKROW0];
-    const int ck_single = (ck_mode == 1) ? chain[C_CKSINGLE] : 0;
+    const int ck_single = (ck_mode == 1) ? ck_single_raw : 0;
 
     // gate-in-kernel constants for this thread's 16 channels
     float Aexp = 0.f;
     if (RG) {
-        Aexp = __expf(p.A_log[h]);
+        Aexp = __expf(alog);
         if (tid < D) sDT[tid] = dtb;
     }
     // A_qk blocks (0,1) and (2,3) are read by the walk and never written by the Gram phase
