@@ -277,19 +277,18 @@ __device__ __forceinline__ void copy_staged_blocked(float* dst, const float* sta
         *reinterpret_cast<f32x4*>(dst + 4 * i) = v;
     }
 }
-// A staged [128][128] fp32 array as the bf16 pair hi = RNE(x), lo = RNE(x - hi) (two arrays of 16384 bf16, lo after
-// hi), each in the order: element (a, b) at ((a / 8) * 128 + b) * 8 + a % 8, i.e. the 8 values of each column in one
-// group of 8 rows are 16 contiguous bytes, the operand of one lane of a bf16 16x16x32 MFMA.
-__device__ __forceinline__ void copy_staged_split(uint16_t* dst, const float* stage) {
+// A staged [128][128] fp32 array as fp16 (RNE; 16384 values) in the order: element (a, b) at
+// ((a / 8) * 128 + b) * 8 + a % 8, i.e. the 8 values of each column in one group of 8 rows are 16 contiguous bytes,
+// the operand of one lane of a 16x16x32 MFMA.  The transition is an fp16 MFMA operand at every chunk of the walk
+// that forms it, so one more fp16 rounding here adds an error of the same kind, not a new one.
+__device__ __forceinline__ void copy_staged_h(half_t* dst, const float* stage) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int i = threadIdx.x + PF_THREADS * j, a8 = i >> 7, b = i & 127;
-        uint32_t hi[4], lo[4];
+        f16x8 v;
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-            split_bf16x2(stage[(8 * a8 + 2 * r) * RS32 + b], stage[(8 * a8 + 2 * r + 1) * RS32 + b], hi[r], lo[r]);
-        *reinterpret_cast<u32x4*>(dst + 8 * i) = u32x4{hi[0], hi[1], hi[2], hi[3]};
-        *reinterpret_cast<u32x4*>(dst + D * D + 8 * i) = u32x4{lo[0], lo[1], lo[2], lo[3]};
+        for (int r = 0; r < 8; ++r) v[r] = (half_t)stage[(8 * a8 + r) * RS32 + b];
+        *reinterpret_cast<f16x8*>(dst + 8 * i) = v;
     }
 }
 
@@ -914,7 +913,7 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
         // chunk's raw-row phase writes (raw v rows, gate rows, beta); the barrier after that phase orders everything
         // the walk reads before the cumsum and factors overwrite it
     }
-    if (fix) {  // the piece's local end state (blocked order) and transition (bf16 pair) for the scan; LDS is free now
+    if (fix) {  // the piece's local end state (blocked order) and transition (fp16) for the scan; LDS is free now
         float* st0 = reinterpret_cast<float*>(lds);
         float* st1 = st0 + D * RS32;
         lds_barrier();  // every wave has finished the walk's LDS reads
@@ -922,7 +921,7 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
         stage_state(st1, Pm, w, g, m);
         lds_barrier();
         copy_staged_blocked(ws_h, st0);
-        copy_staged_split(reinterpret_cast<uint16_t*>(ws_h + ws_arr), st1);
+        copy_staged_h(reinterpret_cast<half_t*>(ws_h + ws_arr), st1);
         return;
     }
     if (P1 && (pflags & PIECE_STORE_END)) {  // the first piece of a split sequence: the second piece's start state
@@ -1006,24 +1005,31 @@ __device__ __forceinline__ void scan_task(int H, int blk, int nblk, int& ei, int
 }
 
 // The scan's operands: a later piece stores its local end state S_loc in blocked order (element (a, b) at
-// ((a / 4) * 128 + b) * 4 + a % 4, a = v) and its transition P[k'][k] as the bf16 pair hi = RNE(x), lo = RNE(x - hi)
-// in groups of 8 rows (copy_staged_split).  The product X P runs on bf16 16x16x32 MFMAs as X_hi P_hi + X_hi P_lo +
-// X_lo P_hi: each pair carries 16 bits of mantissa and the dropped X_lo P_lo term is below 2^-16 of each product, at
-// a fifth of the MFMA cycles of fp32 16x16x4 MFMAs (which bound the step before).  4 waves per workgroup, wave w on
-// the two 16-column tiles 32 w + 16 ct + j; MFMA t covers k' = 32 t + 8 kq .. + 7 (kq = lane / 16, j = lane % 16),
-// so a lane's B values per MFMA are one 16-byte load of hi and one of lo, with the 16 lanes of a row group reading
-// 256 contiguous bytes, and its L values (rows 16 rb + 4 kq .. + 3 of S_loc) one more 16-byte load.  The running
-// state block X sits in LDS as the bf16 pair (16 hi rows, then 16 lo rows, SCAN_XS bf16 per row: the 16-byte A reads
-// of the 16 rows fall on distinct banks).  One register set of operands is 72 VGPRs; three sets leave two
-// workgroups per CU, which a scan of one or two steps over many sequences needs more than a shorter step.
+// ((a / 4) * 128 + b) * 4 + a % 4, a = v) and its transition P[k'][k] as fp16 in groups of 8 rows (copy_staged_h).
+// The product X P runs on f16 16x16x32 MFMAs as X_lo P + X_hi P, X held as the fp16 pair hi = RNE(x),
+// lo = RNE(x - hi) (22 bits of mantissa; the state's fp16 range is the walk's own), P as the walk formed it (an fp16
+// operand at each of its chunks).  The step is bound by moving its operands into the CU, not by its 16 MFMAs per wave:
+// P as one fp16 array is 32 KiB a step against 64 KiB as a bf16 pair.  4 waves per workgroup, wave w on the two
+// 16-column tiles 32 w + 16 ct + j; MFMA t covers k' = 32 t + 8 kq .. + 7 (kq = lane / 16, j = lane % 16), so a
+// lane's B values per MFMA are one 16-byte load, with the 16 lanes of a row group reading 256 contiguous bytes, and
+// its L values (rows 16 rb + 4 kq .. + 3 of S_loc) one more 16-byte load.  The running state block X sits in LDS as
+// the fp16 pair (16 hi rows, then 16 lo rows, SCAN_XS halves per row: the 16-byte A reads of the 16 rows fall on
+// distinct banks).  One register set of operands is 40 VGPRs.
 constexpr int SCAN_THREADS = 256;
 constexpr int SCAN_XS = 136;
-constexpr int SCAN_XBUF = 2 * SC_ROWS * SCAN_XS;  // bf16 of one staged block
+constexpr int SCAN_XBUF = 2 * SC_ROWS * SCAN_XS;  // halves of one staged block
 constexpr int SCAN_SMEM = 2 * SCAN_XBUF * 2;      // two blocks (the scan alternates between them)
 struct ScanOps {
-    u32x4 b[2][8];  // b[ct][2 t + {0: hi, 1: lo}] = P[32 t + 8 kq .. + 7][32 w + 16 ct + j]
+    u32x4 b[2][4];  // b[ct][t] = P[32 t + 8 kq .. + 7][32 w + 16 ct + j]
     f32x4 l[2];     // l[ct] = L[16 rb + 4 kq .. + 3][32 w + 16 ct + j]
 };
+// the fp16 pair hi = RNE(x), lo = RNE(x - hi) of two fp32 values, each pair packed in one word (element 0 low)
+__device__ __forceinline__ void split_f16x2(float x0, float x1, uint32_t& hi, uint32_t& lo) {
+    const half_t h0 = (half_t)x0, h1 = (half_t)x1;
+    const half_t l0 = (half_t)(x0 - (float)h0), l1 = (half_t)(x1 - (float)h1);
+    hi = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+    lo = (uint32_t)__builtin_bit_cast(uint16_t, l0) | ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
+}
 // Buffer loads: the lane part of the address is one VGPR, the steps between a lane's operand groups are scalar
 // offsets (a global load's immediate offset does not reach them, and 64-bit addresses per load cost VGPRs).
 // live = false loads nothing (descriptors of no records: the loads return zeros and move no data).
@@ -1037,29 +1043,25 @@ __device__ __forceinline__ void fetch_scan(const float* PB, const float* LB, int
         const int col = 32 * w + 16 * ct + j;
 #pragma unroll
         for (int t = 0; t < 4; ++t)
-#pragma unroll
-            for (int hl = 0; hl < 2; ++hl)
-                o.b[ct][2 * t + hl] = __builtin_bit_cast(
-                    u32x4, __builtin_amdgcn_raw_buffer_load_b128(rp, (kq * D + col) * 16, t * 4 * D * 16 + hl * D * D * 2, 0));
+            o.b[ct][t] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rp, (kq * D + col) * 16,
+                                                                                         t * 4 * D * 16, 0));
         o.l[ct] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rl, ((4 * rb + kq) * D + col) * 16, 0, 0));
     }
 }
-// acc[ct][e] = out[4 kq + e][32 w + 16 ct + j]; sX (the bf16 pair block) staged and synced
+// acc[ct][e] = out[4 kq + e][32 w + 16 ct + j]; sX (the fp16 pair block) staged and synced
 __device__ __forceinline__ void compose_scan(const uint16_t* sX, const ScanOps& o, f32x4 (&acc)[2]) {
     const int j = threadIdx.x & 15, kq = (threadIdx.x & 63) >> 4;
     acc[0] = o.l[0];
     acc[1] = o.l[1];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-        const bf16x8 ah = *reinterpret_cast<const bf16x8*>(sX + j * SCAN_XS + 32 * t + 8 * kq);
-        const bf16x8 al = *reinterpret_cast<const bf16x8*>(sX + (SC_ROWS + j) * SCAN_XS + 32 * t + 8 * kq);
+        const f16x8 ah = *reinterpret_cast<const f16x8*>(sX + j * SCAN_XS + 32 * t + 8 * kq);
+        const f16x8 al = *reinterpret_cast<const f16x8*>(sX + (SC_ROWS + j) * SCAN_XS + 32 * t + 8 * kq);
 #pragma unroll
         for (int ct = 0; ct < 2; ++ct) {
-            const bf16x8 bh = __builtin_bit_cast(bf16x8, o.b[ct][2 * t]);
-            const bf16x8 bl = __builtin_bit_cast(bf16x8, o.b[ct][2 * t + 1]);
-            acc[ct] = mfma32bf(al, bh, acc[ct]);
-            acc[ct] = mfma32bf(ah, bl, acc[ct]);
-            acc[ct] = mfma32bf(ah, bh, acc[ct]);
+            const f16x8 b = __builtin_bit_cast(f16x8, o.b[ct][t]);
+            acc[ct] = mfma32(al, b, acc[ct]);
+            acc[ct] = mfma32(ah, b, acc[ct]);
         }
     }
 }
@@ -1072,7 +1074,7 @@ __device__ __forceinline__ void compose_scan(const uint16_t* sX, const ScanOps& 
 // the states are not waited for.  A freshly written transition takes about two compositions to arrive, so each
 // piece's operands are fetched two steps ahead, into one of three register sets (refilled right after the step that
 // used it, behind that step's state stores, so that a wait for a store never waits for a prefetch).
-// LEAN (every split sequence in at most 3 pieces, config 1's case): one register set, no fetch ahead; ~100 VGPRs fit
+// LEAN (every split sequence in at most 3 pieces, config 1's case): one register set, no fetch ahead; ~70 registers fit
 // four workgroups per CU, so a launch of many short scans runs in one round.
 template <bool LEAN>
 __device__ __forceinline__ void scan_body(const PfParams& p, const int32_t* __restrict__ tab, unsigned char* lds, int wg,
@@ -1117,9 +1119,9 @@ __device__ __forceinline__ void scan_body(const PfParams& p, const int32_t* __re
 #pragma unroll
             for (int ee = 0; ee < 4; ++ee) {
                 const int rr = 4 * kq + ee, col = 32 * w + 16 * ct + j;
-                const uint32_t hb = f2bf(acc[ct][ee]);
-                sN[rr * SCAN_XS + col] = (uint16_t)hb;
-                sN[(SC_ROWS + rr) * SCAN_XS + col] = (uint16_t)f2bf(acc[ct][ee] - bf2f(hb));
+                const half_t hh = (half_t)acc[ct][ee];
+                sN[rr * SCAN_XS + col] = __builtin_bit_cast(uint16_t, hh);
+                sN[(SC_ROWS + rr) * SCAN_XS + col] = __builtin_bit_cast(uint16_t, (half_t)(acc[ct][ee] - (float)hh));
                 __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[ct][ee]), rs, (int)(blk + rr * D + col) * 4, 0,
                                                       0);
             }
@@ -1143,8 +1145,8 @@ __device__ __forceinline__ void scan_body(const PfParams& p, const int32_t* __re
         for (int q = 0; q < 2; ++q) {
             const int i = threadIdx.x + SCAN_THREADS * q, rr = i >> 5, c = 4 * (i & 31);
             uint32_t h0, l0, h1, l1;
-            split_bf16x2(x1[q][0], x1[q][1], h0, l0);
-            split_bf16x2(x1[q][2], x1[q][3], h1, l1);
+            split_f16x2(x1[q][0], x1[q][1], h0, l0);
+            split_f16x2(x1[q][2], x1[q][3], h1, l1);
             *reinterpret_cast<u32x2*>(sX + rr * SCAN_XS + c) = u32x2{h0, h1};
             *reinterpret_cast<u32x2*>(sX + (SC_ROWS + rr) * SCAN_XS + c) = u32x2{l0, l1};
         }
@@ -1164,8 +1166,8 @@ __device__ __forceinline__ void scan_body(const PfParams& p, const int32_t* __re
     for (int q = 0; q < 2; ++q) {
         const int i = threadIdx.x + SCAN_THREADS * q, rr = i >> 5, c = 4 * (i & 31);
         uint32_t h0, l0, h1, l1;
-        split_bf16x2(x1[q][0], x1[q][1], h0, l0);
-        split_bf16x2(x1[q][2], x1[q][3], h1, l1);
+        split_f16x2(x1[q][0], x1[q][1], h0, l0);
+        split_f16x2(x1[q][2], x1[q][3], h1, l1);
         *reinterpret_cast<u32x2*>(sX + rr * SCAN_XS + c) = u32x2{h0, h1};
         *reinterpret_cast<u32x2*>(sX + (SC_ROWS + rr) * SCAN_XS + c) = u32x2{l0, l1};
     }
@@ -1242,18 +1244,9 @@ __device__ __forceinline__ void fixup_body(const PfParams& p, const int32_t* __r
     const half_t* R0 = reinterpret_cast<const half_t*>(p.ws + 3 * ws_arr + (int64_t)tab[H_NCKSLOTS] * 2 * H * D * D) +
                        ((int64_t)e[X_RSLOT] * H + h) * (64 * D);                  // [token][k], chunk c at + c H 64 D
     const int64_t rstep = (int64_t)H * 64 * D;
-    {  // S_start -> LDS fp16: thread t converts 4 values at a time (v = i / 32, k = 4 (i % 32))
-        f32x4 x[16];
+    f32x4 x[16];  // S_start, 4 values at a time (v = i / 32, k = 4 (i % 32))
 #pragma unroll
-        for (int j = 0; j < 16; ++j) x[j] = reinterpret_cast<const f32x4*>(Sst)[threadIdx.x + FX_THREADS * j];
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            const int i = threadIdx.x + FX_THREADS * j, v = i >> 5, c4 = i & 31;
-            const f16x4 hv = {(half_t)x[j][0], (half_t)x[j][1], (half_t)x[j][2], (half_t)x[j][3]};
-            *reinterpret_cast<f16x4*>(lds + fx_slot(v, c4 >> 1) + 8 * (c4 & 1)) = hv;
-        }
-    }
-    __syncthreads();
+    for (int j = 0; j < 16; ++j) x[j] = reinterpret_cast<const f32x4*>(Sst)[threadIdx.x + FX_THREADS * j];
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, m = lane & 15, g = lane >> 4;
     const int rs = p.out_rs * 2;  // bytes per output row
     const int tok = 16 * w + m;   // this lane's token inside a chunk
@@ -1306,9 +1299,18 @@ __device__ __forceinline__ void fixup_body(const PfParams& p, const int32_t* __r
             __builtin_amdgcn_raw_buffer_store_b128(r, ob, obase + 16 * i, 0, 0);
         }
     };
-    // each chunk's loads are issued one chunk ahead; the loop is unrolled whole (straight-line waits)
+    // each chunk's loads are issued one chunk ahead; the loop is unrolled whole (straight-line waits).  The first
+    // chunk's loads follow the start state's at once, and the barrier after the start state's LDS writes waits for
+    // LDS alone, so they stay in flight through the conversion.
     Ops A, B;
     load(A, 0);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {  // S_start -> LDS fp16
+        const int i = threadIdx.x + FX_THREADS * j, v = i >> 5, c4 = i & 31;
+        const f16x4 hv = {(half_t)x[j][0], (half_t)x[j][1], (half_t)x[j][2], (half_t)x[j][3]};
+        *reinterpret_cast<f16x4*>(lds + fx_slot(v, c4 >> 1) + 8 * (c4 & 1)) = hv;
+    }
+    lds_barrier();
 #pragma unroll
     for (int i = 0; i < FX_GROUP; i += 2) {
         if (i + 1 < FX_GROUP) load(B, 64 * (i + 1));
