@@ -1415,9 +1415,10 @@ extern "C" int kda355_prefill_plan(const KdaPrefillPlanIn* in, KdaPrefillPlan* p
     // fixup (FIX_BASE + FIX_UNITS per chunk-head of later pieces, spread over the chip); every workgroup also pays a
     // start-up of START_QUARTERS / 4 chunk times.  The cheapest candidate wins; ties keep fewer pieces.  The first piece of a split sequence runs from the
     // true start state; later pieces run from S = 0, carry their transition and are completed by the scan, fixup and
-    // checkpoint-compose kernels.  Measured on MI355X: scan steps ~2.7 us, fixup ~11 ns per chunk-head.
+    // checkpoint-compose kernels.  Measured on MI355X: the scan ~7 us to start and ~0.55 us a step, the fixup ~11 ns
+    // per chunk-head.
     constexpr int MIN_PIECE = 2;
-    constexpr double SCAN_BASE = 0.5, STEP_UNITS = 0.15, SCAN_WG_UNITS = 0.25, FIX_BASE = 0.5, FIX_UNITS = 0.0012;
+    constexpr double SCAN_BASE = 0.6, STEP_UNITS = 0.05, SCAN_WG_UNITS = 0.25, FIX_BASE = 0.5, FIX_UNITS = 0.0012;
     constexpr int64_t START_QUARTERS = 4;  // a workgroup's start-up (state, first rows): about one chunk time
     const int num_cus = in->num_cus > 0 ? in->num_cus : 256;
     // chunk counts of the pieces of a c-chunk sequence for piece length T: near-equal (mode 0), or T chunks each and
