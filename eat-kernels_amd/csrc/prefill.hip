@@ -1406,53 +1406,55 @@ extern "C" int kda355_prefill_plan(const KdaPrefillPlanIn* in, KdaPrefillPlan* p
     }
     // Pieces.  A workgroup walks one (piece, head) chain and a CU holds one such workgroup at a time; the chain list is
     // dispatched longest first.  Candidate cuts: every sequence longer than a piece length T is cut into
-    // ceil(nch / T) near-equal pieces of >= MIN_PIECE chunks, or into pieces of T chunks followed by the remainder
-    // (which fills CUs the long pieces leave idle: 16 chunks on 3/4 of the CUs cut as 12 + 4), for T on a geometric
-    // ladder from a quarter of the balanced per-CU load.  Each candidate is costed in chunk times (one chunk of one head on one CU, ~11 us) by
-    // list-scheduling its chains onto the CUs (later pieces cost as much per chunk as first ones), plus the passes a
-    // split adds: the scan, sequential over the pieces of a sequence (SCAN_BASE + STEP_UNITS per later piece of the
-    // most-cut sequence, + SCAN_WG_UNITS per scan workgroup per CU: 8 per split sequence and head), and the output
-    // fixup (FIX_BASE + FIX_UNITS per chunk-head of later pieces, spread over the chip); every workgroup also pays a
-    // start-up of START_QUARTERS / 4 chunk times.  The cheapest candidate wins; ties keep fewer pieces.  The first piece of a split sequence runs from the
-    // true start state; later pieces run from S = 0, carry their transition and are completed by the scan, fixup and
-    // checkpoint-compose kernels.  Measured on MI355X: the scan ~7 us to start and ~0.55 us a step, the fixup ~11 ns
-    // per chunk-head.
-    constexpr int MIN_PIECE = 2;
+    // ceil(nch / T) near-equal pieces, or into pieces of T chunks followed by the remainder (which fills CUs the long
+    // pieces leave idle: 16 chunks on 3/4 of the CUs cut as 12 + 4), for T on a geometric ladder from a quarter of the
+    // balanced per-CU load.  Pieces have >= MIN_PIECE chunks, or >= 1 in a plan whose workgroups all start at once.
+    // Each candidate is costed in chunk times (one chunk of one head on one CU, ~11 us) by list-scheduling its
+    // workgroups onto each XCD's CUs in launch order (later pieces cost as much per chunk as first ones), plus the
+    // passes a split adds: the scan, sequential over the pieces of a sequence (SCAN_BASE + STEP_UNITS per later piece
+    // of the most-cut sequence, + SCAN_WG_UNITS per scan workgroup per CU: 8 per split sequence and head), and the
+    // output fixup (FIX_BASE + FIX_UNITS per chunk-head of later pieces, spread over the chip); every workgroup also
+    // pays a start-up of START_QUARTERS / 4 chunk times.  The cheapest candidate wins; ties keep fewer pieces.  The
+    // first piece of a split sequence runs from the true start state; later pieces run from S = 0, carry their
+    // transition and are completed by the scan, fixup and checkpoint-compose kernels.  Measured on MI355X: the scan
+    // ~7 us to start and ~0.55 us a step, the fixup ~11 ns per chunk-head.
+    constexpr int MIN_PIECE = 2;  // the shortest piece of a plan whose workgroups run in more than one round
     constexpr double SCAN_BASE = 0.6, STEP_UNITS = 0.05, SCAN_WG_UNITS = 0.25, FIX_BASE = 0.5, FIX_UNITS = 0.0012;
     constexpr int64_t START_QUARTERS = 4;  // a workgroup's start-up (state, first rows): about one chunk time
     const int num_cus = in->num_cus > 0 ? in->num_cus : 256;
-    // chunk counts of the pieces of a c-chunk sequence for piece length T: near-equal (mode 0), or T chunks each and
-    // the remainder last (mode 1; a remainder under MIN_PIECE joins the piece before it)
-    auto piece_lengths = [](int c, int T, int mode, std::vector<int>& out) {
+    const int nxcd = (num_cus >= 8 && num_cus % 8 == 0) ? 8 : 1, cus_per_xcd = num_cus / nxcd;  // MI355X: 8 XCDs
+    // chunk counts of the pieces of a c-chunk sequence for piece length T and shortest piece minp: near-equal (mode 0),
+    // or T chunks each and the remainder last (mode 1; a remainder under minp joins the piece before it)
+    auto piece_lengths = [](int c, int T, int mode, int minp, std::vector<int>& out) {
         out.clear();
-        if (c <= T || c < 2 * MIN_PIECE) {
+        if (c <= T || c < 2 * minp) {
             out.push_back(c);
         } else if (mode == 0) {
-            const int np = std::max(1, std::min(c / MIN_PIECE, (c + T - 1) / T));
+            const int np = std::max(1, std::min(c / minp, (c + T - 1) / T));
             for (int pc = 0; pc < np; ++pc) out.push_back(c / np + (pc < c % np ? 1 : 0));
         } else {
             int left = c;
             while (left > T) { out.push_back(T); left -= T; }
-            if (left >= MIN_PIECE) out.push_back(left); else out.back() += left;
+            if (left >= minp) out.push_back(left); else out.back() += left;
         }
     };
-    int cutT = 1 << 30, cutMode = 0;  // no cut unless the cost model finds one
+    int cutT = 1 << 30, cutMode = 0, cutMin = MIN_PIECE;  // no cut unless the cost model finds one
     if (nchunks > 0) {
         int maxc = 0;
         for (int n = 0; n < N; ++n) maxc = std::max(maxc, nch[n]);
         const int64_t avg = std::max<int64_t>(1, (nchunks * in->H + num_cus - 1) / num_cus);
         const bool idle = (int64_t)N * in->H < num_cus;
-        if ((idle || 4 * (int64_t)maxc > 5 * avg) && maxc >= 2 * MIN_PIECE) {
+        if ((idle || 4 * (int64_t)maxc > 5 * avg) && maxc >= 2) {
             std::vector<int> counts, lens;
             std::vector<int64_t> loads;
             const int64_t total_units = nchunks * in->H;
             double best = 0.0;
-            auto cost = [&](int T, int mode, bool first) {
+            auto cost = [&](int T, int mode, int minp, bool first) {
                 counts.clear();
                 int64_t fixch = 0;
                 int nsplit = 0, most = 0, maxnp = 1;
                 for (int n = 0; n < N; ++n) {
-                    piece_lengths(nch[n], T, mode, lens);
+                    piece_lengths(nch[n], T, mode, minp, lens);
                     const int np = (int)lens.size();
                     maxnp = std::max(maxnp, np);
                     for (int pc = 0; pc < np; ++pc) {
@@ -1467,6 +1469,10 @@ extern "C" int kda355_prefill_plan(const KdaPrefillPlanIn* in, KdaPrefillPlan* p
                     nsplit ? SCAN_BASE + STEP_UNITS * (maxnp - 1) + SCAN_WG_UNITS * 8.0 * nsplit * in->H / num_cus +
                                  FIX_BASE + FIX_UNITS * (double)fixch * in->H
                            : 0.0;
+                // one-chunk pieces only in plans whose workgroups all start at once: a workgroup left waiting for a CU
+                // waits for one in its own part of the chip, measured 2-3 chunk times later than this schedule puts
+                // it, which pieces that short do not repay
+                if (minp < MIN_PIECE && (int64_t)counts.size() * in->H > num_cus) return 1e30;
                 // loads in quarter chunk times: a workgroup costs its chunks plus its start-up
                 const int64_t q_total = 4 * total_units + START_QUARTERS * (int64_t)counts.size() * in->H;
                 // no schedule beats the longest piece or the perfect balance
@@ -1474,35 +1480,39 @@ extern "C" int kda355_prefill_plan(const KdaPrefillPlanIn* in, KdaPrefillPlan* p
                     0.25 * (double)std::max<int64_t>(4 * most + START_QUARTERS, (q_total + num_cus - 1) / num_cus) + extra;
                 if (!first && bound >= best) return bound;
                 std::sort(counts.begin(), counts.end(), std::greater<int>());
-                // list scheduling, longest first: each workgroup goes to the CU that frees up first
-                loads.assign(num_cus, 0);  // a min-heap of finish times (all zero: a valid heap)
-                int64_t span = 0;
+                // list scheduling in launch order (chains longest first, heads within a chain): the hardware sends
+                // workgroup i to XCD i % 8, and there it takes the CU that frees up first; a workgroup waiting for a
+                // CU does not move to another XCD
+                loads.assign(num_cus, 0);  // per XCD a min-heap of finish times (all zero: valid heaps)
+                int64_t span = 0, wg = 0;
                 for (int c : counts)
-                    for (int hh = 0; hh < in->H; ++hh) {
-                        std::pop_heap(loads.begin(), loads.end(), std::greater<int64_t>());
-                        loads.back() += 4 * c + START_QUARTERS;
-                        span = std::max(span, loads.back());
-                        std::push_heap(loads.begin(), loads.end(), std::greater<int64_t>());
+                    for (int hh = 0; hh < in->H; ++hh, ++wg) {
+                        const auto b = loads.begin() + (wg % nxcd) * cus_per_xcd, e = b + cus_per_xcd;
+                        std::pop_heap(b, e, std::greater<int64_t>());
+                        *(e - 1) += 4 * c + START_QUARTERS;
+                        span = std::max(span, *(e - 1));
+                        std::push_heap(b, e, std::greater<int64_t>());
                     }
                 return 0.25 * (double)span + extra;
             };
-            best = cost(maxc, 0, true);
+            best = cost(maxc, 0, MIN_PIECE, true);
             // pieces shorter than a quarter of the balanced load per CU only add fixup work: the ladder starts there
-            for (double t = std::max<double>(MIN_PIECE, (double)avg / 4); t < maxc; t *= 1.12) {
-                const int T = (int)t;
-                for (int mode = 0; mode < 2; ++mode) {
-                    const double c = cost(T, mode, false);
-                    if (c < best - 1e-9) { best = c; cutT = T; cutMode = mode; }
+            for (int minp = MIN_PIECE; minp >= 1; --minp)
+                for (double t = std::max<double>(minp, (double)avg / 4); t < maxc; t *= 1.12) {
+                    const int T = (int)t;
+                    for (int mode = 0; mode < 2; ++mode) {
+                        const double c = cost(T, mode, minp, false);
+                        if (c < best - 1e-9) { best = c; cutT = T; cutMode = mode; cutMin = minp; }
+                    }
                 }
-            }
             // then piece lengths within one ladder step of the best (at most ~32 per cut style)
             if (cutT < maxc) {
-                const int lo = std::max(MIN_PIECE, (int)(cutT / 1.12)), hi = std::min(maxc - 1, (int)(cutT * 1.12) + 1);
+                const int lo = std::max(cutMin, (int)(cutT / 1.12)), hi = std::min(maxc - 1, (int)(cutT * 1.12) + 1);
                 const int T0 = cutT, step = std::max(1, (hi - lo) / 32);
                 for (int T = lo; T <= hi; T += step)
                     for (int mode = 0; mode < 2; ++mode) {
                         if (T == T0) continue;
-                        const double c = cost(T, mode, false);
+                        const double c = cost(T, mode, cutMin, false);
                         if (c < best - 1e-9) { best = c; cutT = T; cutMode = mode; }
                     }
             }
@@ -1529,7 +1539,7 @@ extern "C" int kda355_prefill_plan(const KdaPrefillPlanIn* in, KdaPrefillPlan* p
     int nslots = 0, nsplit = 0, nrslots = 0, nfix = 0, nsplitpieces = 0;
     std::vector<int> plens, npieces(N, 1);
     for (int n = 0; n < N; ++n) {
-        piece_lengths(nch[n], cutT, cutMode, plens);
+        piece_lengths(nch[n], cutT, cutMode, cutMin, plens);
         const int np = (int)plens.size();
         npieces[n] = np;
         int f = 0;

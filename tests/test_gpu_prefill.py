@@ -515,6 +515,98 @@ def test_split_pool_every_n_checkpoints(oracle, ckdt):
             assert np.isnan(got[i]).all(), f"checkpoint row {i} should be untouched"
 
 
+ONE_CHUNK_LENS = [1024, 200, 130, 64]  # at H = 4 the plan cuts the first three into one-chunk pieces
+
+
+def _one_chunk_plan_ok(meta, lens):
+    # every split sequence in pieces of one chunk: as many pieces as chunks
+    nch = [-(-n // 64) for n in lens]
+    assert meta.split == (sum(nch[:3]), 3), f"expected one-chunk pieces, got {meta.split}"
+
+
+def test_split_one_chunk_pieces_serving(oracle):
+    """Pieces of a single chunk (short sequences spread over idle CUs): the serving path with single checkpoints at
+    the ends of later pieces (chunks 10, 2, 2, and the whole one-chunk sequence), partial last chunks (200 and 130
+    tokens), has_initial_state mixed; outputs and pool rows against the fp64 oracle, other rows untouched."""
+    kda = _kda()
+    H, lens = 4, ONE_CHUNK_LENS
+    hinit = [1, 0, 1, 1]
+    ck_off = [640, 128, 128, 64]
+    g = gen(74)
+    T, N = sum(lens), len(lens)
+    q, k, v, raw_g, raw_b, A_log, dt_bias = _raw_inputs(g, T, H)
+    slots = 2 * N + 3
+    raw, ssm = _pages(slots, H, 3, g)
+    perm = torch.randperm(slots - 1, generator=g) + 1
+    sidx = perm[:N].to(torch.int32)
+    cidx = perm[N:2 * N].to(torch.int32)
+    for n in range(N):
+        if not hinit[n]:
+            ssm[int(sidx[n])] = float("nan")
+        ssm[int(cidx[n])] = float("nan")
+    pool0 = ssm.cpu().numpy().copy()
+    cu_cpu = torch.tensor(_cu(lens), dtype=torch.int32)
+    meta = kda.prefill_prepare(cu_cpu, H, torch.tensor(ck_off, dtype=torch.int32), cidx, device=DEV)
+    _one_chunk_plan_ok(meta, lens)
+    _say(f"one-chunk pieces serving H={H} lens={lens} pieces={meta.split}")
+    out = torch.empty(1, T, H, D, dtype=torch.bfloat16, device=DEV)
+    kda.prefill(q[None].to(DEV), k[None].to(DEV), v[None].to(DEV), raw_g[None].to(DEV), raw_b[None].to(DEV),
+                A_log.to(DEV), dt_bias.to(DEV), D ** -0.5, -5.0, ssm, sidx.to(DEV),
+                torch.tensor(hinit, dtype=torch.bool).to(DEV), cu_cpu.to(DEV), out,
+                torch.tensor(ck_off, dtype=torch.int32).to(DEV), cidx.to(DEV), meta=meta)
+    torch.cuda.synchronize()
+    ro, rnew = oracle.prefill_serving(f32(q), f32(k), f32(v), f32(raw_g), f32(raw_b), f32(A_log), f32(dt_bias), -5.0,
+                                      D ** -0.5, pool0, sidx.numpy(), np.array(hinit, bool), _cu(lens),
+                                      np.array(ck_off), cidx.numpy(), precision=64)
+    _check_out(out[0], ro, "one-chunk serving", _cu(lens))
+    got = ssm.cpu().numpy()
+    written = [int(s) for s in sidx] + [int(c) for c in cidx]
+    for r in written:
+        e = rel_frob(got[r], rnew[r])
+        assert e <= STATE_TOL, f"pool row {r}: relF {e:.3e}"
+    for r in range(slots):
+        if r not in written:
+            assert np.array_equal(got[r], pool0[r], equal_nan=True), f"pool row {r} should be untouched"
+
+
+def test_split_one_chunk_pieces_every_n(oracle):
+    """One-chunk pieces with a checkpoint row at every chunk boundary (every = 64 tokens): every row after a
+    sequence's first chunk is composed from a later piece's (local state, transition) pair."""
+    kda = _kda()
+    H, lens, every = 4, ONE_CHUNK_LENS, 64
+    g = gen(75)
+    T, N = sum(lens), len(lens)
+    q, k, v, gg, beta = config_inputs(T, H, g)
+    P = N + 3
+    pool0 = torch.randn(P, H, D, D, generator=g) * 0.05
+    slot = (torch.randperm(P, generator=g)[:N]).to(torch.int32)
+    nck = sum(-(-n // every) for n in lens)
+    rows = torch.randperm(nck + 4, generator=g)[:nck].to(torch.int32)
+    ck = torch.full((nck + 4, H, D, D), float("nan"), dtype=torch.float32, device=DEV)
+    pool = pool0.clone().to(DEV)
+    meta = kda.plan(torch.tensor(_cu(lens)), H, ck_every=every, device=DEV)
+    _one_chunk_plan_ok(meta, lens)
+    _say(f"one-chunk pieces every-n pieces={meta.split}")
+    o, fin, ckr = kda.chunk_kda(q[None].to(DEV), k[None].to(DEV), v[None].to(DEV), gg[None].to(DEV), beta[None].to(DEV),
+                                initial_state=pool, meta=meta, ssm_state_indices=slot.to(DEV), state_checkpoints=ck,
+                                checkpoint_every_n_tokens=every, checkpoint_state_indices=rows.to(DEV))
+    torch.cuda.synchronize()
+    ro, rf, rrows, _ = oracle.checkpoints_every_n(f32(q), f32(k), f32(v), f32(gg), f32(beta), _cu(lens), every,
+                                                 initial_state=f32(pool0)[slot.numpy()], precision=64)
+    _check_out(o[0], ro, "one-chunk every-n", _cu(lens))
+    for n in range(N):
+        assert rel_frob(f32(pool[int(slot[n])]), rf[n]) <= STATE_TOL, f"final state {n}"
+    untouched = [i for i in range(P) if i not in set(slot.tolist())]
+    assert torch.equal(pool[untouched].cpu(), pool0[untouched]), "other pool slots changed"
+    got = f32(ck)
+    for j in range(nck):
+        assert rel_frob(got[rows[j]], rrows[j]) <= STATE_TOL, f"row {j}"
+    written = set(rows.tolist())
+    for i in range(nck + 4):
+        if i not in written:
+            assert np.isnan(got[i]).all(), f"checkpoint row {i} should be untouched"
+
+
 def test_split_serving_single_checkpoints(oracle):
     """Split sequences on the serving path with one checkpoint each, at chunk boundaries the plan puts inside or at
     the end of first and later pieces (chunks 48, 127 in a partial last chunk, 3, 16); has_initial_state mixed."""
