@@ -1408,21 +1408,23 @@ extern "C" int kda355_prefill_plan(const KdaPrefillPlanIn* in, KdaPrefillPlan* p
     // dispatched longest first.  Candidate cuts: every sequence longer than a piece length T is cut into
     // ceil(nch / T) near-equal pieces, or into pieces of T chunks followed by the remainder (which fills CUs the long
     // pieces leave idle: 16 chunks on 3/4 of the CUs cut as 12 + 4), for T on a geometric ladder from a quarter of the
-    // balanced per-CU load.  Pieces have >= MIN_PIECE chunks, or >= 1 in a plan whose workgroups all start at once.
-    // Each candidate is costed in chunk times (one chunk of one head on one CU, ~11 us) by list-scheduling its
-    // workgroups onto each XCD's CUs in launch order (later pieces cost as much per chunk as first ones), plus the
-    // passes a split adds: the scan, sequential over the pieces of a sequence (SCAN_BASE + STEP_UNITS per later piece
-    // of the most-cut sequence, + SCAN_WG_UNITS per scan workgroup per CU: 8 per split sequence and head), and the
-    // output fixup (FIX_BASE + FIX_UNITS per chunk-head of later pieces, spread over the chip); every workgroup also
-    // pays a start-up of START_QUARTERS / 4 chunk times.  The cheapest candidate wins; ties keep fewer pieces.  The
+    // balanced per-CU load.  Pieces have >= MIN_PIECE chunks in a first pass and >= 1 in a second, whose candidates
+    // must beat the first pass's best.  Each candidate is costed in chunk times (one chunk of one head on one CU,
+    // ~11 us) by list-scheduling its workgroups in launch order onto the CUs of the shader engine each one is sent to
+    // (later pieces cost as much per chunk as first ones), plus the passes a split adds: the scan, sequential over the
+    // pieces of a sequence (SCAN_BASE + STEP_UNITS per later piece of the most-cut sequence, + SCAN_WG_UNITS per scan
+    // workgroup per CU: 8 per split sequence and head), and the output fixup (FIX_BASE + FIX_UNITS per chunk-head of
+    // later pieces, spread over the chip); every workgroup also pays a start-up of START_QUARTERS / 4 chunk times.  The cheapest candidate wins; ties keep fewer pieces.  The
     // first piece of a split sequence runs from the true start state; later pieces run from S = 0, carry their
     // transition and are completed by the scan, fixup and checkpoint-compose kernels.  Measured on MI355X: the scan
     // ~7 us to start and ~0.55 us a step, the fixup ~11 ns per chunk-head.
-    constexpr int MIN_PIECE = 2;  // the shortest piece of a plan whose workgroups run in more than one round
+    constexpr int MIN_PIECE = 2;  // the shortest piece of the first pass (the second allows one chunk)
     constexpr double SCAN_BASE = 0.6, STEP_UNITS = 0.05, SCAN_WG_UNITS = 0.25, FIX_BASE = 0.5, FIX_UNITS = 0.0012;
     constexpr int64_t START_QUARTERS = 4;  // a workgroup's start-up (state, first rows): about one chunk time
     const int num_cus = in->num_cus > 0 ? in->num_cus : 256;
-    const int nxcd = (num_cus >= 8 && num_cus % 8 == 0) ? 8 : 1, cus_per_xcd = num_cus / nxcd;  // MI355X: 8 XCDs
+    // MI355X: 8 XCDs of 4 shader engines of 8 CUs; workgroup i goes to XCD i % 8 and, dealt round-robin over the
+    // XCD's engines, to the group of workgroups j == i (mod 32)
+    const int ngrp = (num_cus >= 32 && num_cus % 32 == 0) ? 32 : 1, cus_per_grp = num_cus / ngrp;
     // chunk counts of the pieces of a c-chunk sequence for piece length T and shortest piece minp: near-equal (mode 0),
     // or T chunks each and the remainder last (mode 1; a remainder under minp joins the piece before it)
     auto piece_lengths = [](int c, int T, int mode, int minp, std::vector<int>& out) {
@@ -1469,10 +1471,6 @@ extern "C" int kda355_prefill_plan(const KdaPrefillPlanIn* in, KdaPrefillPlan* p
                     nsplit ? SCAN_BASE + STEP_UNITS * (maxnp - 1) + SCAN_WG_UNITS * 8.0 * nsplit * in->H / num_cus +
                                  FIX_BASE + FIX_UNITS * (double)fixch * in->H
                            : 0.0;
-                // one-chunk pieces only in plans whose workgroups all start at once: a workgroup left waiting for a CU
-                // waits for one in its own part of the chip, measured 2-3 chunk times later than this schedule puts
-                // it, which pieces that short do not repay
-                if (minp < MIN_PIECE && (int64_t)counts.size() * in->H > num_cus) return 1e30;
                 // loads in quarter chunk times: a workgroup costs its chunks plus its start-up
                 const int64_t q_total = 4 * total_units + START_QUARTERS * (int64_t)counts.size() * in->H;
                 // no schedule beats the longest piece or the perfect balance
@@ -1481,13 +1479,14 @@ extern "C" int kda355_prefill_plan(const KdaPrefillPlanIn* in, KdaPrefillPlan* p
                 if (!first && bound >= best) return bound;
                 std::sort(counts.begin(), counts.end(), std::greater<int>());
                 // list scheduling in launch order (chains longest first, heads within a chain): the hardware sends
-                // workgroup i to XCD i % 8, and there it takes the CU that frees up first; a workgroup waiting for a
-                // CU does not move to another XCD
-                loads.assign(num_cus, 0);  // per XCD a min-heap of finish times (all zero: valid heaps)
+                // workgroup i to one shader engine (8 CUs) of one XCD, the same for every i of one residue mod 32,
+                // and there it takes the CU that frees up first; a workgroup waiting for a CU does not move to
+                // another engine, even when CUs elsewhere are idle
+                loads.assign(num_cus, 0);  // per engine a min-heap of finish times (all zero: valid heaps)
                 int64_t span = 0, wg = 0;
                 for (int c : counts)
                     for (int hh = 0; hh < in->H; ++hh, ++wg) {
-                        const auto b = loads.begin() + (wg % nxcd) * cus_per_xcd, e = b + cus_per_xcd;
+                        const auto b = loads.begin() + (wg % ngrp) * cus_per_grp, e = b + cus_per_grp;
                         std::pop_heap(b, e, std::greater<int64_t>());
                         *(e - 1) += 4 * c + START_QUARTERS;
                         span = std::max(span, *(e - 1));

@@ -82,10 +82,10 @@ def _plan(lens, H, cus, every=0, ck=None):
     return pl, tab
 
 
-def _check_pieces(pl, tab, lens, H, every=0, ck_chunk=None, cus=256):
+def _check_pieces(pl, tab, lens, H, every=0, ck_chunk=None):
     """The invariants of a split plan, from its tables: every sequence's chunks are covered once, in order; a split
     sequence is a first piece (flag 4: hands over its end state) followed by later pieces (flag 1: run from zero) of
-    >= 2 chunks, or >= 1 when every workgroup of the plan (chains x heads) has a CU of its own; fixup tasks = one per group of <= 2 chunks of a later piece; compose tasks = one per checkpoint that
+    >= 1 chunk; fixup tasks = one per group of <= 2 chunks of a later piece; compose tasks = one per checkpoint that
     falls strictly inside a later piece (every-n row j: the state after j * every chunks, j * every < chunks of the
     sequence; single: the state after ck_chunk[n] chunks); the workspace = (3 slots per piece + 2 per compose task)
     states per head + one 16 KiB R tile per later-piece chunk and head."""
@@ -100,7 +100,7 @@ def _check_pieces(pl, tab, lens, H, every=0, ck_chunk=None, cus=256):
             assert pieces[0][2] == 2                      # a whole sequence: writes its final state
             continue
         assert pieces[0][2] == 4 and all(fl == 1 for _, _, fl in pieces[1:])
-        assert all(k >= 2 for _, k, _ in pieces) or pl.num_chains * H <= cus
+        assert all(k >= 1 for _, k, _ in pieces)
         for f, k, _ in pieces[1:]:
             fix += (k + 1) // 2
             r_chunks += k
@@ -178,20 +178,27 @@ def test_prefill_plan_splits_long_sequences():
     assert pl.num_split == 1 and time.perf_counter() - t0 < 0.05
 
 
-def test_prefill_plan_one_chunk_pieces_only_in_one_round():
-    """Short sequences on an idle chip are cut down to one-chunk pieces when every workgroup of the plan starts at
-    once; a plan whose workgroups would run in two rounds keeps pieces of >= 2 chunks (a workgroup waiting for a CU
-    starts later than a list schedule over all CUs puts it, which one-chunk pieces do not repay)."""
+def test_prefill_plan_one_chunk_pieces_and_engine_rounds():
+    """Short sequences on an idle chip are cut down to one-chunk pieces; and the schedule the plan is costed with
+    sends workgroup i to one shader engine of 8 CUs (the same for every i of one residue mod 32), where a workgroup
+    that finds no free CU waits for one of that engine's, even with CUs idle elsewhere.  So a cut whose extra
+    workgroups would wait behind long pieces loses to one that starts every workgroup at once (the reference eval's
+    p12_loaded8k_0: 18 pieces, 228 workgroups, 141 us against 21 pieces, 264 workgroups, 164 us on MI355X), and
+    one-chunk remainders that would wait are not made (p12_loaded16k_0)."""
     pl, tab = _plan([1024], 12, 256)                     # 16 chunks x 12 heads: 16 pieces of one chunk, 192 workgroups
     _check_pieces(pl, tab, [1024], 12)
     assert (pl.num_pieces, pl.num_split) == (16, 1)
     pl, tab = _plan([1600], 12, 256)                     # 25 chunks: twelve pieces of 2 and one of 1
     counts = _check_pieces(pl, tab, [1600], 12)[:, 1]
     assert sorted(counts.tolist()) == [1] + [2] * 12
-    lens = [5440, 1920, 8768]                            # the reference eval's p12_loaded16k_0 layout
+    lens = [7808, 128]                                   # p12_loaded8k_0: 122 + 2 chunks
+    pl, tab = _plan(lens, 12, 256)
+    _check_pieces(pl, tab, lens, 12)
+    assert pl.num_pieces == 18 and pl.num_chains * 12 <= 256
+    lens = [5440, 1920, 8768]                            # p12_loaded16k_0
     pl, tab = _plan(lens, 12, 256)
     counts = _check_pieces(pl, tab, lens, 12)[:, 1]
-    assert counts.min() >= 2
+    assert counts.min() >= 2 and pl.num_chains * 12 <= 256
 
 
 # the reference eval's host gate layouts (kda/mi350x/benchmark/eval_kda_mi350x.py:98-112: (new tokens, has initial
