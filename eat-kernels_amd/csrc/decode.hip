@@ -66,8 +66,12 @@ __device__ __forceinline__ bool slot_ok(int64_t r, int lo, int64_t n) { return r
 // key column).  Each slice writes bf16(o) of its rows to `out`; finish_kernel then applies the gated RMSNorm over the 128
 // rows of every (token, head) and commits the conv cache (finish_kernel; a slice cannot commit: the other slices of
 // its state may not have read the window yet).
+// Streaming-store launches (more written state than the MALL holds) are held to fewer workgroups per CU: one for spec
+// verify (2 waves per SIMD; s8_h96_b32 338 -> 322 us), two for single-token decode (4 waves per SIMD; the config-3
+// shape 193 -> 189 us, one per CU measured slower); smaller launches keep the compiler's default.
 template <bool SPEC, bool SINGLE, bool NT, int NP>
-__global__ void __launch_bounds__(DC_THREADS) decode_kernel(DecParams p) {
+__global__ void __launch_bounds__(DC_THREADS)
+    __attribute__((amdgpu_waves_per_eu(NT ? (SPEC ? 2 : 4) : 1, NT ? (SPEC ? 2 : 4) : 8))) decode_kernel(DecParams p) {
     constexpr bool PRE = !SINGLE && !NT;
     constexpr int VS = 8 / NP;  // slices per (sequence, head)
     // dynamic LDS: conv weights [4][384] fp32 | conv + SiLU outputs [S][384] fp32 | bf16-rounded outputs [S][128] fp32

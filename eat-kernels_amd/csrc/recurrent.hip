@@ -41,8 +41,12 @@ __device__ __forceinline__ bool row_ok(int64_t r, int64_t lo, int64_t slots) { r
 // the final state written back, REC_PER_TOKEN the state after every token written (spec verify).
 enum { REC_SINGLE = 0, REC_MULTI = 1, REC_PER_TOKEN_MODE = 2 };
 
+// The streaming-store instantiations (launches that write more state than the MALL holds) are held to 2 waves per
+// SIMD, one workgroup per CU: an HBM-bound stream of state rows runs faster with fewer workgroups in flight per CU
+// (config 3 179 -> 173 us, spec verify H = 64 234 -> 226 us); smaller launches keep the compiler's default.
 template <bool RAW_GATE, bool RAW_BETA, bool NORM, int MODE, bool NT>
-__global__ void __launch_bounds__(REC_THREADS) recurrent_kernel(RecParams p) {
+__global__ void __launch_bounds__(REC_THREADS) __attribute__((amdgpu_waves_per_eu(NT ? 2 : 1, NT ? 2 : 8)))
+recurrent_kernel(RecParams p) {
     constexpr bool PER_TOKEN = MODE == REC_PER_TOKEN_MODE;
     // (sequence, head) of this workgroup, kept in SGPRs: buffer descriptors built from them must be wave-uniform
     // values the compiler can see as such, or it wraps every buffer access in a waterfall loop
@@ -144,8 +148,9 @@ __global__ void __launch_bounds__(REC_THREADS) recurrent_kernel(RecParams p) {
 }
 
 // Copy one (sequence, head) state: scratch[scratch_idx[n, a-1]] -> pool[pool_idx[n]].
-template <bool NT>
-__global__ void __launch_bounds__(WK_THREADS) spec_commit_kernel(KdaSpecCommitArgs a, bool slot0) {
+template <bool NT>  // streaming form: one workgroup per CU, as recurrent_kernel (H = 64 commit 60 -> 52 us)
+__global__ void __launch_bounds__(WK_THREADS) __attribute__((amdgpu_waves_per_eu(NT ? 2 : 1, NT ? 2 : 8)))
+spec_commit_kernel(KdaSpecCommitArgs a, bool slot0) {
     const int task = xcd_task(blockIdx.x, gridDim.x);
     const int n = __builtin_amdgcn_readfirstlane(task / a.H);
     const int h = __builtin_amdgcn_readfirstlane(task - n * a.H);
