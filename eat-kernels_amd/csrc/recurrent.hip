@@ -148,9 +148,8 @@ recurrent_kernel(RecParams p) {
 }
 
 // Copy one (sequence, head) state: scratch[scratch_idx[n, a-1]] -> pool[pool_idx[n]].
-template <bool NT>  // streaming form: one workgroup per CU, as recurrent_kernel (H = 64 commit 60 -> 52 us)
-__global__ void __launch_bounds__(WK_THREADS) __attribute__((amdgpu_waves_per_eu(NT ? 2 : 1, NT ? 2 : 8)))
-spec_commit_kernel(KdaSpecCommitArgs a, bool slot0) {
+template <bool NT>
+__global__ void __launch_bounds__(WK_THREADS) spec_commit_kernel(KdaSpecCommitArgs a, bool slot0) {
     const int task = xcd_task(blockIdx.x, gridDim.x);
     const int n = __builtin_amdgcn_readfirstlane(task / a.H);
     const int h = __builtin_amdgcn_readfirstlane(task - n * a.H);
