@@ -419,8 +419,8 @@ def test_split_matches_whole_walk():
 
 @pytest.mark.parametrize("gscale", [1.0, 0.01])
 def test_split_long_scan_matches_whole_walk(gscale):
-    """A chain of many pieces: the scan composes the final state through every piece's transition (bf16 hi/lo pair
-    products), so its rounding adds up over the pieces.  With the config gates (gscale 1) a piece's transition
+    """A chain of many pieces: the scan composes the final state through every piece's transition (fp16 MFMA
+    products with the state as an fp16 hi/lo pair), so its rounding adds up over the pieces.  With the config gates (gscale 1) a piece's transition
     underflows to zero within a chunk or two; gscale 0.01 (log-decay ~ -0.007 per token and channel) keeps every
     transition and every start state live, which exercises the scan and the output fixup in full.  Outputs and final
     states against the unsplit walk of the same call."""
