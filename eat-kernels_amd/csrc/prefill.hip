@@ -45,8 +45,11 @@ namespace {
 constexpr int PF_THREADS = 512;
 
 // LDS layout (bytes).  Region A: gate / Gamma fp32 [64][132], then k^ fi fp32 [64][132].  Region B: q^ fi fp32
-// [64][132], then Q~ fp16 [64][136] and beta v fp16 [64][136].  Region C: k^ fj fp32 [64][132], then Kd^T fp16
-// [128][72].  Row paddings keep the 16-lane MFMA fragment reads and the column reads free of bank conflicts.
+// [64][132], then Q~ fp16 [64][136] and W fp16 [64][136].  Region C: k^ fj fp32 [64][132], then Kd^T fp16
+// [128][72].  The row paddings keep the scattered two-byte stores of the layouts and the column reads free of bank
+// conflicts and every MFMA fragment at a constant offset from its lane's base.  On gfx950 the 16-byte fragment reads
+// of these rows still take two LDS passes (SQ_LDS_BANK_CONFLICT); swizzled rows that read in one pass measured no
+// faster, since the kernel's phases wait on VALU issue, not on the LDS.
 constexpr int RS32 = 132;   // fp32 rows of 128
 constexpr int RS16 = 136;   // fp16 rows of 128
 constexpr int RS16S = 72;   // fp16 rows of 64
