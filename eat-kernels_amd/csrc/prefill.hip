@@ -29,11 +29,10 @@
 //       each 32-block, position 8g + 4h + e <-> index 16h + 4g + e)
 // Precision: MFMA operands are fp16 (11-bit significand) except the diagonal Gram blocks (bf16 hi/lo); fp32
 // accumulation; the state is fp32 and is rounded to fp16 only as the B operand of W S and Q~ S.  Range: fp16 holds
-// |x| < 65504 (state, U, T entries); the diagonal blocks need |Gamma_i - Gamma_m| < 88 over 8 tokens, i.e. a
-// per-token log-decay above ~ -11 (gate-in-kernel calls with lower_bound >= -11 always satisfy it).
+// |x| < 65504 (state, U, T entries); the diagonal blocks need |Gamma_i - Gamma_m| <= 72 over 8 tokens, so every
+// per-token log-decay is raised to KDA355_MIN_LOG_DECAY (-9) if it is below (clamp_decay).
 #include <algorithm>
 #include <functional>
-#include <mutex>
 #include <numeric>
 #include <vector>
 
@@ -128,6 +127,11 @@ __device__ __forceinline__ bf16x8 as_bf16x8(const uint32_t (&w)[4]) {
 }
 // 2^x (v_exp_f32)
 __device__ __forceinline__ float exp2_(float x) { return __builtin_amdgcn_exp2f(x); }
+// A per-token log-decay below KDA355_MIN_LOG_DECAY (-9) is raised to it: the diagonal Gram blocks hold e^{+-8 g} over
+// 8 tokens, inside 2^{+-104} for g >= -9, where the factors and the low halves of their bf16 pairs stay normal (the
+// MFMAs flush subnormal operands; at -11 the factors reach 2^-127).  The state change this makes is below e^{-9} =
+// 1.2e-4 of the affected channel's value (a decay of e^{-9} instead of a smaller one).  NaN passes through unchanged.
+__device__ __forceinline__ float clamp_decay(float g) { return g < KDA355_MIN_LOG_DECAY ? KDA355_MIN_LOG_DECAY : g; }
 
 // Workgroup barrier for LDS traffic only.  __syncthreads() also fences global memory (s_waitcnt vmcnt(0)), which
 // would wait for the next chunk's prefetched loads and for the output stores at every phase boundary; the waves of
@@ -446,12 +450,13 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
             const u32x4 gg[2] = {nx.g[0], nx.g[1]};
             unpack16(gg, rg);
 #pragma unroll
-            for (int c = 0; c < 16; ++c) gv[c] = (r < L) ? p.lb * sigmoidf_(Aexp * (rg[c] + sDT[16 * cb + c])) : 0.f;
+            for (int c = 0; c < 16; ++c)
+                gv[c] = (r < L) ? clamp_decay(p.lb * sigmoidf_(Aexp * (rg[c] + sDT[16 * cb + c]))) : 0.f;
         } else {
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
-                for (int j = 0; j < 4; ++j) gv[4 * i + j] = __uint_as_float(nx.g[i][j]);
+                for (int j = 0; j < 4; ++j) gv[4 * i + j] = clamp_decay(__uint_as_float(nx.g[i][j]));
         }
         const float bt = (r >= L) ? 0.f : (RB ? sigmoidf_(bf2f(nx.beta)) : __uint_as_float(nx.beta));
 #pragma unroll
@@ -1693,11 +1698,6 @@ extern "C" int kda355_prefill_launch(const KdaPrefillArgs* a, kda355_stream_t st
     const uint32_t f = a->flags;
     KDA_CHECK_ARG(a->q && a->k && a->v && a->g && a->beta && a->out && a->tables, "prefill: a required pointer is null");
     KDA_CHECK_ARG(!(f & KDA355_PF_RAW_GATE) || (a->A_log && a->dt_bias), "prefill: raw gate needs A_log and dt_bias");
-    // the in-kernel gate keeps every log-decay in [lower_bound, 0]; the diagonal Gram blocks span e^{+-8 |g|} in bf16
-    // pairs, which holds for a per-token log-decay above -11 (a given g must satisfy the same: g >= -11)
-    KDA_CHECK_ARG(!(f & KDA355_PF_RAW_GATE) || a->lower_bound >= KDA355_MIN_LOG_DECAY,
-                  "prefill: lower_bound %g is below %g (the chunk kernel's decay range)", (double)a->lower_bound,
-                  (double)KDA355_MIN_LOG_DECAY);
     const bool pool = f & KDA355_PF_POOL;
     KDA_CHECK_ARG(pool ? (a->state_pool && a->state_idx && a->has_initial_state) : (a->final_state != nullptr),
                   "prefill: pool mode needs state_pool/state_idx/has_initial_state, contiguous mode final_state");
@@ -1777,62 +1777,4 @@ extern "C" int kda355_prefill_launch(const KdaPrefillArgs* a, kda355_stream_t st
         return KDA355_ELAUNCH;
     }
     return 0;
-}
-
-// ---------------------------------------------------------------------------------------------------- no-alloc launch
-// The workspace of split layouts in a static device array instead of caller memory, for callers that cannot allocate
-// (code under graph capture with no allocator at hand, tight serving loops).  Every GPU the library runs on holds its
-// own copy of the array from the code object's load to the end of the process.  The host never uses the array's name
-// as an address: the device address of the current device's copy comes from hipGetSymbolAddress, once per device.
-// Every kernel writes each workspace word it reads earlier in the same call (the chunk kernel writes the pieces'
-// states, transitions and correction operands; the scan and compose passes read them after it), so nothing has to
-// start at zero and what an earlier call left there is never read.  Calls that overlap on one GPU (two streams, or
-// two threads) share the array and race.
-static __device__ __align__(256) unsigned char scratch[KDA355_NOALLOC_SCRATCH_BYTES];
-
-namespace {
-constexpr int MAX_DEVICES = 64;
-std::mutex g_scratch_mu;
-void* g_scratch_ptr[MAX_DEVICES] = {nullptr};
-
-// the device address of the current device's scratch copy (resolved at the first call on that device)
-int scratch_address(void** out) {
-    int dev = -1;
-    const hipError_t e0 = hipGetDevice(&dev);
-    if (e0 != hipSuccess || dev < 0 || dev >= MAX_DEVICES) {
-        set_error("prefill_noalloc: hipGetDevice failed (%s, device %d)", hipGetErrorString(e0), dev);
-        return KDA355_ELAUNCH;
-    }
-    std::lock_guard<std::mutex> lock(g_scratch_mu);
-    if (!g_scratch_ptr[dev]) {
-        void* ptr = nullptr;
-        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
-        if (e != hipSuccess || !ptr) {
-            set_error("prefill_noalloc: hipGetSymbolAddress of the static scratch failed on device %d: %s", dev,
-                      hipGetErrorString(e));
-            return KDA355_ELAUNCH;
-        }
-        g_scratch_ptr[dev] = ptr;
-    }
-    *out = g_scratch_ptr[dev];
-    return 0;
-}
-}  // namespace
-
-extern "C" int kda355_prefill_launch_noalloc(const KdaPrefillArgs* a, kda355_stream_t stream) {
-    KDA_CHECK_ARG(a && a->plan, "prefill_noalloc: null args or plan");
-    KDA_CHECK_ARG(a->plan->magic == PLAN_MAGIC, "prefill_noalloc: plan is not a kda355_prefill_plan() result");
-    KDA_CHECK_ARG(a->workspace == nullptr, "prefill_noalloc: takes no workspace (it uses the library's static scratch)");
-    KDA_CHECK_ARG(a->plan->workspace_bytes <= (int64_t)KDA355_NOALLOC_SCRATCH_BYTES,
-                  "prefill_noalloc: this layout needs %lld bytes of workspace, the static scratch holds %lld "
-                  "(use kda355_prefill_launch with a caller workspace)",
-                  (long long)a->plan->workspace_bytes, (long long)KDA355_NOALLOC_SCRATCH_BYTES);
-    KdaPrefillArgs b = *a;
-    if (a->plan->workspace_bytes > 0) {
-        void* ptr = nullptr;
-        const int rc = scratch_address(&ptr);
-        if (rc != 0) return rc;
-        b.workspace = ptr;
-    }
-    return kda355_prefill_launch(&b, stream);
 }

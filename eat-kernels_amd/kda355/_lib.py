@@ -8,6 +8,7 @@ import ctypes
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libkda355.so"
+NOALLOC_LIB_PATH = Path(__file__).resolve().parent / "libkda355_noalloc.so"
 
 P = ctypes.c_void_p
 I32 = ctypes.c_int32
@@ -91,6 +92,7 @@ class KdaPrefillArgs(ctypes.Structure):
 
 
 _lib = None
+_noalloc = None
 
 
 def lib():
@@ -113,12 +115,26 @@ def lib():
         L.kda355_prefill_workspace_bytes.restype = I64
         L.kda355_prefill_launch.argtypes = [ctypes.POINTER(KdaPrefillArgs), P]
         L.kda355_prefill_launch.restype = ctypes.c_int
-        L.kda355_prefill_launch_noalloc.argtypes = [ctypes.POINTER(KdaPrefillArgs), P]
-        L.kda355_prefill_launch_noalloc.restype = ctypes.c_int
         L.kda355_last_error.restype = ctypes.c_char_p
         L.kda355_version.restype = ctypes.c_int
         _lib = L
     return _lib
+
+
+def noalloc_lib():
+    """libkda355_noalloc.so (kda355_prefill_launch_noalloc and its static device scratch), loaded on first use only: a
+    process that never calls the no-allocation entry point never holds the scratch."""
+    global _noalloc
+    if _noalloc is None:
+        lib()
+        if not NOALLOC_LIB_PATH.exists():
+            raise RuntimeError(f"kda355: native library not built: {NOALLOC_LIB_PATH} "
+                               "(run __graft_entry__.build() or `make -C eat-kernels_amd/csrc`)")
+        L = ctypes.CDLL(str(NOALLOC_LIB_PATH))
+        L.kda355_prefill_launch_noalloc.argtypes = [ctypes.POINTER(KdaPrefillArgs), P]
+        L.kda355_prefill_launch_noalloc.restype = ctypes.c_int
+        _noalloc = L
+    return _noalloc
 
 
 def check(rc: int, what: str):
@@ -135,6 +151,9 @@ def exported_symbols():
     return ["kda355_recurrent_launch", "kda355_spec_commit_launch", "kda355_decode_launch", "kda355_prefill_plan",
             "kda355_prefill_workspace_bytes", "kda355_prefill_launch", "kda355_prefill_launch_noalloc",
             "kda355_last_error", "kda355_version"]
+
+
+NOALLOC_SYMBOLS = ("kda355_prefill_launch_noalloc",)  # exported by libkda355_noalloc.so, the rest by libkda355.so
 
 
 NOALLOC_SCRATCH_BYTES = 256 << 20  # KDA355_NOALLOC_SCRATCH_BYTES

@@ -210,7 +210,7 @@ def _launch(meta, q, k, v, gt, bt, out, flags, scale, lower_bound, A_log=None, d
     a.plan = ctypes.pointer(meta.plan)
     stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
     if static:
-        _lib.check(_lib.lib().kda355_prefill_launch_noalloc(ctypes.byref(a), stream), "prefill_noalloc")
+        _lib.check(_lib.noalloc_lib().kda355_prefill_launch_noalloc(ctypes.byref(a), stream), "prefill_noalloc")
     else:
         _lib.check(_lib.lib().kda355_prefill_launch(ctypes.byref(a), stream), "prefill")
 

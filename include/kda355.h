@@ -44,10 +44,12 @@ typedef struct ihipStream_t* kda355_stream_t; /* == hipStream_t */
 #define KDA355_ELAUNCH (-2)
 #define KDA355_HEAD_DIM 128
 #define KDA355_CHUNK 64
-/* Smallest per-token log-decay the chunked prefill accepts: its diagonal Gram blocks hold e^{+-8 g} over 8 tokens in
-   bf16 pairs.  Raw-gate launches (g = lower_bound * sigmoid(..) in [lower_bound, 0]) with lower_bound below it are
-   rejected; a given fp32 g must stay >= it. */
-#define KDA355_MIN_LOG_DECAY (-11.0f)
+/* Smallest per-token log-decay the chunked prefill uses: its diagonal Gram blocks hold e^{+-8 g} over 8 tokens, which
+   for g >= -9 stays inside 2^{+-104}, where fp32 and bf16 are normal with room for the low half of a bf16 pair (the
+   MFMAs flush subnormal operands).  A log-decay below it (given, or formed in the kernel from a lower_bound below it)
+   is raised to it, which changes the state by less than e^{-9} = 1.2e-4 of the affected channel.  The
+   reference guards the same range by recomputing overflowed slices in fp32 (kda/mi350x/kda/kernel.py:113-128). */
+#define KDA355_MIN_LOG_DECAY (-9.0f)
 
 /* ------------------------------------------------------------------------------------------------ recurrent */
 

@@ -16,9 +16,9 @@ input projection, A_log ~ U(-1, 1), dt_bias ~ N(0, 0.5^2), pool rows ~ N(0, 0.05
 bound -5, scale 128^-1/2; cold sequences' slots and checkpoint rows are poisoned with NaN (write-only).
 
 Bars: the north-star bars (output max-abs beyond bf16 rounding <= 2e-2 x RMS; written rows relative Frobenius
-<= 1e-3) plus the eval's per-sequence relative L2 <= 2e-2; for the numerics probes, which drive the operator far
-outside the configs' distributions, the eval's own bar on the pool rows (relative L2 <= 2e-2, P_RTOL).  Every byte
-outside `out` and the written rows is compared with a saved copy.
+<= 1e-3) plus the eval's per-sequence relative L2 <= 2e-2, for the contract cases and the numerics probes alike (the
+eval itself holds the probes' pool rows to relative L2 <= 2e-2, P_RTOL, twenty times looser).  Every byte outside
+`out` and the written rows is compared with a saved copy.
 """
 import random
 import zlib
@@ -222,7 +222,7 @@ def test_numerics_probe(oracle, probe):
     _say(f"numerics probe {name}: H={H} seqs={[s[0] for s in seqs]} gates={gates}")
     c = Serving(H, seqs, 31 + len(name), gates=gates)
     c.run(_kda())
-    c.verify(oracle, state_tol=P_RTOL, what=name)
+    c.verify(oracle, state_tol=STATE_TOL, what=name)
 
 
 # ------------------------------------------------------------------------------------------------ integration

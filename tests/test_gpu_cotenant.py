@@ -15,7 +15,7 @@ from test_gpu_decode import Case, _call, _check, _device_args
 
 pytestmark = pytest.mark.gpu
 HOG = Path(__file__).resolve().parent / "cotenant" / "libhog.so"
-HOG_SECONDS = 3.0
+HOG_SECONDS = 4.0  # the eval's co-tenant duration (eval_kda_mi350x.py:945)
 FINISH_S = 1.5  # the eval's bar: finished this long after launch, i.e. not waiting for the co-tenant to leave
 # p12_loaded16k_1 (kda/mi350x/benchmark/eval_kda_mi350x.py:92-115): (tokens, has_initial_state, checkpoint offset)
 P12_LOADED16K_1 = [(3008, 1, 3008), (1536, 1, 1536), (256, 1, 64), (128, 0, 0), (1600, 1, 832), (640, 1, 0),
@@ -42,19 +42,25 @@ def _beside_hog(lib, fn):
     started = torch.zeros(blocks * 64, dtype=torch.int32, device=DEV)
     side = torch.cuda.Stream(device=DEV)
     torch.cuda.synchronize()
+    t_launch = time.perf_counter()
     rc = lib.kda355_test_hog(blocks, 160 * 1024, HOG_SECONDS, ctypes.c_void_p(started.data_ptr()),
                              ctypes.c_void_p(side.cuda_stream))
     assert rc == 0, f"hog launch failed: HIP error {rc}"
-    t_wait = time.perf_counter()
-    while int(started.sum()) < blocks * 64 and time.perf_counter() - t_wait < 2.0:
+    while int(started.sum()) < blocks * 64 and time.perf_counter() - t_launch < 2.0:
         time.sleep(0.01)
     resident = int(started.sum()) // 64
     t0 = time.perf_counter()
+    left = HOG_SECONDS - (t0 - t_launch)  # co-tenant time still ahead when fn starts (an upper bound)
+    if resident != blocks or left <= FINISH_S:
+        side.synchronize()  # let the co-tenant finish before failing
+    assert resident == blocks, f"only {resident} of {blocks} co-tenant workgroups became resident"
+    assert left > FINISH_S, f"the co-tenant had only {left:.2f} s left when the call started (needs > {FINISH_S})"
     fn()
     torch.cuda.current_stream().synchronize()
     dt = time.perf_counter() - t0
     side.synchronize()
-    _say(f"{resident} of {blocks} co-tenant workgroups resident; finished {dt * 1e3:.1f} ms after launch")
+    _say(f"{resident} of {blocks} co-tenant workgroups resident, {left:.2f} s of co-tenant time left at the call; "
+         f"finished {dt * 1e3:.1f} ms after launch")
     return dt
 
 

@@ -34,13 +34,15 @@ def _check_out(got, ref, what, cu=None):
     return check_out(got, ref, what, cu)
 
 
-def _plain_case(oracle, H, lens, seed, init=True, gscale=1.0, heads_checked=None):
+def _plain_case(oracle, H, lens, seed, init=True, gscale=1.0, heads_checked=None, gmod=None):
     kda = _kda()
     _say(f"plain H={H} lens={lens[:10]} init={init} seed={seed}")
     g = gen(seed)
     T = int(sum(lens))
     q, k, v, gg, beta = config_inputs(T, H, g)
     gg = gg * gscale
+    if gmod is not None:
+        gg = gmod(gg, g)
     N = len(lens)
     h0 = torch.randn(N, H, D, D, generator=g) * 0.02 if init else None
     cu = torch.tensor(_cu(lens), dtype=torch.int32)
@@ -78,6 +80,44 @@ def test_other_head_counts(oracle):
 def test_slow_and_fast_decay(oracle):
     _plain_case(oracle, 2, [2048, 500], 20, gscale=0.01)   # long memory: cross-chunk state carries
     _plain_case(oracle, 2, [1000], 21, gscale=4.0)         # fast decay
+
+
+def test_log_decay_below_range_is_clamped(oracle):
+    """Given per-token log-decays far below KDA355_MIN_LOG_DECAY (-9): -20 and -30 on random channels and tokens (a
+    quarter of all values), on a split layout (one long sequence in many pieces) and a whole one.  The kernel raises
+    them to -9, a decay of e^-9 instead of a smaller one, which moves the state by less than 1.2e-4 of the affected
+    channel; outputs and states stay finite and within the bars of the exact fp64 oracle."""
+    def deep(gg, g):
+        pick = torch.rand(gg.shape, generator=g)
+        return torch.where(pick < 0.125, torch.full_like(gg, -20.0), torch.where(pick < 0.25, torch.full_like(gg, -30.0), gg))
+    _plain_case(oracle, 2, [6000, 300], 22, gmod=deep)
+    _plain_case(oracle, 4, [700, 1], 23, gmod=deep)
+
+
+def test_raw_gate_lower_bound_below_range(oracle):
+    """kda_prefill with lower_bound = -20 and saturated gates (dt_bias 20..30, so g = lower_bound * sigmoid(.) reaches
+    -20 on every channel): the in-kernel gate is raised to -9 like a given one, and the result matches the oracle."""
+    kda = _kda()
+    H, lens = 2, [1100, 64]
+    _say("kda_prefill lower_bound=-20, saturated gates")
+    g = gen(33)
+    T = sum(lens)
+    q, k, v, raw_g, raw_b, A_log, dt_bias = _raw_inputs(g, T, H)
+    A_log = torch.full((H,), 2.0)
+    dt_bias = torch.linspace(20.0, 30.0, D).repeat(H)
+    h0 = torch.randn(len(lens), H, D, D, generator=g) * 0.25
+    cu = torch.tensor(_cu(lens), dtype=torch.int64)
+    o, fin = kda.kda_prefill(q[None].to(DEV), k[None].to(DEV), v[None].to(DEV), raw_g[None].to(DEV),
+                             raw_b[None].to(DEV), A_log.to(DEV), dt_bias.to(DEV), h0.to(DEV), cu.to(DEV),
+                             lower_bound=-20.0)
+    torch.cuda.synchronize()
+    qn, kn, vf, gl, bt = _oracle_gated(oracle, q, k, v, raw_g, raw_b, A_log, dt_bias, lb=-20.0)
+    assert gl.min() < -19.0, "the case must drive the gate below the range"
+    ro, rf, _ = oracle.chains(qn, kn, vf, gl, bt, _cu(lens), D ** -0.5, f32(h0), precision=64)
+    _check_out(o[0], ro, "lower_bound=-20", _cu(lens))
+    for n in range(len(lens)):
+        e = rel_frob(f32(fin[n]), rf[n])
+        assert np.isfinite(f32(fin[n])).all() and e <= STATE_TOL, f"seq {n}: final state relF {e:.3e}"
 
 
 def test_config1_layout_subset_of_heads(oracle):

@@ -463,6 +463,8 @@ def test_decode_full_gated_rmsnorm(oracle):
                   o / np.sqrt(ms + eps) * nw):
         assert np.abs(got - wrong).max() > 0.3 * scale
 
+
+def test_config0_shapes(oracle):
     """Config 0 (T = 1024, H = 4, zero initial state) runs and is finite; fp32 agrees with fp64."""
     q, k, v, gg, beta = config_inputs(1024, 4, gen(0))
     o32, f32_ = oracle.prefill_plain(f32(q), f32(k), f32(v), f32(gg), f32(beta), [0, 1024], precision=32)

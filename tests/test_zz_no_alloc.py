@@ -40,20 +40,3 @@ def test_noalloc_matches_workspace_launch():
         torch.cuda.synchronize()
         assert torch.equal(o1, o2), f"call {i}: output differs from the workspace launch"
         assert torch.equal(f1, f2), f"call {i}: final states differ from the workspace launch"
-
-
-def test_noalloc_rejects_oversized_layout():
-    import kda355
-    from kda355 import _lib
-    T, H = 131072, 32                                    # config 2's layout: ~1 GB of workspace
-    meta = kda355.plan(torch.tensor([0, T]), H, device=DEV)
-    assert meta.workspace_bytes > _lib.NOALLOC_SCRATCH_BYTES
-    a = _lib.KdaPrefillArgs()
-    fake = ctypes.c_void_p(1 << 20)                      # never dereferenced: the call is rejected first
-    for f in ("q", "k", "v", "g", "beta", "out", "tables", "final_state"):
-        setattr(a, f, fake)
-    a.T, a.N, a.H = T, 1, H
-    a.plan = ctypes.pointer(meta.plan)
-    L = _lib.lib()
-    assert L.kda355_prefill_launch_noalloc(ctypes.byref(a), None) == _lib.EINVAL
-    assert b"static scratch" in L.kda355_last_error()
