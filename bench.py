@@ -716,14 +716,15 @@ def main():
                                   "mean_ratio": round(sum(x["ratio"] for x in rows) / len(rows), 3),
                                   "geomean_ratio": round(gm([x["ratio"] for x in rows]), 3), "rows": rows}
 
-    if "legacy" in cfgs:  # opt-in: the reference eval's phase-1 no-regression gates, its metric mean(recorded / ours)
+    if cfgs & {"legacy", "legacy_prefill", "legacy_decode"}:  # opt-in: the reference eval's phase-1 no-regression
+        # gates, its metric mean(recorded / ours); legacy_prefill / legacy_decode run one of the two
         prows, drows = [], []
-        for name, base_ms in LEGACY_PREFILL_BASE_MS.items():
+        for name, base_ms in (LEGACY_PREFILL_BASE_MS.items() if cfgs & {"legacy", "legacy_prefill"} else ()):
             us = bench_legacy_prefill(kda355, torch, dev, PLAIN_PREFILL[name][0], max(args.steps, 50), flush)
             prows.append({"workload": name, "us": round(us, 2), "recorded_vllm_us": round(base_ms * 1e3, 2),
                           "vs_base": round(base_ms * 1e3 / us, 3)})
             log(f"legacy prefill {name}: {us:.1f} us (recorded vLLM {base_ms * 1e3:.1f} us)")
-        for name, (H, B, S, base) in LEGACY_DECODE.items():
+        for name, (H, B, S, base) in (LEGACY_DECODE.items() if cfgs & {"legacy", "legacy_decode"} else ()):
             us = bench_legacy_decode(kda355, torch, dev, name, H, B, S, max(args.steps, 100), flush)
             drows.append({"workload": name, "H": H, "B": B, "S": S, "us": round(us, 2), "recorded_best_baseline_us": base,
                           "vs_base": round(base / us, 3)})
@@ -731,8 +732,8 @@ def main():
         extra["legacy"] = {
             "method": "the reference eval's phase-1 gates (eval_kda_mi350x.py:979-1098): single calls / graph replays "
                       "after a 512 MiB cache flush, median; metric mean(recorded / ours)",
-            "prefill_mean_vs_base": round(sum(x["vs_base"] for x in prows) / len(prows), 3),
-            "decode_mean_vs_base": round(sum(x["vs_base"] for x in drows) / len(drows), 3),
+            "prefill_mean_vs_base": round(sum(x["vs_base"] for x in prows) / len(prows), 3) if prows else None,
+            "decode_mean_vs_base": round(sum(x["vs_base"] for x in drows) / len(drows), 3) if drows else None,
             "reference_mean_vs_base": LEGACY_REFERENCE_MEAN, "floors": {"prefill": 0.932, "decode": 1.5},
             "prefill_rows": prows, "decode_rows": drows}
 

@@ -48,9 +48,11 @@ struct DecParams {
     uint16_t* out;            // [T, dim] bf16, row stride out_rs
     int64_t x_rs, gate_rs, beta_rs, og_rs, out_rs;
     int64_t conv_ss, conv_ts, conv_slots, ssm_ss, ssm_slots;
+    int32_t* ws;              // sliced launches: counters [pairs] int32, then partial sums [pairs][VS][DC_MAX_S] fp32
     int B, S, H;
     float eps, lb, scale;
 };
+constexpr int DC_WS_PART = 256;  // byte offset of the partial sums (after DC_SLICE_CUS / 4 counters)
 
 __device__ __forceinline__ bool slot_ok(int64_t r, int lo, int64_t n) { return r >= lo && r < n; }
 
@@ -60,12 +62,15 @@ __device__ __forceinline__ bool slot_ok(int64_t r, int lo, int64_t n) { return r
 // in series); launches that stream more state than the MALL holds are bound by HBM, and there the extra phase and
 // the higher occupancy its smaller register set allows measured 1-3 % slower, so they form them per token.
 //
-// NP < 8 (small launches): the state rows are split over 8 / NP workgroups per (sequence, head), slice vs holding
-// rows 16 NP vs .. 16 NP (vs + 1) - 1 (NP rows per lane), so a token's step is 8 / NP times shorter and 8 / NP times
-// more CUs walk.  Every slice forms the conv and the q / k / gate operands of all 128 channels (the walk needs every
-// key column).  Each slice writes bf16(o) of its rows to `out`; finish_kernel then applies the gated RMSNorm over the 128
-// rows of every (token, head) and commits the conv cache (finish_kernel; a slice cannot commit: the other slices of
-// its state may not have read the window yet).
+// NP < 8 (small launches, given a workspace): the state rows are split over VS = 8 / NP workgroups per (sequence,
+// head), slice vs holding rows 16 NP vs .. 16 NP (vs + 1) - 1 (NP rows per lane), so a token's step is 8 / NP times
+// shorter and 8 / NP times more CUs walk.  Every slice forms the conv and the q / k / gate operands of all 128 channels
+// (the walk needs every key column).  Each slice writes bf16(o) of its rows to `out` and its per-token partial sums of
+// squares to the workspace, then counts itself in the (sequence, head)'s counter (one vector atomic, no waiting); the
+// slice that arrives last applies the gated RMSNorm to the 128 rows of every token, commits the conv cache (every
+// slice has read the window by then) and sets the counter back to zero, so the workspace is all-zero counters again
+// after every launch.  A slice cannot commit on its own: the other slices of its state may not have read the window
+// yet.
 // Streaming-store launches (more written state than the MALL holds) are held to fewer workgroups per CU: one for spec
 // verify (2 waves per SIMD; s8_h96_b32 338 -> 322 us), two for single-token decode (4 waves per SIMD; the config-3
 // shape 193 -> 189 us, one per CU measured slower); smaller launches keep the compiler's default.
@@ -166,9 +171,8 @@ __global__ void __launch_bounds__(DC_THREADS)
 #pragma unroll
     for (int k = 0; k < OG_PER; ++k) {
         const int i = min(tid + k * DC_THREADS, S * D - 1);
-        ogv[k] = NP < 8 ? 0u
-                        : __builtin_amdgcn_raw_buffer_load_b16(
-                              row_rsrc(p.og + ((int64_t)n * S + (i >> 7)) * p.og_rs + h * D, D * 2), 2 * (i & 127), 0, 0);
+        ogv[k] = __builtin_amdgcn_raw_buffer_load_b16(row_rsrc(p.og + ((int64_t)n * S + (i >> 7)) * p.og_rs + h * D, D * 2),
+                                                      2 * (i & 127), 0, 0);
     }
     const float nw = p.nw[tid & (D - 1)];
     const float A = __expf(p.A_log[h]);
@@ -198,8 +202,9 @@ __global__ void __launch_bounds__(DC_THREADS)
         for (int tap = 0; tap < 4; ++tap) acc += bf2f(sWin[(t + tap) * DC_CH + c]) * sCw[tap * DC_CH + c];
         sX[i] = acc * sigmoidf_(acc);
     }
-    if (NP == 8) {  // (sliced launches commit in finish_kernel, after every slice has read the window)
-        // spec: taps [0, 2 + S) <- window[1 .. 3 + S);  plain: taps [0, 3) <- window[S .. S + 3)
+    // conv cache commit from the window in LDS; spec: taps [0, 2 + S) <- window[1 .. 3 + S);  plain: taps [0, 3) <-
+    // window[S .. S + 3)
+    auto conv_commit = [&]() {
         const int ntap = SPEC ? 2 + S : 3, first = SPEC ? 1 : S;
 #pragma unroll 1
         for (int i = tid; i < ntap * (DC_CH / 8); i += DC_THREADS) {
@@ -208,7 +213,9 @@ __global__ void __launch_bounds__(DC_THREADS)
             *reinterpret_cast<u32x4*>(crow + (int64_t)r * p.conv_ts + (int64_t)grpc * dim + h * D + ci) =
                 *reinterpret_cast<const u32x4*>(&sWin[(first + r) * DC_CH + c8]);
         }
-    }
+    };
+    if constexpr (NP == 8) conv_commit();  // (a sliced launch commits in its last slice, after every slice has read
+                                           // the window)
     lds_barrier();  // sX complete
     if (PRE) {
         // the per-token operands that do not depend on the state, formed before the walk (wave w takes tokens w and
@@ -270,8 +277,15 @@ __global__ void __launch_bounds__(DC_THREADS)
             const float ss = sum32(wk.c < 8 ? ob * ob : 0.f);
             if (wk.c < 8) sO[t * D + wk.row(wk.c)] = ob;
             if (wk.c == 0) sRed[t * 16 + 2 * wk.w + wk.half] = ss;
-        } else {  // bf16(o) of the slice's rows straight to `out`; finish_kernel finishes them
-            if (wk.c < NP) p.out[((int64_t)n * S + t) * p.out_rs + h * D + row0 + wk.row(wk.c)] = (uint16_t)f2bf(o);
+        } else {  // bf16(o) of the slice's rows straight to `out` and the half wave's sum of squares; the last slice
+                  // finishes them
+            const uint32_t o16 = f2bf(o);
+            if (wk.c < NP)
+                __hip_atomic_store(p.out + ((int64_t)n * S + t) * p.out_rs + h * D + row0 + wk.row(wk.c), (uint16_t)o16,
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const float ob = bf2f(o16);
+            const float ss = sum32(wk.c < NP ? ob * ob : 0.f);
+            if (wk.c == 0) sRed[t * 16 + 2 * wk.w + wk.half] = ss;
         }
         if (SPEC) {
             const int64_t wr = __builtin_amdgcn_readlane(wr_l, t);
@@ -280,7 +294,43 @@ __global__ void __launch_bounds__(DC_THREADS)
         }
     }
     if (!SPEC) store_state<NT, NP>(wk, p.ssm + rd * p.ssm_ss + slice, st);
-    if constexpr (NP < 8) return;
+    if constexpr (NP < 8) {
+        // The rows and sums the slices exchange are written and read with device-scope (coherent) accesses: the
+        // slices of one head may sit on different XCDs, whose L2s are not coherent with each other, and a full L2
+        // write-back (a device-scope fence) costs the whole launch several microseconds after a cache flush.
+        float* part = reinterpret_cast<float*>(reinterpret_cast<unsigned char*>(p.ws) + DC_WS_PART);
+        lds_barrier();  // sRed complete
+        if (tid < S) {
+            const f32x4* r4 = reinterpret_cast<const f32x4*>(sRed + tid * 16);
+            const f32x4 s4 = (r4[0] + r4[1]) + (r4[2] + r4[3]);
+            __hip_atomic_store(part + ((int64_t)nh * VS + vs) * DC_MAX_S + tid, (s4.x + s4.y) + (s4.z + s4.w),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads();  // every thread's coherent stores have completed (the barrier waits for them)
+        int* s_arrive = reinterpret_cast<int*>(sKB);  // (k . q, beta) are dead after the walk
+        if (tid == 0) s_arrive[0] = __hip_atomic_fetch_add(p.ws + nh, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        if (s_arrive[0] != VS - 1) return;  // workgroup-uniform: the last slice to arrive finishes the head
+#pragma unroll
+        for (int k = 0; k < OG_PER; ++k) {
+            const int i = tid + k * DC_THREADS;
+            if (i < S * D) {
+                const int t = i >> 7;
+                float ss = 0.f;
+#pragma unroll
+                for (int j = 0; j < VS; ++j)
+                    ss += __hip_atomic_load(part + ((int64_t)nh * VS + j) * DC_MAX_S + t, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT);
+                const float rstd = __frsqrt_rn(ss * (1.f / D) + p.eps);
+                uint16_t* o = p.out + ((int64_t)n * S + t) * p.out_rs + h * D + (i & 127);
+                const uint16_t x = __hip_atomic_load(o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                *o = (uint16_t)f2bf(bf2f(x) * rstd * ogw[k]);
+            }
+        }
+        conv_commit();
+        if (tid == 0) p.ws[nh] = 0;  // the next launch starts from a zero counter
+        return;
+    }
     lds_barrier();
     // ---- gated RMSNorm of every token's 128 outputs: y = bf16(o) rsqrt(mean(bf16(o)^2) + eps) nw sigmoid(og)
 #pragma unroll
@@ -297,92 +347,6 @@ __global__ void __launch_bounds__(DC_THREADS)
                                                   2 * (i & 127), 0, 0);
         }
     }
-}
-
-// Read row, conv row and accepted length of sequence n under decode_kernel's slot rules; false for a dead sequence
-// (read or conv row is padding), whose output rows are zero.
-template <bool SPEC>
-__device__ __forceinline__ bool seq_slots(const DecParams& p, int n, int& a, int64_t& rd, int64_t& cs) {
-    a = 1;
-    if (SPEC) {
-        a = p.acc[n];
-        a = a < 1 ? 1 : (a > p.S ? p.S : a);
-        rd = p.idx[(int64_t)n * p.S + a - 1];
-        cs = p.idx[(int64_t)n * p.S];
-    } else {
-        rd = p.idx[n];
-        cs = rd;
-    }
-    return slot_ok(rd, 1, p.ssm_slots) && slot_ok(cs, 1, p.conv_slots);
-}
-
-// The gated RMSNorm after a sliced decode (finish_kernel): y = x rsqrt(mean(x^2) + eps) nw sigmoid(og) over the 128 values x = bf16(o)
-// of one (token, head) row of `out` (one wave per row, two values per lane), in place.  A dead sequence's rows were
-// written as zeros by the slices and are left alone (rescaling them would turn a NaN out_gate or a negative weight
-// into NaN or -0).
-constexpr int NM_THREADS = 256;
-template <bool SPEC>
-__device__ __forceinline__ void norm_rows(const DecParams& p, int blk, int rows) {
-    const int row = blk * (NM_THREADS / 64) + (threadIdx.x >> 6);  // (token, head): token-major
-    if (row >= rows) return;  // wave-uniform
-    const int l = threadIdx.x & 63, t = row / p.H, h = row - t * p.H;
-    {
-        int a;
-        int64_t rd, cs;
-        if (!seq_slots<SPEC>(p, t / p.S, a, rd, cs)) return;  // wave-uniform
-    }
-    uint32_t* o = reinterpret_cast<uint32_t*>(p.out + (int64_t)t * p.out_rs + h * D) + l;
-    const uint32_t xo = *o;
-    // out_gate and norm_weight element by element: the launch checks neither for more than their element alignment
-    const uint16_t* og = p.og + (int64_t)t * p.og_rs + h * D + 2 * l;
-    const float x0 = bf2f(xo & 0xffffu), x1 = bf2f(xo >> 16);
-    const float rstd = __frsqrt_rn(sum64(x0 * x0 + x1 * x1) * (1.f / D) + p.eps);
-    *o = f2bf(x0 * rstd * p.nw[2 * l] * sigmoidf_(bf2f(og[0]))) |
-         (f2bf(x1 * rstd * p.nw[2 * l + 1] * sigmoidf_(bf2f(og[1]))) << 16);
-}
-
-// The conv cache commit of a sliced decode (finish_kernel), one workgroup per (sequence, head), with the slot and liveness rules of
-// decode_kernel: spec taps [0, 2 + S) <- window rows [1, 3 + S), plain taps [0, 3) <- window rows [S, S + 3), where
-// window row r < 3 is history tap start + r and row r >= 3 is input row r - 3.  Every piece is read before any is
-// written (the commit shifts the slot's own taps).
-constexpr int CC_THREADS = NM_THREADS;
-template <bool SPEC>
-__device__ __forceinline__ void conv_commit(const DecParams& p, int blk) {
-    const int n = blk / p.H, h = blk - n * p.H, S = p.S, dim = p.H * D;
-    int a;
-    int64_t rd, cs;
-    if (!seq_slots<SPEC>(p, n, a, rd, cs)) return;
-    const int start = SPEC ? a - 1 : 0, ntap = SPEC ? 2 + S : 3, first = SPEC ? 1 : S;
-    uint16_t* crow = p.conv + cs * p.conv_ss;
-    constexpr int PER = ((2 + DC_MAX_S) * (DC_CH / 8) + CC_THREADS - 1) / CC_THREADS;
-    const int npieces = ntap * (DC_CH / 8);
-    u32x4 v[PER];
-#pragma unroll
-    for (int k = 0; k < PER; ++k) {
-        const int i = min((int)threadIdx.x + CC_THREADS * k, npieces - 1);
-        const int r = first + i / (DC_CH / 8), c8 = (i % (DC_CH / 8)) * 8;
-        const int64_t col = (int64_t)(c8 / D) * dim + h * D + c8 % D;
-        const uint16_t* src =
-            (r < 3) ? crow + (int64_t)(start + r) * p.conv_ts + col : p.x + ((int64_t)n * S + (r - 3)) * p.x_rs + col;
-        v[k] = *reinterpret_cast<const u32x4*>(src);
-    }
-    __syncthreads();  // every read is complete before the first write
-#pragma unroll
-    for (int k = 0; k < PER; ++k) {
-        const int i = threadIdx.x + CC_THREADS * k;
-        if (i < npieces) {
-            const int r = i / (DC_CH / 8), c8 = (i % (DC_CH / 8)) * 8;
-            *reinterpret_cast<u32x4*>(crow + (int64_t)r * p.conv_ts + (int64_t)(c8 / D) * dim + h * D + c8 % D) = v[k];
-        }
-    }
-}
-// One launch after a sliced decode: workgroups [0, nnorm) run norm_rows, the rest commit one (sequence, head) each.
-template <bool SPEC>
-__global__ void __launch_bounds__(NM_THREADS) finish_kernel(DecParams p, int rows, int nnorm) {
-    if ((int)blockIdx.x < nnorm)
-        norm_rows<SPEC>(p, blockIdx.x, rows);
-    else
-        conv_commit<SPEC>(p, blockIdx.x - nnorm);
 }
 
 bool aligned(const void* q, size_t a) { return (reinterpret_cast<uintptr_t>(q) % a) == 0; }
@@ -443,29 +407,25 @@ extern "C" int kda355_decode_launch(const KdaDecodeArgs* a, kda355_stream_t stre
     p.H = a->H;
     p.eps = a->norm_eps;
     p.lb = a->lower_bound;
+    p.ws = static_cast<int32_t*>(a->workspace);
     p.scale = 0.08838834764831845f;  // 128^-1/2: the reference scales the normalized q
     const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const size_t lds = ((size_t)(4 + a->S) * DC_CH + (size_t)a->S * (2 * D + 18)) * sizeof(float) +
                        (size_t)(3 + a->S) * DC_CH * sizeof(uint16_t);
     const bool nt = (long long)a->B * (spec ? a->S : 1) * a->H * D * D * 4 >= DC_STREAM_BYTES;
-    // small multi-token launches split each state over 4 workgroups (32 rows each) while the slices fit one per CU, so
-    // that more CUs walk and each token's step is shorter; the gated RMSNorm then runs as a second kernel.  (Halves of
-    // 64 rows for launches of up to 128 pairs measured no faster than whole states: s8_h96_b1 27.5 against 27.1 us.)
-    // A single-token launch keeps whole states: its one step is short, and the second kernel cost more than slicing
-    // saved (d_k3_b1 17.0 -> 15.8 us, d_glm16_b1 17.0 -> 15.9 us unsliced).
+    // Small launches split each state over 4 workgroups (32 rows each) while the slices fit one per CU, so that more
+    // CUs walk and each token's step is shorter; the last slice of each (sequence, head) finishes its rows, which needs
+    // the caller's workspace (without one, whole states).  (Halves of 64 rows for launches of up to 128 pairs measured
+    // no faster than whole states: s8_h96_b1 27.5 against 27.1 us.)
     const int64_t pairs = (int64_t)a->B * a->H;
-    const int np = (!nt && a->S > 1 && 4 * pairs <= DC_SLICE_CUS) ? 2 : 8;
+    const int np = (a->workspace && !nt && 4 * pairs <= DC_SLICE_CUS) ? 2 : 8;
     void (*kernel)(DecParams) =
-        np == 2 ? (spec ? decode_kernel<true, false, false, 2> : decode_kernel<false, false, false, 2>)
+        np == 2 ? (spec ? decode_kernel<true, false, false, 2>
+                        : a->S == 1 ? decode_kernel<false, true, false, 2> : decode_kernel<false, false, false, 2>)
         : spec ? (nt ? decode_kernel<true, false, true, 8> : decode_kernel<true, false, false, 8>)
         : a->S == 1 ? (nt ? decode_kernel<false, true, true, 8> : decode_kernel<false, true, false, 8>)
                     : (nt ? decode_kernel<false, false, true, 8> : decode_kernel<false, false, false, 8>);
     hipLaunchKernelGGL(kernel, dim3(a->B * a->H * (8 / np)), dim3(DC_THREADS), lds, s, p);
-    if (np < 8) {
-        const int rows = a->B * a->S * a->H, nnorm = (rows + NM_THREADS / 64 - 1) / (NM_THREADS / 64);
-        hipLaunchKernelGGL(spec ? finish_kernel<true> : finish_kernel<false>, dim3(nnorm + a->B * a->H), dim3(NM_THREADS),
-                           0, s, p, rows, nnorm);
-    }
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         set_error("decode: launch failed: %s", hipGetErrorString(e));

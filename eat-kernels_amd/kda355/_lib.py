@@ -57,6 +57,7 @@ class KdaDecodeArgs(ctypes.Structure):
         ("ssm_slots", I64),
         ("B", I32), ("S", I32), ("H", I32), ("conv_taps", I32),
         ("norm_eps", F32), ("lower_bound", F32), ("flags", U32), ("reserved", I32),
+        ("workspace", P),
     ]
 
 

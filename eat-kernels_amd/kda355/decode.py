@@ -15,6 +15,13 @@ rows must be dense).  Slot rows <= 0 are padding (zero output rows, nothing writ
 Errors follow the reference validator (kda/mi350x/kda/decode/kernel_v13_a.py:697-735): TypeError for a wrong dtype or
 device, ValueError for a wrong shape or stride.  Nothing data dependent is checked on the host, so the call is
 capturable in a HIP graph.
+
+Small launches (B * H <= 64) split each state over 4 workgroups, which needs a workspace of KDA355_DECODE_WS_BYTES
+whose counters (its first 256 bytes) are zero before its first launch; every launch leaves them zero.  The keyword
+`workspace` selects it: by default
+the device's own (zeroed once, on the first call outside graph capture; a call captured before any eager call runs
+whole states), None for whole states, or a caller's uint8 tensor.  Launches that may run at the same time on one GPU
+(several streams) must not share a workspace.
 """
 from __future__ import annotations
 
@@ -26,6 +33,22 @@ from . import _lib
 
 D = 128
 MAX_S = 16
+WS_BYTES = 16640  # KDA355_DECODE_WS_BYTES
+_DEFAULT = object()
+_ws_by_device = {}
+
+
+def default_workspace(device):
+    """The device's default decode workspace (zeroed when first made), or None while a graph is being captured and
+    there is none yet (making one then would record its zeroing into the graph)."""
+    key = torch.device(device).index if torch.device(device).index is not None else torch.cuda.current_device()
+    ws = _ws_by_device.get(key)
+    if ws is None:
+        if torch.cuda.is_current_stream_capturing():
+            return None
+        ws = torch.zeros(WS_BYTES, dtype=torch.uint8, device=torch.device("cuda", key))
+        _ws_by_device[key] = ws
+    return ws
 
 
 def _chk(name, t, dtype, shape, device, rows_only=False):
@@ -45,16 +68,16 @@ def _slot_stride(t, per_slot):
 
 
 def decode(mixed_qkv, conv_state, conv_weight, gate, beta, out_gate, A_log, dt_bias, norm_weight, ssm_state,
-           state_indices, num_accepted_tokens, cu_seqlens, norm_eps, lower_bound, out):
+           state_indices, num_accepted_tokens, cu_seqlens, norm_eps, lower_bound, out, *, workspace=_DEFAULT):
     if not isinstance(cu_seqlens, torch.Tensor):
         raise TypeError("kda355 decode: cu_seqlens must be a tensor")
     return decode_batch(mixed_qkv, conv_state, conv_weight, gate, beta, out_gate, A_log, dt_bias, norm_weight,
                         ssm_state, state_indices, num_accepted_tokens, cu_seqlens.numel() - 1, norm_eps, lower_bound,
-                        out)
+                        out, workspace=workspace)
 
 
 def decode_batch(mixed_qkv, conv_state, conv_weight, gate, beta, out_gate, A_log, dt_bias, norm_weight, ssm_state,
-                 state_indices, num_accepted_tokens, B, norm_eps, lower_bound, out):
+                 state_indices, num_accepted_tokens, B, norm_eps, lower_bound, out, *, workspace=_DEFAULT):
     """decode() with the batch size B given directly (only the length of cu_seqlens is ever used: every sequence has
     the same S = T / B tokens)."""
     if not isinstance(mixed_qkv, torch.Tensor) or mixed_qkv.dim() != 2:
@@ -103,6 +126,13 @@ def decode_batch(mixed_qkv, conv_state, conv_weight, gate, beta, out_gate, A_log
                          f"got {num_accepted_tokens.dtype} {tuple(num_accepted_tokens.shape)}")
     idx = state_indices.contiguous()
     acc = num_accepted_tokens.contiguous() if spec else None
+    if workspace is _DEFAULT:
+        workspace = default_workspace(dev)
+    elif workspace is not None:
+        if not isinstance(workspace, torch.Tensor) or workspace.device != dev:
+            raise TypeError(f"kda355 decode: workspace must be a tensor on {dev}")
+        if not workspace.is_contiguous() or workspace.numel() * workspace.element_size() < WS_BYTES:
+            raise ValueError(f"kda355 decode: workspace must be contiguous with >= {WS_BYTES} bytes")
 
     a = _lib.KdaDecodeArgs()
     a.mixed_qkv, a.conv_state, a.conv_weight = mixed_qkv.data_ptr(), conv_state.data_ptr(), conv_weight.data_ptr()
@@ -120,6 +150,7 @@ def decode_batch(mixed_qkv, conv_state, conv_weight, gate, beta, out_gate, A_log
     a.B, a.S, a.H = B, S, H
     a.norm_eps, a.lower_bound = float(norm_eps), float(lower_bound)
     a.flags = 0
+    a.workspace = workspace.data_ptr() if workspace is not None else None
     stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
     _lib.check(_lib.lib().kda355_decode_launch(ctypes.byref(a), stream), "decode")
     return out

@@ -155,7 +155,17 @@ typedef struct KdaDecodeArgs {
     float norm_eps, lower_bound;
     uint32_t flags;             /* 0 */
     int32_t reserved;
+    void* workspace;            /* NULL, or KDA355_DECODE_WS_BYTES of device memory whose first 256 bytes (the
+                                   counters) are zero before the first launch: launches of at most 64 (sequence, head)
+                                   pairs (B * H) then split each state over 4 workgroups, the last of which finishes the
+                                   head's outputs.  Each such launch leaves the counters zero again (the rest is
+                                   written before it is read); launches that may run at the same time on one GPU need
+                                   workspaces of their own.  No counterpart in the reference's decode entry (its
+                                   single-launch small-batch kernel is kda/mi350x/kda/decode/kda_v14_b.cu:1856-). */
 } KdaDecodeArgs;
+
+/* Bytes of the decode workspace: 64 int32 counters, then 64 x 4 x 16 fp32 partial sums of squares. */
+#define KDA355_DECODE_WS_BYTES 16640
 
 int kda355_decode_launch(const KdaDecodeArgs* args, kda355_stream_t stream);
 

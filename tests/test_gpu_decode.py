@@ -141,9 +141,9 @@ def _device_args(c, dev):
     return d
 
 
-def _call(kda, d):
+def _call(kda, d, **kw):
     return kda.decode(d["mixed"], d["conv"], d["conv_weight"], d["gate"], d["beta"], d["out_gate"], d["A_log"],
-                      d["dt_bias"], d["norm_weight"], d["ssm"], d["idx"], d["acc"], d["cu"], NORM_EPS, LB, d["out"])
+                      d["dt_bias"], d["norm_weight"], d["ssm"], d["idx"], d["acc"], d["cu"], NORM_EPS, LB, d["out"], **kw)
 
 
 def _check(c, d, O, tag=""):
@@ -174,12 +174,12 @@ def _check(c, d, O, tag=""):
         assert torch.equal(raw[mask], c.raw[mask]), f"{tag}page padding changed"
 
 
-def _run(oracle, **kw):
+def _run(oracle, call_kw=None, **kw):
     import kda355
-    _say("decode " + " ".join(f"{k}={v}" for k, v in kw.items()))
+    _say("decode " + " ".join(f"{k}={v}" for k, v in kw.items()) + (f" {list(call_kw)}" if call_kw else ""))
     c = Case(**kw)
     d = _device_args(c, torch.device("cuda", 0))
-    _call(kda355, d)
+    _call(kda355, d, **(call_kw or {}))
     torch.cuda.synchronize()
     _check(c, d, oracle)
     return c, d
@@ -198,9 +198,9 @@ def test_plain_decode_padding_slot(oracle):
 
 
 def test_sliced_decode_dead_rows_stay_zero(oracle):
-    """Multi-token launches of at most 64 (sequence, head) pairs split each state over 4 workgroups and finish the
-    gated RMSNorm in a second kernel.  Dead sequences (padding read or conv row) with NaN out_gate rows and negative
-    norm weights: their output rows stay +0, as in the whole-state path (single-token launches, below)."""
+    """Launches of at most 64 (sequence, head) pairs split each state over 4 workgroups, the last of which finishes
+    the gated RMSNorm of the head.  Dead sequences (padding read or conv row) with NaN out_gate rows and negative norm
+    weights: their output rows stay +0, as in the whole-state path."""
     _run(oracle, B=6, S=2, H=2, seed=15, spec=False, pad=[(1,), (4,)], hostile_dead=True)
     _run(oracle, B=6, S=1, H=2, seed=17, spec=False, pad=[(1,), (4,)], hostile_dead=True)
     _run(oracle, B=6, S=3, H=2, seed=16, spec=True, pad=[(2, 0), (3, 1)], hostile_dead=True)
@@ -232,10 +232,24 @@ def test_spec_verify_streaming_size(oracle):
 
 
 def test_spec_verify_whole_state_workgroups(oracle):
-    """A launch above the slicing size (9 x 32 = 288 > 64 (sequence, head) pairs): one workgroup per whole state and
-    the gated RMSNorm inside the decode kernel (the launches of at most 64 pairs above split each state over 4
-    workgroups of 32 rows and finish the norm in a second kernel)."""
+    """A launch above the slicing size (9 x 32 = 288 > 64 (sequence, head) pairs): one workgroup per whole state (the
+    launches of at most 64 pairs above split each state over 4 workgroups of 32 rows)."""
     _run(oracle, B=9, S=4, H=32, seed=13, spec=True, pages=False)
+
+
+def test_sliced_decode_workspace(oracle):
+    """A caller's workspace: two sliced launches in a row share it and leave its counters (the first 256 bytes) zero
+    (the last slice of every (sequence, head) resets its counter), and the same calls without a workspace run whole
+    states; all against the oracle."""
+    import importlib
+    dec = importlib.import_module("kda355.decode")
+    dev = torch.device("cuda", 0)
+    ws = torch.zeros(dec.WS_BYTES, dtype=torch.uint8, device=dev)
+    for spec, S in ((False, 1), (False, 3), (True, 4)):
+        for rep in range(2):
+            _run(oracle, call_kw={"workspace": ws}, B=5, S=S, H=3, seed=40 + 2 * S + rep, spec=spec)
+            assert int(ws[:256].count_nonzero()) == 0, f"workspace counters not zero after spec={spec} S={S} call {rep}"
+        _run(oracle, call_kw={"workspace": None}, B=5, S=S, H=3, seed=60 + S, spec=spec)
 
 
 def test_plain_decode_whole_state_workgroups(oracle):
