@@ -92,8 +92,23 @@ def read_traffic(name):
 
 
 # ------------------------------------------------------------------------------------------------ timing helpers
+SETTLE_MS = 30.0  # untimed calls before the warmup, whatever --warmup is: an idle GPU runs its first ~15 ms slow
+
+
+def settle(fn, torch, ms=SETTLE_MS):
+    """Untimed calls until at least `ms` of wall time has passed, synchronized: the clocks of an idle GPU ramp up over
+    the first ~15 ms of work (config-1 calls run ~10 % slower there), so no timed region starts inside the ramp."""
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < ms:
+        fn()
+        torch.cuda.synchronize()
+
+
 def time_steps(fn, steps, warmup, torch):
-    """W untimed calls, then K calls bracketed by synchronize; HIP events on the current (launch) stream."""
+    """Clock settling (SETTLE_MS, outside the timed region), W untimed calls, then K calls bracketed by synchronize;
+    HIP events on the current (launch) stream."""
+    settle(fn, torch)
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -606,8 +621,8 @@ def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    # default W = 50: an idle MI355X needs a few tens of ms under load to reach its clocks (the first ~15 ms of
-    # config-1 calls run ~10 % slower); an explicit --warmup W is honoured as given
+    # W untimed calls after the clock settling (SETTLE_MS of untimed calls, done whatever W is: an idle MI355X needs
+    # ~15 ms under load to reach its clocks, and the first config-1 calls run ~10 % slower)
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--configs", default="c1,c3,c4,d1,c2")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -748,7 +763,8 @@ def main():
     traffic = read_traffic("prefill_c1_c2_split.md")
     line = {
         "metric": METRIC, "value": round(c1["T"] / s, 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": round(c1["ms"], 4), "higher_is_better": True, "scaling": "weak",
+        "warmup": args.warmup, "clock_settle_ms": SETTLE_MS, "ms_per_step": round(c1["ms"], 4),
+        "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "fp16-mfma/fp32-state (bf16 io)", "data": "synthetic",
         "config": {"workload": "configs[1]: chunk_kda plain call, 8 varlen sequences (lengths U[256,8192] seed 1: "
                                f"{c1['lens']}), T={c1['T']}, H=32, D=128, bf16 q/k/v, fp32 g/beta, fp32 initial "
