@@ -303,7 +303,13 @@ __device__ __forceinline__ void copy_staged_h(half_t* dst, const float* stage) {
 // flagged PIECE_FIX starts from S = 0 and also carries its state transition P (S_end = P S_start + S_loc); its outputs
 // are partial (fp16, without the S_start term), and for every chunk it stores R = Q~ P + A_qk (-W P), the operand of
 // the correction O += scale R S_start; its checkpoints go to the workspace as (S_loc, P) pairs.
-template <bool RG, bool P1>
+// PREC = true (KDA355_PF_PRECISE) carries five operands of the solve and the state update as fp16 pairs (hi = RNE(x),
+// lo = RNE(x - hi): 22 bits) instead of single fp16 values: -A_IJ, T_II, the solved blocks X_J, the right-hand side
+// before T_II, and V' (-W P for a transition).  On chunks of nearly parallel keys with beta ~ 1 the substitution
+// cancels, and these single roundings set the state error: the reference eval's deep-layer probe measures 9.3e-4
+// relative Frobenius with single operands and 4.9e-4 with the pairs; config 1 takes ~11 % longer (more MFMAs in the
+// dependent chain of the solve, twice as many in the state update).
+template <bool RG, bool P1, bool PREC>
 __global__ void __launch_bounds__(PF_THREADS, 1)
     chunk_kernel(PfParams p, const int32_t* __restrict__ tab, const int32_t* __restrict__ ck_idx, int list_off) {
     extern __shared__ __align__(16) unsigned char lds[];
@@ -626,7 +632,13 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
                 }
                 if (g == 0) {
 #pragma unroll
-                    for (int ii = 0; ii < 16; ++ii) sAk[(16 * I + ii) * RS16S + 16 * I + m] = (half_t)x[ii];
+                    for (int ii = 0; ii < 16; ++ii) {
+                        const half_t hi = (half_t)x[ii];
+                        sAk[(16 * I + ii) * RS16S + 16 * I + m] = hi;
+                        // PREC: the low part in the A_qk block (I / 2, 2 + I % 2), a block of rows 0..31 and columns
+                        // 32..63 that the walk never reads and the Gram phase never writes
+                        if (PREC) sAq[(16 * (I >> 1) + ii) * RS16S + 32 + 16 * (I & 1) + m] = (half_t)(x[ii] - (float)hi);
+                    }
                 }
             }
         } else {
@@ -675,10 +687,17 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
             for (int t = 0; t < 2; ++t) {
                 if (t < nJ) {
                     const int J = J0 + t;
-                    f16x4 ak, aq;
+                    f16x4 ak, al, aq;
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) { ak[e] = (half_t)(nb * akk[t][e]); aq[e] = (half_t)aqk[t][e]; }
+                    for (int e = 0; e < 4; ++e) {
+                        const float x = nb * akk[t][e];
+                        ak[e] = (half_t)x;
+                        al[e] = (half_t)(x - (float)ak[e]);
+                        aq[e] = (half_t)aqk[t][e];
+                    }
                     *reinterpret_cast<f16x4*>(&sAk[i * RS16S + 16 * J + 4 * g]) = ak;
+                    // PREC: the low part goes to the unused mirrored block (J, I) of the same array
+                    if (PREC) *reinterpret_cast<f16x4*>(&sAk[(16 * J + m) * RS16S + 16 * I + 4 * g]) = al;
                     *reinterpret_cast<f16x4*>(&sAq[i * RS16S + pos64(16 * J + 4 * g)]) = aq;
                 }
             }
@@ -733,6 +752,12 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
         {
             const int c = 16 * w + m;
             f32x4 Xw[4];
+            // PREC: -A_IJ, T_II, the solved blocks X_J and the right-hand side before T_II as fp16 pairs
+            f16x4 Xh[4], Xl[4], Uh[4], Ul[4];
+            auto split4 = [](const f32x4& x, f16x4& hi, f16x4& lo) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) { hi[e] = (half_t)x[e]; lo[e] = (half_t)(x[e] - (float)hi[e]); }
+            };
 #pragma unroll
             for (int I = 0; I < 4; ++I) {
                 const float xI = sF[(F_X + I) * 128 + c];
@@ -746,19 +771,34 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
 #pragma unroll
                 for (int J = 0; J < I; ++J) {
                     const f16x4 A = *reinterpret_cast<const f16x4*>(&sAk[(16 * I + m) * RS16S + 16 * J + 4 * g]);
-                    f16x4 bw, bu;
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) { bw[e] = (half_t)Xw[J][e]; bu[e] = (half_t)Ur[J][e]; }
-                    aw = mfma16(A, bw, aw);
-                    au = mfma16(A, bu, au);
+                    const f16x4 Al = PREC ? *reinterpret_cast<const f16x4*>(&sAk[(16 * J + m) * RS16S + 16 * I + 4 * g])
+                                          : f16x4{};
+                    aw = mfma16(A, Xh[J], aw);
+                    au = mfma16(A, Uh[J], au);
+                    if (PREC) {
+                        aw = mfma16(A, Xl[J], aw);
+                        au = mfma16(A, Ul[J], au);
+                        aw = mfma16(Al, Xh[J], aw);
+                        au = mfma16(Al, Uh[J], au);
+                    }
                 }
                 const f16x4 T = *reinterpret_cast<const f16x4*>(&sAk[(16 * I + m) * RS16S + 16 * I + 4 * g]);
-                f16x4 bw, bu;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) { bw[e] = (half_t)aw[e]; bu[e] = (half_t)au[e]; }
+                f16x4 bwh, bwl, buh, bul;
+                split4(aw, bwh, bwl);
+                split4(au, buh, bul);
                 const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-                Xw[I] = mfma16(T, bw, z);
-                Ur[I] = mfma16(T, bu, z);
+                Xw[I] = mfma16(T, bwh, z);
+                Ur[I] = mfma16(T, buh, z);
+                if (PREC) {
+                    const f16x4 Tl = *reinterpret_cast<const f16x4*>(&sAq[(16 * (I >> 1) + m) * RS16S + 32 + 16 * (I & 1) +
+                                                                            4 * g]);
+                    Xw[I] = mfma16(Tl, bwh, mfma16(T, bwl, Xw[I]));
+                    Ur[I] = mfma16(Tl, buh, mfma16(T, bul, Ur[I]));
+                }
+                if (I < 3) {
+                    split4(Xw[I], Xh[I], Xl[I]);
+                    split4(Ur[I], Uh[I], Ul[I]);
+                }
             }
             const int pc = 32 * (c >> 5) + pos32(c & 31);
 #pragma unroll
@@ -796,7 +836,7 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
 #pragma unroll
                 for (int e = 0; e < 4; ++e) { Vp[it][e] = Ur[it][e] - acc[e]; Wp[it][e] = -acp[e]; }
             }
-            f16x8 VB[2], WB[2];
+            f16x8 VB[2], WB[2], VL[2], WL[2];  // V' and -W P; PREC: also their low parts (fp16 pairs)
 #pragma unroll
             for (int s = 0; s < 2; ++s)
 #pragma unroll
@@ -805,6 +845,10 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
                     VB[s][4 + e] = (half_t)Vp[2 * s + 1][e];
                     WB[s][e] = (half_t)Wp[2 * s][e];
                     WB[s][4 + e] = (half_t)Wp[2 * s + 1][e];
+                    VL[s][e] = (half_t)(Vp[2 * s][e] - (float)VB[s][e]);
+                    VL[s][4 + e] = (half_t)(Vp[2 * s + 1][e] - (float)VB[s][4 + e]);
+                    WL[s][e] = (half_t)(Wp[2 * s][e] - (float)WB[s][e]);
+                    WL[s][4 + e] = (half_t)(Wp[2 * s + 1][e] - (float)WB[s][4 + e]);
                 }
             // partial O^T = S^T Q~^T + V'^T A_qk^T (fp16, to `out`) and R^T = P^T Q~^T + W'^T A_qk^T (to the workspace),
             // transposed tiles sharing the Q~ and A_qk fragments: lane (g, m) holds token 16 it + m, columns
@@ -844,6 +888,10 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
                     const f16x8 A = *reinterpret_cast<const f16x8*>(&sKd[(16 * dt + (m ^ dt)) * RS16S + 32 * s + 8 * g]);
                     S[dt] = mfma32(A, VB[s], S[dt]);
                     Pm[dt] = mfma32(A, WB[s], Pm[dt]);
+                    if (PREC) {
+                        S[dt] = mfma32(A, VL[s], S[dt]);
+                        Pm[dt] = mfma32(A, WL[s], Pm[dt]);
+                    }
                 }
             }
         } else {
@@ -865,13 +913,15 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
 #pragma unroll
                 for (int e = 0; e < 4; ++e) Vp[it][e] = Ur[it][e] - acc[e];
             }
-            f16x8 VB[2];
+            f16x8 VB[2], VL[2];  // V'; PREC: also its low part (an fp16 pair)
 #pragma unroll
             for (int s = 0; s < 2; ++s)
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     VB[s][e] = (half_t)Vp[2 * s][e];
                     VB[s][4 + e] = (half_t)Vp[2 * s + 1][e];
+                    VL[s][e] = (half_t)(Vp[2 * s][e] - (float)VB[s][e]);
+                    VL[s][4 + e] = (half_t)(Vp[2 * s + 1][e] - (float)VB[s][4 + e]);
                 }
             // O^T = S^T Q~^T + V'^T A_qk^T: the same fragments with the MFMA operands swapped give the transposed tile, so
             // lane (g, m) holds token 16 it + m, values 16 w + 4 g .. + 3 and stores them to `out` with one 8-byte store
@@ -898,9 +948,11 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
 #pragma unroll
                 for (int e = 0; e < 4; ++e) S[dt][e] *= d4[e];
 #pragma unroll
-                for (int s = 0; s < 2; ++s)
-                    S[dt] = mfma32(*reinterpret_cast<const f16x8*>(&sKd[(16 * dt + (m ^ dt)) * RS16S + 32 * s + 8 * g]), VB[s],
-                                   S[dt]);
+                for (int s = 0; s < 2; ++s) {
+                    const f16x8 A = *reinterpret_cast<const f16x8*>(&sKd[(16 * dt + (m ^ dt)) * RS16S + 32 * s + 8 * g]);
+                    S[dt] = mfma32(A, VB[s], S[dt]);
+                    if (PREC) S[dt] = mfma32(A, VL[s], S[dt]);
+                }
             }
         }
         // checkpoints at chunk boundaries, counted in chunks of the whole sequence
@@ -1348,18 +1400,23 @@ __global__ void __launch_bounds__(FX_THREADS) __attribute__((amdgpu_waves_per_eu
         ck_body(p, tab, lds, b - nscan - nfix, (int)gridDim.x - nscan - nfix);
 }
 
-template <bool RG, bool P1>
+template <bool RG, bool P1, bool PREC>
 hipError_t launch_chunk(const PfParams& p, int list_off, int entries, hipStream_t s) {
     static bool attr_set = false;  // idempotent; a race only repeats the call
     if (!attr_set) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&chunk_kernel<RG, P1>),
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&chunk_kernel<RG, P1, PREC>),
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, LDS_TOTAL);
         if (e != hipSuccess) return e;
         attr_set = true;
     }
-    hipLaunchKernelGGL((chunk_kernel<RG, P1>), dim3(entries * p.H), dim3(PF_THREADS), LDS_TOTAL, s, p, p.tab, p.ck_idx,
-                       list_off);
+    hipLaunchKernelGGL((chunk_kernel<RG, P1, PREC>), dim3(entries * p.H), dim3(PF_THREADS), LDS_TOTAL, s, p, p.tab,
+                       p.ck_idx, list_off);
     return hipGetLastError();
+}
+template <bool P1>
+hipError_t launch_chunk_any(const PfParams& p, bool rg, bool prec, int list_off, int entries, hipStream_t s) {
+    return rg ? (prec ? launch_chunk<true, P1, true>(p, list_off, entries, s) : launch_chunk<true, P1, false>(p, list_off, entries, s))
+              : (prec ? launch_chunk<false, P1, true>(p, list_off, entries, s) : launch_chunk<false, P1, false>(p, list_off, entries, s));
 }
 template <typename K>
 hipError_t launch_composer(K kernel, const PfParams& p, int entries, int threads, int smem, hipStream_t s,
@@ -1754,13 +1811,14 @@ extern "C" int kda355_prefill_launch(const KdaPrefillArgs* a, kda355_stream_t st
     p.ws = static_cast<float*>(a->workspace);
     const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const bool rg = (f & KDA355_PF_RAW_GATE) != 0;
+    const bool prec = (f & KDA355_PF_PRECISE) != 0;
     const int off_final = H_WORDS;
     hipError_t e = hipSuccess;
     if (pl->num_split > 0) {
         // one chunk launch for every piece (first pieces from their true start states, later pieces from zero with their
         // transitions), then the start / final states of the split sequences, the later pieces' outputs and their
         // checkpoints
-        e = rg ? launch_chunk<true, true>(p, off_final, pl->num_chains, s) : launch_chunk<false, true>(p, off_final, pl->num_chains, s);
+        e = launch_chunk_any<true>(p, rg, prec, off_final, pl->num_chains, s);
         // every split sequence has >= 2 pieces, so the most-cut one has at most num_pieces - 2 (num_split - 1)
         const bool lean = pl->num_pieces - 2 * (pl->num_split - 1) <= 3;
         if (pl->num_pieces == 2 * pl->num_split) {  // every split sequence in 2 pieces: the scan joins the tail launch
@@ -1770,7 +1828,7 @@ extern "C" int kda355_prefill_launch(const KdaPrefillArgs* a, kda355_stream_t st
             if (e == hipSuccess) e = launch_tail(p, 0, pl->num_fix_tasks, pl->num_ck_tasks, s);
         }
     } else {
-        e = rg ? launch_chunk<true, false>(p, off_final, pl->num_chains, s) : launch_chunk<false, false>(p, off_final, pl->num_chains, s);
+        e = launch_chunk_any<false>(p, rg, prec, off_final, pl->num_chains, s);
     }
     if (e != hipSuccess) {
         set_error("prefill: launch failed: %s", hipGetErrorString(e));

@@ -38,6 +38,7 @@ PF_RAW_BETA = 4
 PF_POOL = 8
 PF_CK_SINGLE = 16
 PF_CK_EVERY = 32
+PF_PRECISE = 64  # KDA355_PF_PRECISE: the solve's and state update's fp16 operands as fp16 pairs (precise=True)
 
 
 def _ptr(t):
@@ -333,7 +334,7 @@ def chunk_kda(q, k, v, g, beta, scale=None, initial_state=None, output_final_sta
               use_qk_l2norm_in_kernel=True, use_gate_in_kernel=False, use_beta_sigmoid_in_kernel=False,
               A_log=None, dt_bias=None, lower_bound=-5.0, state_v_first=True, meta=None, out=None, workspace=None,
               *, ssm_state_indices=None, state_checkpoints=None, checkpoint_cu_starts=None,
-              checkpoint_every_n_tokens=0, checkpoint_state_indices=None, **unused):
+              checkpoint_every_n_tokens=0, checkpoint_state_indices=None, precise=False, **unused):
     """fla chunk_kda plain call. q, k, v [1, T, H, 128] bf16; g [1, T, H, 128] (fp32 log-decay, or the raw gate with
     use_gate_in_kernel); beta [1, T, H] (fp32 activated, or logits with use_beta_sigmoid_in_kernel); initial_state
     [N, H, 128(V), 128(K)] fp32 or None; cu_seqlens [N+1] (None: one sequence).  meta: a plan(...) result for this
@@ -349,7 +350,9 @@ def chunk_kda(q, k, v, g, beta, scale=None, initial_state=None, output_final_sta
           checkpoint_cu_starts int64 [N+1] (row checkpoint_cu_starts[i] + j = state before token j*n of sequence i,
           j < ceil(len_i / n)) or checkpoint_state_indices int32 [>= rows] (the r-th such state, sequence-major, goes to
           row checkpoint_state_indices[r]); bf16 rows are the fp32 states rounded to nearest even.
-    With checkpoints the call returns (o, final_state, state_checkpoints)."""
+    With checkpoints the call returns (o, final_state, state_checkpoints).
+    precise=True (no counterpart in fla): the kernel carries the solve's and the state update's fp16 operands as fp16
+    pairs, which about halves the state error on chunks of nearly parallel keys with beta ~ 1 at ~11 % more time."""
     if not state_v_first:
         raise ValueError("kda355: only the value-first state layout [N, H, V, K] is supported (state_v_first=True)")
     dev, T, H = _check_qkv(q, k, v)
@@ -359,6 +362,8 @@ def chunk_kda(q, k, v, g, beta, scale=None, initial_state=None, output_final_sta
                                             A_log, dt_bias)
     if use_qk_l2norm_in_kernel:
         flags |= PF_NORMALIZE_QK
+    if precise:
+        flags |= PF_PRECISE
     out, final, ck, _ = _run_plain(q, k, v, g, beta, scale, initial_state, cu_seqlens, lower_bound, meta, out,
                                    workspace, flags, A_log, dt_bias, ssm_state_indices, state_checkpoints,
                                    checkpoint_cu_starts, checkpoint_every_n_tokens, checkpoint_state_indices)
@@ -369,10 +374,11 @@ def chunk_kda(q, k, v, g, beta, scale=None, initial_state=None, output_final_sta
 
 def kda_prefill(q, k, v, raw_g, raw_beta, A_log, dt_bias, initial_state, cu_seqlens=None, scale=None,
                 lower_bound=-5.0, meta=None, *, ssm_state_indices=None, state_checkpoints=None,
-                checkpoint_cu_starts=None, checkpoint_every_n_tokens=0, checkpoint_state_indices=None):
+                checkpoint_cu_starts=None, checkpoint_every_n_tokens=0, checkpoint_state_indices=None, precise=False):
     """kda/mi350x_plain/kda_mi350x.py:37-46 (gates, beta sigmoid and q/k norm in the kernel) with the B200 serving
     keywords of chunk_kda (kda/b200/kda_b200.py:15-24).  raw_g [1, T, H, 128] bf16, raw_beta [1, T, H] bf16 logits,
-    A_log [H], dt_bias [H*128] fp32.  Returns (output, final_state) or (output, final_state, state_checkpoints)."""
+    A_log [H], dt_bias [H*128] fp32.  precise: as chunk_kda.  Returns (output, final_state) or (output, final_state,
+    state_checkpoints)."""
     dev, T, H = _check_qkv(q, k, v)
     if scale is None:
         scale = D ** -0.5
@@ -380,7 +386,8 @@ def kda_prefill(q, k, v, raw_g, raw_beta, A_log, dt_bias, initial_state, cu_seql
     _need("raw_beta", raw_beta, torch.bfloat16, dev)
     g, beta, A_log, dt_bias, flags = _gates(dev, T, H, raw_g, raw_beta, True, True, A_log, dt_bias)
     out, final, ck, _ = _run_plain(q, k, v, g, beta, scale, initial_state, cu_seqlens, lower_bound, meta, None, None,
-                                   flags | PF_NORMALIZE_QK, A_log, dt_bias, ssm_state_indices, state_checkpoints,
+                                   flags | PF_NORMALIZE_QK | (PF_PRECISE if precise else 0), A_log, dt_bias,
+                                   ssm_state_indices, state_checkpoints,
                                    checkpoint_cu_starts, checkpoint_every_n_tokens, checkpoint_state_indices)
     return (out, final, ck) if ck is not None else (out, final)
 
@@ -406,10 +413,11 @@ def prefill_prepare(cu_seqlens, num_heads, checkpoint_offsets=None, checkpoint_s
 
 def prefill(q, k, v, raw_g, raw_beta, A_log, dt_bias, scale, lower_bound, state_cache, state_indices,
             has_initial_state, cu_seqlens, out, checkpoint_offsets=None, checkpoint_state_indices=None, meta=None,
-            workspace=None):
+            workspace=None, *, precise=False):
     """kda/mi350x/kda/kernel.py:131-147 (contract kda/mi350x/CONTRACT.md:32-50).  In place: writes `out` and the pool
     rows state_indices[n] (final states) and checkpoint_state_indices[n] (state after checkpoint_offsets[n] tokens);
-    nothing else.  No host synchronization when meta is given."""
+    nothing else.  No host synchronization when meta is given.  precise: as chunk_kda (no counterpart in the
+    reference)."""
     dev, T, H = _check_qkv(q, k, v)
     if meta is None:
         meta = prefill_prepare(cu_seqlens, H, checkpoint_offsets, checkpoint_state_indices, dev)
@@ -434,7 +442,7 @@ def prefill(q, k, v, raw_g, raw_beta, A_log, dt_bias, scale, lower_bound, state_
     ck_given = checkpoint_offsets is not None and checkpoint_state_indices is not None
     if meta.any_ck and not ck_given:
         raise ValueError("kda355: meta was prepared with checkpoints but no checkpoint tensors were passed")
-    flags = PF_NORMALIZE_QK | PF_RAW_GATE | PF_RAW_BETA
+    flags = PF_NORMALIZE_QK | PF_RAW_GATE | PF_RAW_BETA | (PF_PRECISE if precise else 0)
     ck_pool = ck_idx = None
     if ck_given and meta.any_ck:
         _need("checkpoint_state_indices", checkpoint_state_indices, torch.int32, dev)

@@ -183,6 +183,9 @@ int kda355_decode_launch(const KdaDecodeArgs* args, kda355_stream_t stream);
 #define KDA355_PF_CK_EVERY 32u     /* every-n checkpoints: row j of sequence n (j < ceil(len_n / ck_every)) is the state
                                       before token j * ck_every, stored to ck_pool[ck_idx[row_start_n + j]] with
                                       row_start_n = sum of the earlier sequences' row counts (kda/b200/kda_b200.py:19-22) */
+#define KDA355_PF_PRECISE 64u      /* the solve's and the state update's fp16 operands as fp16 pairs (22 bits): about half
+                                      the state error on chunks of nearly parallel keys with beta ~ 1, ~11 % more time.
+                                      No counterpart in the reference (its prefill precision is fixed). */
 
 /* Host-side plan input: the layout only (never the data). */
 typedef struct KdaPrefillPlanIn {

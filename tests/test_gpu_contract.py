@@ -120,12 +120,12 @@ class Serving:
         self.written = sorted(set(self.sidx.tolist()) | {int(c) for c in self.cidx.tolist() if c >= 0})
         self.snap = (self.raw if self.raw is not None else self.ssm).clone()
 
-    def run(self, kda, meta_none=False):
+    def run(self, kda, meta_none=False, precise=False):
         cu_cpu = torch.tensor(self.cu, dtype=torch.int32)
         meta = None if meta_none else kda.prefill_prepare(cu_cpu, self.H, self.ck_off, self.cidx, device=DEV)
         kda.prefill(self.q, self.k, self.v, self.raw_g, self.raw_b, self.A_log, self.dt_bias, SCALE, LB, self.ssm,
                     self.sidx.to(DEV), torch.tensor(self.hinit, dtype=torch.bool, device=DEV), cu_cpu.to(DEV),
-                    self.out, self.ck_off.to(DEV), self.cidx.to(DEV), meta=meta)
+                    self.out, self.ck_off.to(DEV), self.cidx.to(DEV), meta=meta, precise=precise)
         torch.cuda.synchronize()
         return meta
 
@@ -218,11 +218,26 @@ _PROBES = [
 
 @pytest.mark.parametrize("probe", _PROBES, ids=[p[0] for p in _PROBES])
 def test_numerics_probe(oracle, probe):
+    """Written pool rows at the north-star state bar (1e-3); the worst, deep_layer, measures 9.3e-4."""
     name, H, seqs, gates = probe
     _say(f"numerics probe {name}: H={H} seqs={[s[0] for s in seqs]} gates={gates}")
     c = Serving(H, seqs, 31 + len(name), gates=gates)
     c.run(_kda())
     c.verify(oracle, state_tol=STATE_TOL, what=name)
+
+
+PRECISE_STATE_TOL = 0.5 * STATE_TOL
+
+
+@pytest.mark.parametrize("probe", _PROBES, ids=[p[0] for p in _PROBES])
+def test_numerics_probe_precise(oracle, probe):
+    """precise=True (fp16-pair operands in the solve and the state update): every probe's written rows at half the
+    north-star bar (5e-4); deep_layer measures 4.9e-4 there."""
+    name, H, seqs, gates = probe
+    _say(f"numerics probe (precise) {name}: H={H} seqs={[s[0] for s in seqs]} gates={gates}")
+    c = Serving(H, seqs, 31 + len(name), gates=gates)
+    c.run(_kda(), precise=True)
+    c.verify(oracle, state_tol=PRECISE_STATE_TOL, what=f"{name} (precise)")
 
 
 # ------------------------------------------------------------------------------------------------ integration

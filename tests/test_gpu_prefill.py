@@ -34,9 +34,9 @@ def _check_out(got, ref, what, cu=None):
     return check_out(got, ref, what, cu)
 
 
-def _plain_case(oracle, H, lens, seed, init=True, gscale=1.0, heads_checked=None, gmod=None):
+def _plain_case(oracle, H, lens, seed, init=True, gscale=1.0, heads_checked=None, gmod=None, precise=False):
     kda = _kda()
-    _say(f"plain H={H} lens={lens[:10]} init={init} seed={seed}")
+    _say(f"plain H={H} lens={lens[:10]} init={init} seed={seed}" + (" precise" if precise else ""))
     g = gen(seed)
     T = int(sum(lens))
     q, k, v, gg, beta = config_inputs(T, H, g)
@@ -47,7 +47,8 @@ def _plain_case(oracle, H, lens, seed, init=True, gscale=1.0, heads_checked=None
     h0 = torch.randn(N, H, D, D, generator=g) * 0.02 if init else None
     cu = torch.tensor(_cu(lens), dtype=torch.int32)
     o, fin = kda.chunk_kda(q[None].to(DEV), k[None].to(DEV), v[None].to(DEV), gg[None].to(DEV), beta[None].to(DEV),
-                           initial_state=h0.to(DEV) if init else None, output_final_state=True, cu_seqlens=cu.to(DEV))
+                           initial_state=h0.to(DEV) if init else None, output_final_state=True, cu_seqlens=cu.to(DEV),
+                           precise=precise)
     torch.cuda.synchronize()
     hs = list(range(H)) if heads_checked is None else heads_checked
     sel = lambda x: np.ascontiguousarray(f32(x)[:, hs])  # noqa: E731
@@ -66,6 +67,13 @@ def test_config0_single_sequence(oracle):
 
 def test_varlen_with_initial_states(oracle):
     _plain_case(oracle, 4, [300, 64, 1, 1000, 77], 1)
+
+
+def test_precise_mode_whole_and_split(oracle):
+    """precise=True (fp16-pair operands in the solve and the state updates) on whole sequences and on a layout cut
+    into pieces (later pieces carry their transition, whose update takes the pair too), against the fp64 oracle."""
+    _plain_case(oracle, 4, [300, 64, 1, 1000, 77], 1, precise=True)
+    _plain_case(oracle, 2, [8192, 300], 70, precise=True)
 
 
 def test_ragged_tiny_and_empty(oracle):
