@@ -34,6 +34,7 @@
 #include <algorithm>
 #include <functional>
 #include <numeric>
+#include <queue>
 #include <vector>
 
 #include "common.h"
@@ -81,7 +82,7 @@ constexpr uint32_t PLAN_MAGIC = 0x4b443535u;  // "KD55"
 // after the chunk kernel); the fixup list holds one task per group of up to FX_GROUP chunks of a later piece (their
 // outputs get R S_start added); the compose list holds the checkpoints inside later pieces (row = P S_start + S_local).
 enum { H_MAGIC = 0, H_N, H_T, H_NCHUNK, H_EVERY, H_CKROWS, H_OFF_FINAL, H_NFINAL, H_OFF_FIX, H_NFIX, H_OFF_SCAN,
-       H_NSCAN, H_NSLOTS, H_OFF_CKC, H_NCKC, H_NRSLOTS, H_NCKSLOTS, H_WORDS = 20 };
+       H_NSCAN, H_NSLOTS, H_OFF_CKC, H_NCKC, H_NRSLOTS, H_NCKSLOTS, H_OFF_WG, H_WORDS = 20 };
 // one piece entry: chunks [0, nch) starting at sequence chunk `first` of sequence n, tokens [t_start, t_start + len)
 enum { C_SEQ = 0, C_NCH, C_TSTART, C_LEN, C_CKSINGLE, C_CKROW0, C_FIRST, C_FLAGS, C_SLOT, C_SEQCH, C_RBASE, C_CKWS,
        C_CKWS1, C_WORDS = 13 };
@@ -299,6 +300,16 @@ __device__ __forceinline__ void copy_staged_h(half_t* dst, const float* stage) {
     }
 }
 
+// One item of a chunk-kernel workgroup: a (chain entry, head) pair's table words, and for pool layouts the state row
+// and the aligned word holding has_initial_state[n]; alog = A_log[h] for the gate-in-kernel form.
+struct ItemWords {
+    int h, n, nch, tstart, len, first, pflags, slot, seqch, ck_row0, ck_single_raw;
+    const int32_t* e;  // the chain entry (the later-piece words are read where they are used)
+    int64_t row;
+    uint32_t hword;
+    float alog;
+};
+
 // The chunk walk with outputs, checkpoints and states.  P1 = true compiles in the pieces of split sequences: an entry
 // flagged PIECE_FIX starts from S = 0 and also carries its state transition P (S_end = P S_start + S_loc); its outputs
 // are partial (fp16, without the S_start term), and for every chunk it stores R = Q~ P + A_qk (-W P), the operand of
@@ -331,24 +342,74 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
     float* sDT = reinterpret_cast<float*>(lds + LDS_DT);
 
     const int H = p.H;
-    const int ci = blockIdx.x / H;
-    const int h = blockIdx.x - ci * H;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
-    // uniform table reads through a __restrict__ pointer: scalar loads, which never join the vector-memory counter that
-    // the prefetched rows are waited on with
-    const int32_t* chain = tab + list_off + C_WORDS * ci;
-    const int n = chain[C_SEQ], nch = chain[C_NCH], tstart = chain[C_TSTART], len = chain[C_LEN];
-    const int first = chain[C_FIRST], pflags = chain[C_FLAGS], slot = chain[C_SLOT], seqch = chain[C_SEQCH];
-    const bool fix = P1 && (pflags & PIECE_FIX);
-    const int every = tab[H_EVERY];
-    const int64_t ws_arr = (int64_t)tab[H_NSLOTS] * H * D * D;  // floats per workspace array
-    const int64_t ck_words = (int64_t)tab[H_NCKSLOTS];
-    float* ws_h = p.ws + ((int64_t)slot * H + h) * D * D;        // this piece-head in array 0 (+ ws_arr: 1, 2)
-    float* ws_ck = p.ws + 3 * ws_arr;                            // checkpoint (S_loc, P) pairs
-    half_t* ws_r = reinterpret_cast<half_t*>(ws_ck + ck_words * 2 * H * D * D);  // R operands
+    // The workgroup's items (item = chain entry * H + head): item blockIdx.x alone, or, when the table holds workgroup
+    // lists (unsplit layouts with more (chain, head) pairs than CUs), the items of list blockIdx.x in turn.  An item's
+    // table words are read when the item before it starts; its first rows and gate dt_bias are fetched during the
+    // last chunk of the item before it, and its start state right after that item's final state is stored, so only a
+    // workgroup's first item pays the start-up of loading rows and state.
+    // Uniform table reads through a __restrict__ pointer are scalar loads, which never join the vector-memory counter
+    // that the prefetched rows are waited on with.
+    const int32_t* wl = nullptr;
+    int kpos = 0, kend = 1;
+    if (!P1 && tab[H_OFF_WG] > 0) {
+        wl = tab + tab[H_OFF_WG];
+        kpos = wl[blockIdx.x];
+        kend = wl[blockIdx.x + 1];
+    }
     const bool pool = (p.flags & KDA355_PF_POOL) != 0;
     const bool RB = (p.flags & KDA355_PF_RAW_BETA) != 0;
     const bool NORM = (p.flags & KDA355_PF_NORMALIZE_QK) != 0;
+    auto load_item = [&](int kp) {
+        ItemWords it;
+        const int item = wl ? wl[gridDim.x + 1 + kp] : (int)blockIdx.x;
+        const int c = item / H;
+        it.h = item - c * H;
+        const int32_t* e = tab + list_off + C_WORDS * c;
+        it.n = e[C_SEQ];
+        it.nch = e[C_NCH];
+        it.tstart = e[C_TSTART];
+        it.len = e[C_LEN];
+        it.first = e[C_FIRST];
+        it.pflags = e[C_FLAGS];
+        it.slot = e[C_SLOT];
+        it.seqch = e[C_SEQCH];
+        it.ck_row0 = e[C_CKROW0];
+        it.ck_single_raw = e[C_CKSINGLE];
+        it.e = e;
+        it.row = -1;
+        it.hword = 0;
+        if (pool) {
+            // the pool row and has_initial_state[n] in one round: the flag by a scalar read of its aligned word through
+            // the constant address space (read-only for the kernel; a uniform address there becomes s_load_dword, so
+            // no vector load has to be waited for).  The aligned word may cover bytes next to the flag but never
+            // leaves the flag's page.
+            typedef const __attribute__((address_space(4))) uint32_t cword_t;
+            typedef const __attribute__((address_space(4))) int32_t cint_t;
+            it.row = *reinterpret_cast<cint_t*>(reinterpret_cast<uintptr_t>(p.state_idx + it.n));
+            it.hword = *reinterpret_cast<cword_t*>(reinterpret_cast<uintptr_t>(p.has_init + it.n) & ~(uintptr_t)3);
+        }
+        typedef const __attribute__((address_space(4))) float cfloat_t;
+        it.alog = RG ? *reinterpret_cast<cfloat_t*>(reinterpret_cast<uintptr_t>(p.A_log + it.h)) : 0.f;
+        return it;
+    };
+    // the start state's source: none for a later piece (it runs from zero) and for a pool sequence without an initial
+    // state; S is loaded through a descriptor of no records when there is none
+    auto state_source = [&](const ItemWords& it) -> const float* {
+        if (P1 && (it.pflags & PIECE_FIX)) return nullptr;
+        if (pool) {
+            const uintptr_t ha = reinterpret_cast<uintptr_t>(p.has_init + it.n);
+            const bool hinit = ((it.hword >> (8 * (ha & 3))) & 0xffu) != 0;
+            return (it.row >= 0 && it.row < p.state_slots && hinit)
+                       ? p.state_pool + it.row * p.state_ss + (int64_t)it.h * D * D : nullptr;
+        }
+        return p.init_state ? p.init_state + ((int64_t)it.n * H + it.h) * D * D : nullptr;
+    };
+    const int every = tab[H_EVERY];
+    const int64_t ws_arr = (int64_t)tab[H_NSLOTS] * H * D * D;  // floats per workspace array
+    const int64_t ck_words = (int64_t)tab[H_NCKSLOTS];
+    float* ws_ck = p.ws + 3 * ws_arr;                            // checkpoint (S_loc, P) pairs
+    half_t* ws_r = reinterpret_cast<half_t*>(ws_ck + ck_words * 2 * H * D * D);  // R operands
 
     // ---- prologue.  Loads are issued in the order they are needed and none sits under a branch (the memory counter
     // completes in issue order, and a load on one path only makes the compiler wait for everything older): the first
@@ -360,70 +421,33 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
     // initial state is issued last and only waited for before the first walk.  Every table word the loop uses is read
     // here (empty asm operands pin the reads in the first round), so the first LDS barrier has no scalar read left to
     // wait for.
-    typedef const __attribute__((address_space(4))) float cfloat_t;
-    const float dtb = RG ? p.dt_bias[h * D + (tid & (D - 1))] : 0.f;
-    const float alog = RG ? *reinterpret_cast<cfloat_t*>(reinterpret_cast<uintptr_t>(p.A_log + h)) : 0.f;
-    const int ck_row0 = chain[C_CKROW0], ck_single_raw = chain[C_CKSINGLE];
-    asm volatile("" ::"s"(every), "s"(ws_arr), "s"(ck_row0), "s"(ck_single_raw), "s"(ck_words), "s"(alog), "s"(p.ws));
+    ItemWords cur = load_item(kpos);
+    float dtb = RG ? p.dt_bias[cur.h * D + (tid & (D - 1))] : 0.f;
+    asm volatile("" ::"s"(every), "s"(ws_arr), "s"(cur.ck_row0), "s"(cur.ck_single_raw), "s"(ck_words), "s"(cur.alog),
+                 "s"(p.ws));
     RawRow nx;
-    load_row<RG>(p, h, tstart, nch > 0 ? min(64, len) : 0, r, cb, RB, nx);  // an empty sequence loads nothing
-    // initial state (lane: v = 16w + m, k = 16dt + 4g + e), through a descriptor of no records when there is none
-    const float* src = nullptr;
-    int64_t row = -1;
-    uint32_t hword = 0;
-    const uintptr_t ha = reinterpret_cast<uintptr_t>(p.has_init + n);
-    if (pool) {
-        // the pool row and has_initial_state[n] in one round: the flag by a scalar read of its aligned word through
-        // the constant address space (read-only for the kernel; a uniform address there becomes s_load_dword, so no
-        // vector load has to be waited for).  The aligned word may cover bytes next to the flag but never leaves the
-        // flag's page.
-        typedef const __attribute__((address_space(4))) uint32_t cword_t;
-        typedef const __attribute__((address_space(4))) int32_t cint_t;
-        row = *reinterpret_cast<cint_t*>(reinterpret_cast<uintptr_t>(p.state_idx + n));
-        hword = *reinterpret_cast<cword_t*>(ha & ~(uintptr_t)3);
-    }
-    if (fix) {
-        // a later piece's local run starts from zero
-    } else if (pool) {
-        const bool hinit = ((hword >> (8 * (ha & 3))) & 0xffu) != 0;
-        if (row >= 0 && row < p.state_slots && hinit) src = p.state_pool + row * p.state_ss + (int64_t)h * D * D;
-    } else if (p.init_state) {
-        src = p.init_state + ((int64_t)n * H + h) * D * D;
-    }
+    // an empty sequence loads nothing
+    load_row<RG>(p, cur.h, cur.tstart, cur.nch > 0 ? min(64, cur.len) : 0, r, cb, RB, nx);
     f32x4 S[8];
-    {
+    // initial state (lane: v = 16w + m, k = 16dt + 4g + e)
+    auto load_start_state = [&](const float* src) {
         // base and size taken through readfirstlane: a descriptor the compiler cannot see as wave-uniform becomes a
         // waterfall loop
         const int nrec = __builtin_amdgcn_readfirstlane(src ? D * D * 4 : 0);
         const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
             uniform_ptr(src ? static_cast<const void*>(src) : static_cast<const void*>(p.q)), (short)0, nrec, 0x00020000);
-        const int voff = ((16 * w + m) * D + 4 * g) * 4;
+        const int voff = ((16 * w + (threadIdx.x & 15)) * D + 4 * ((threadIdx.x >> 4) & 3)) * 4;
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt)
             S[dt] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, voff + 64 * dt, 0, 0));
-    }
-    f32x4 Pm[8];  // fix: the transition, P[k][k'] at (k = 16dt + 4g + e, k' = 16w + m); starts as the identity
-    if (fix) {
-#pragma unroll
-        for (int dt = 0; dt < 8; ++dt)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) Pm[dt][e] = (16 * dt + 4 * g + e == 16 * w + m) ? 1.f : 0.f;
-    }
+    };
+    load_start_state(state_source(cur));
 
     const int ck_mode = (p.flags & KDA355_PF_CK_EVERY) ? 2 : ((p.flags & KDA355_PF_CK_SINGLE) ? 1 : 0);
-    auto ck_store = [&](int64_t rr) {
-        if (rr < 0 || rr >= p.ck_slots) return;
-        if (p.ck_bf16)
-            store_state_bf16(reinterpret_cast<uint16_t*>(p.ck_pool) + rr * p.ck_ss + (int64_t)h * D * D, S, w, g, m);
-        else
-            store_state(reinterpret_cast<float*>(p.ck_pool) + rr * p.ck_ss + (int64_t)h * D * D, S, w, g, m);
-    };
-    const int ck_single = (ck_mode == 1) ? ck_single_raw : 0;
-
     // gate-in-kernel constants for this thread's 16 channels
     float Aexp = 0.f;
     if (RG) {
-        Aexp = __expf(alog);
+        Aexp = __expf(cur.alog);
         if (tid < D) sDT[tid] = dtb;
     }
     // A_qk blocks (0,1) and (2,3) are read by the walk and never written by the Gram phase
@@ -433,568 +457,630 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
     }
     lds_barrier();  // sDT and the zeroed A_qk blocks are visible to every wave
 
-    for (int cl = 0; cl < nch; ++cl) {
-        // Lane indices are re-derived every chunk from an opaque copy so that the per-lane LDS addresses of all phases
-        // are recomputed where they are used instead of being kept live (and spilled) across the whole loop.
-        tid = threadIdx.x;
-        asm volatile("" : "+v"(tid));
-        lane = tid & 63;
-        m = lane & 15;
-        g = lane >> 4;
-        r = tid >> 3;
-        cb = tid & 7;
-        const int t0 = tstart + 64 * cl, L = min(64, len - 64 * cl);
-        // ================= P0: this chunk's raw rows (prefetched during the previous chunk)
-        // The raw q and k stay in registers until P2 (the next chunk's q, k loads reuse them from P5 on); the raw v
-        // goes to an LDS slot that only this thread reads back (the W area, which is free until P6), so its registers
-        // die here and the next chunk's v loads reuse them without a loop-carried copy.
-        *reinterpret_cast<u32x4*>(lds + LDS_W + r * (2 * RS16) + 32 * cb) = nx.v[0];
-        *reinterpret_cast<u32x4*>(lds + LDS_W + r * (2 * RS16) + 32 * cb + 16) = nx.v[1];
-        float gv[16];
-        if (RG) {
-            float rg[16];
-            const u32x4 gg[2] = {nx.g[0], nx.g[1]};
-            unpack16(gg, rg);
+    for (;;) {  // the workgroup's items
+        const int h = cur.h, n = cur.n, nch = cur.nch, tstart = cur.tstart, len = cur.len, first = cur.first;
+        const int pflags = cur.pflags, slot = cur.slot, seqch = cur.seqch;
+        const bool fix = P1 && (pflags & PIECE_FIX);
+        float* ws_h = p.ws + ((int64_t)slot * H + h) * D * D;        // this piece-head in array 0 (+ ws_arr: 1, 2)
+        const int ck_row0 = cur.ck_row0;
+        const int ck_single = (ck_mode == 1) ? cur.ck_single_raw : 0;
+        // the next item's head, first token, length and chunk count, for the rows fetched during this item's last
+        // chunk; its other words are read when it starts
+        const bool more = kpos + 1 < kend;
+        int nx_h = 0, nx_t = 0, nx_len = 0, nx_nch = 0;
+        float dtb_next = 0.f;
+        if (more) {
+            const int it2 = wl[gridDim.x + 2 + kpos], c2 = it2 / H;
+            const int32_t* e2 = tab + list_off + C_WORDS * c2;
+            nx_h = it2 - c2 * H;
+            nx_nch = e2[C_NCH];
+            nx_t = e2[C_TSTART];
+            nx_len = e2[C_LEN];
+            if (RG) dtb_next = p.dt_bias[nx_h * D + (threadIdx.x & (D - 1))];
+        }
+        f32x4 Pm[8];  // fix: the transition, P[k][k'] at (k = 16dt + 4g + e, k' = 16w + m); starts as the identity
+        if (fix) {
 #pragma unroll
-            for (int c = 0; c < 16; ++c)
-                gv[c] = (r < L) ? clamp_decay(p.lb * sigmoidf_(Aexp * (rg[c] + sDT[16 * cb + c]))) : 0.f;
-        } else {
+            for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) Pm[dt][e] = (16 * dt + 4 * g + e == 16 * w + m) ? 1.f : 0.f;
+        }
+        auto ck_store = [&](int64_t rr) {
+            if (rr < 0 || rr >= p.ck_slots) return;
+            if (p.ck_bf16)
+                store_state_bf16(reinterpret_cast<uint16_t*>(p.ck_pool) + rr * p.ck_ss + (int64_t)h * D * D, S, w, g, m);
+            else
+                store_state(reinterpret_cast<float*>(p.ck_pool) + rr * p.ck_ss + (int64_t)h * D * D, S, w, g, m);
+        };
+
+        for (int cl = 0; cl < nch; ++cl) {
+            // Lane indices are re-derived every chunk from an opaque copy so that the per-lane LDS addresses of all
+            // phases are recomputed where they are used instead of being kept live (and spilled) across the whole loop.
+            tid = threadIdx.x;
+            asm volatile("" : "+v"(tid));
+            lane = tid & 63;
+            m = lane & 15;
+            g = lane >> 4;
+            r = tid >> 3;
+            cb = tid & 7;
+            const int t0 = tstart + 64 * cl, L = min(64, len - 64 * cl);
+            // the rows fetched during this chunk: the next chunk's, or during an item's last chunk the next item's
+            // first
+            const bool pf_here = cl + 1 < nch, pf = pf_here || more;
+            const int pf_h = pf_here ? h : nx_h, pf_t = pf_here ? t0 + 64 : nx_t;
+            const int pf_L = pf_here ? min(64, len - 64 * (cl + 1)) : (nx_nch > 0 ? min(64, nx_len) : 0);
+            // ================= P0: this chunk's raw rows (prefetched during the previous chunk) The raw q and k stay
+            // in registers until P2 (the next chunk's q, k loads reuse them from P5 on); the raw v goes to an LDS slot
+            // that only this thread reads back (the W area, which is free until P6), so its registers die here and the
+            // next chunk's v loads reuse them without a loop-carried copy.
+            *reinterpret_cast<u32x4*>(lds + LDS_W + r * (2 * RS16) + 32 * cb) = nx.v[0];
+            *reinterpret_cast<u32x4*>(lds + LDS_W + r * (2 * RS16) + 32 * cb + 16) = nx.v[1];
+            float gv[16];
+            if (RG) {
+                float rg[16];
+                const u32x4 gg[2] = {nx.g[0], nx.g[1]};
+                unpack16(gg, rg);
+#pragma unroll
+                for (int c = 0; c < 16; ++c)
+                    gv[c] = (r < L) ? clamp_decay(p.lb * sigmoidf_(Aexp * (rg[c] + sDT[16 * cb + c]))) : 0.f;
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) gv[4 * i + j] = clamp_decay(__uint_as_float(nx.g[i][j]));
+            }
+            const float bt = (r >= L) ? 0.f : (RB ? sigmoidf_(bf2f(nx.beta)) : __uint_as_float(nx.beta));
+#pragma unroll
+            for (int c = 0; c < 16; ++c) gv[c] *= 1.4426950408889634f;  // log2(e): the cumsum runs in log2 units
+            float rq = 1.f, rk = 1.f;
+            if (NORM) {  // F.normalize(x, eps=1e-6) = x / max(|x|, 1e-6)  (kda/mi350x/reference.py:59-60)
+                float qf[16], kf[16];
+                {
+                    const u32x4 a[2] = {nx.q[0], nx.q[1]}, b[2] = {nx.k[0], nx.k[1]};
+                    unpack16(a, qf);
+                    unpack16(b, kf);
+                }
+                float sq = 0.f, sk = 0.f;
+#pragma unroll
+                for (int c = 0; c < 16; ++c) { sq += qf[c] * qf[c]; sk += kf[c] * kf[c]; }
+                sq = sum8(sq);
+                sk = sum8(sk);
+                rq = __builtin_amdgcn_rcpf(fmaxf(sqrtf(sq), 1e-6f));
+                rk = __builtin_amdgcn_rcpf(fmaxf(sqrtf(sk), 1e-6f));
+            }
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) gv[4 * i + j] = clamp_decay(__uint_as_float(nx.g[i][j]));
-        }
-        const float bt = (r >= L) ? 0.f : (RB ? sigmoidf_(bf2f(nx.beta)) : __uint_as_float(nx.beta));
-#pragma unroll
-        for (int c = 0; c < 16; ++c) gv[c] *= 1.4426950408889634f;  // log2(e): the cumsum runs in log2 units
-        float rq = 1.f, rk = 1.f;
-        if (NORM) {  // F.normalize(x, eps=1e-6) = x / max(|x|, 1e-6)  (kda/mi350x/reference.py:59-60)
-            float qf[16], kf[16];
+                *reinterpret_cast<f32x4*>(&sG[r * RS32 + 16 * cb + 4 * (i ^ (cb >> 1))]) =
+                    f32x4{gv[4 * i], gv[4 * i + 1], gv[4 * i + 2], gv[4 * i + 3]};
+            if (cb == 0) sBeta[r] = bt;
+            lds_barrier();
+            // ================= P1: gate cumsum inside 16-row segments
             {
-                const u32x4 a[2] = {nx.q[0], nx.q[1]}, b[2] = {nx.k[0], nx.k[1]};
-                unpack16(a, qf);
-                unpack16(b, kf);
-            }
-            float sq = 0.f, sk = 0.f;
-#pragma unroll
-            for (int c = 0; c < 16; ++c) { sq += qf[c] * qf[c]; sk += kf[c] * kf[c]; }
-            sq = sum8(sq);
-            sk = sum8(sk);
-            rq = __builtin_amdgcn_rcpf(fmaxf(sqrtf(sq), 1e-6f));
-            rk = __builtin_amdgcn_rcpf(fmaxf(sqrtf(sk), 1e-6f));
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            *reinterpret_cast<f32x4*>(&sG[r * RS32 + 16 * cb + 4 * (i ^ (cb >> 1))]) =
-                f32x4{gv[4 * i], gv[4 * i + 1], gv[4 * i + 2], gv[4 * i + 3]};
-        if (cb == 0) sBeta[r] = bt;
-        lds_barrier();
-        // ================= P1: gate cumsum inside 16-row segments
-        {
-            const int c = tid & 127, s = tid >> 7;
-            float x[16];
-#pragma unroll
-            for (int i = 0; i < 16; ++i) x[i] = sG[(16 * s + i) * RS32 + swz(c)];
-#pragma unroll
-            for (int i = 1; i < 16; ++i) x[i] += x[i - 1];
-#pragma unroll
-            for (int i = 0; i < 16; ++i) sG[(16 * s + i) * RS32 + swz(c)] = x[i];
-            sWt[s * 128 + c] = x[15];
-            sGM[s * 128 + c] = x[7];  // the factors' reference row of block s, kept apart so P2 can overwrite sG
-        }
-        lds_barrier();
-        // ================= P2: element factors (raw threads) and block factors (channel threads).  The block middle
-        // rows and segment totals come from sGM / sWt, so each raw thread reads only its own gate row from sG and can
-        // overwrite that row with k^ fi in place (no other thread reads it in this phase).
-        {
-            float qf[16], kf[16];
-            {
-                const u32x4 a[2] = {nx.q[0], nx.q[1]}, b[2] = {nx.k[0], nx.k[1]};
-                unpack16(a, qf);
-                unpack16(b, kf);
-            }
-            if (NORM) {  // uniform: calls without in-kernel normalization skip the 32 multiplies by 1
-#pragma unroll
-                for (int c = 0; c < 16; ++c) { kf[c] *= rk; qf[c] *= rq; }
-            }
-            const int I = r >> 4;
-            // block i of the row: its gate values are read before its k^ fi overwrites them (one thread, in order)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int o = r * RS32 + 16 * cb + 4 * (i ^ (cb >> 1));
-                const f32x4 a = *reinterpret_cast<const f32x4*>(&sG[o]);
-                const f32x4 b = *reinterpret_cast<const f32x4*>(&sGM[I * 128 + 16 * cb + 4 * i]);
-                f32x4 kfi, kfj, qfi;
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int c = 4 * i + j;
-                    const float d = a[j] - b[j];  // Gamma_r - Gamma_m (the segment offset cancels)
-                    const float fi = exp2_(d), fj = exp2_(-d);
-                    kfi[j] = kf[c] * fi;
-                    kfj[j] = kf[c] * fj;
-                    qfi[j] = qf[c] * fi;
-                }
-                *reinterpret_cast<f32x4*>(&sQA[o]) = qfi;
-                *reinterpret_cast<f32x4*>(&sKB[o]) = kfj;
-                *reinterpret_cast<f32x4*>(&sKA[o]) = kfi;
-            }
-        }
-        {
-            const int c = tid & 127, qd = tid >> 7;
-            const float o1 = sWt[c], o2 = o1 + sWt[128 + c], o3 = o2 + sWt[256 + c];
-            float gr[8];  // Gamma at rows 8 i + 7: block middles (sGM) and segment ends (sWt), plus the earlier segments
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const float off = (i < 2) ? 0.f : (i < 4) ? o1 : (i < 6) ? o2 : o3;
-                gr[i] = ((i & 1) ? sWt[(i >> 1) * 128 + c] : sGM[(i >> 1) * 128 + c]) + off;
-            }
-#pragma unroll
-            for (int f = 0; f < F_ROWS; ++f) {  // unrolled: gr[] is indexed by constants only (stays in registers)
-                if ((f & 3) != qd) continue;
-                float x;
-                if (f < F_B) {                       // a_I, I = f + 1: Gamma_m(I) - Gamma_{16I-1}
-                    const int I = f + 1;
-                    x = gr[2 * I] - gr[2 * I - 1];
-                } else if (f < F_X) {                // b_IJ
-                    const int t = f - F_B;
-                    const int I = t < 1 ? 1 : (t < 3 ? 2 : 3);
-                    const int J = t - (I * (I - 1)) / 2;
-                    x = gr[2 * I - 1] - gr[2 * J];
-                } else if (f < F_Y) {
-                    x = gr[2 * (f - F_X)];
-                } else if (f < F_DEC) {
-                    x = gr[7] - gr[2 * (f - F_Y)];
-                } else {
-                    x = gr[7];
-                }
-                sF[f * 128 + c] = exp2_(x);
-            }
-        }
-        lds_barrier();
-        // ================= P4: Gram tiles
-        if (w < 4) {
-            const int I = w, i = 16 * I + m;
-            f32x4 akk = {0.f, 0.f, 0.f, 0.f}, aqk = akk;
-#pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                const int c0 = 32 * s + 8 * g;
-                uint32_t kah[4], kal[4], qah[4], qal[4], kbh[4], kbl[4];  // bf16x8 fragments as 4 packed pairs
-#pragma unroll
-                for (int hf = 0; hf < 2; ++hf) {
-                    const f32x4 ka = *reinterpret_cast<const f32x4*>(&sKA[i * RS32 + swz(c0 + 4 * hf)]);
-                    const f32x4 qa = *reinterpret_cast<const f32x4*>(&sQA[i * RS32 + swz(c0 + 4 * hf)]);
-                    const f32x4 kb = *reinterpret_cast<const f32x4*>(&sKB[i * RS32 + swz(c0 + 4 * hf)]);
-#pragma unroll
-                    for (int j = 0; j < 2; ++j) {
-                        const int e = 2 * hf + j;
-                        split_bf16x2(ka[2 * j], ka[2 * j + 1], kah[e], kal[e]);
-                        split_bf16x2(qa[2 * j], qa[2 * j + 1], qah[e], qal[e]);
-                        split_bf16x2(kb[2 * j], kb[2 * j + 1], kbh[e], kbl[e]);
-                    }
-                }
-                const bf16x8 Kah = as_bf16x8(kah), Kal = as_bf16x8(kal), Qah = as_bf16x8(qah), Qal = as_bf16x8(qal);
-                const bf16x8 Kbh = as_bf16x8(kbh), Kbl = as_bf16x8(kbl);
-                akk = mfma32bf(Kah, Kbh, akk);
-                akk = mfma32bf(Kah, Kbl, akk);
-                akk = mfma32bf(Kal, Kbh, akk);
-                aqk = mfma32bf(Kbh, Qah, aqk);  // transposed: lane (g, m) holds row 16 I + m, columns 16 I + 4 g .. + 3
-                aqk = mfma32bf(Kbl, Qah, aqk);
-                aqk = mfma32bf(Kbh, Qal, aqk);
-            }
-            f32x4 lt;
-            f16x4 aq;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int rr = 4 * g + e, rw = 16 * I + rr;
-                lt[e] = (m < rr) ? sBeta[rw] * akk[e] : 0.f;
-                aq[e] = (half_t)((rr <= m) ? aqk[e] : 0.f);  // A_qk[16 I + m][16 I + rr], causal within the block
-            }
-            *reinterpret_cast<f16x4*>(&sAq[i * RS16S + pos64(16 * I + 4 * g)]) = aq;
-            *reinterpret_cast<f32x4*>(&sL[(I * 16 + m) * 20 + 4 * g]) = lt;
-            // T_II = (I + L_II)^-1 of this wave's block while waves 4..7 still work on the off-diagonal blocks: lane j
-            // (every group of 16 lanes computes the same columns; lanes 0..15 write) solves column j by right-looking
-            // substitution.  The wave reads back the block it has just written: a wave's LDS operations complete in order.
-            {
-                const float* Lb = sL + I * 16 * 20;  // column k of L_II is the contiguous row k
+                const int c = tid & 127, s = tid >> 7;
                 float x[16];
 #pragma unroll
-                for (int ii = 0; ii < 16; ++ii) x[ii] = (ii == m) ? 1.f : 0.f;
+                for (int i = 0; i < 16; ++i) x[i] = sG[(16 * s + i) * RS32 + swz(c)];
 #pragma unroll
-                for (int k = 0; k < 15; ++k) {  // x[k] is final: push it into the rows below
-                    float col[16];
+                for (int i = 1; i < 16; ++i) x[i] += x[i - 1];
 #pragma unroll
-                    for (int q4 = 0; q4 < 4; ++q4) {
-                        const f32x4 c4 = *reinterpret_cast<const f32x4*>(&Lb[k * 20 + 4 * q4]);
-                        col[4 * q4] = c4[0]; col[4 * q4 + 1] = c4[1]; col[4 * q4 + 2] = c4[2]; col[4 * q4 + 3] = c4[3];
-                    }
-#pragma unroll
-                    for (int ii = k + 1; ii < 16; ++ii) x[ii] -= col[ii] * x[k];
-                }
-                if (g == 0) {
-#pragma unroll
-                    for (int ii = 0; ii < 16; ++ii) {
-                        const half_t hi = (half_t)x[ii];
-                        sAk[(16 * I + ii) * RS16S + 16 * I + m] = hi;
-                        // PREC: the low part in the A_qk block (I / 2, 2 + I % 2), a block of rows 0..31 and columns
-                        // 32..63 that the walk never reads and the Gram phase never writes
-                        if (PREC) sAq[(16 * (I >> 1) + ii) * RS16S + 32 + 16 * (I & 1) + m] = (half_t)(x[ii] - (float)hi);
-                    }
-                }
+                for (int i = 0; i < 16; ++i) sG[(16 * s + i) * RS32 + swz(c)] = x[i];
+                sWt[s * 128 + c] = x[15];
+                sGM[s * 128 + c] = x[7];  // the factors' reference row of block s, kept apart so P2 can overwrite sG
             }
-        } else {
-            const int I = (w == 4) ? 1 : ((w == 5) ? 2 : 3);
-            const int J0 = (w == 7) ? 2 : 0;
-            const int nJ = (w == 4 || w == 7) ? 1 : 2;
-            const int i = 16 * I + m;
-            f32x4 akk[2], aqk[2];
+            lds_barrier();
+            // ================= P2: element factors (raw threads) and block factors (channel threads).  The block
+            // middle rows and segment totals come from sGM / sWt, so each raw thread reads only its own gate row from
+            // sG and can overwrite that row with k^ fi in place (no other thread reads it in this phase).
+            {
+                float qf[16], kf[16];
+                {
+                    const u32x4 a[2] = {nx.q[0], nx.q[1]}, b[2] = {nx.k[0], nx.k[1]};
+                    unpack16(a, qf);
+                    unpack16(b, kf);
+                }
+                if (NORM) {  // uniform: calls without in-kernel normalization skip the 32 multiplies by 1
 #pragma unroll
-            for (int t = 0; t < 2; ++t) { akk[t] = f32x4{0.f, 0.f, 0.f, 0.f}; aqk[t] = akk[t]; }
+                    for (int c = 0; c < 16; ++c) { kf[c] *= rk; qf[c] *= rq; }
+                }
+                const int I = r >> 4;
+                // block i of the row: its gate values are read before its k^ fi overwrites them (one thread, in order)
 #pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                const int c0 = 32 * s + 8 * g;
-                f16x8 ka, qa;
-#pragma unroll
-                for (int hf = 0; hf < 2; ++hf) {
-                    const f32x4 a = *reinterpret_cast<const f32x4*>(&sKA[i * RS32 + swz(c0 + 4 * hf)]);
-                    const f32x4 q4 = *reinterpret_cast<const f32x4*>(&sQA[i * RS32 + swz(c0 + 4 * hf)]);
-                    const f32x4 fa = *reinterpret_cast<const f32x4*>(&sF[(F_A + I - 1) * 128 + c0 + 4 * hf]);
+                for (int i = 0; i < 4; ++i) {
+                    const int o = r * RS32 + 16 * cb + 4 * (i ^ (cb >> 1));
+                    const f32x4 a = *reinterpret_cast<const f32x4*>(&sG[o]);
+                    const f32x4 b = *reinterpret_cast<const f32x4*>(&sGM[I * 128 + 16 * cb + 4 * i]);
+                    f32x4 kfi, kfj, qfi;
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
-                        ka[4 * hf + j] = (half_t)(a[j] * fa[j]);
-                        qa[4 * hf + j] = (half_t)(q4[j] * fa[j]);
+                        const int c = 4 * i + j;
+                        const float d = a[j] - b[j];  // Gamma_r - Gamma_m (the segment offset cancels)
+                        const float fi = exp2_(d), fj = exp2_(-d);
+                        kfi[j] = kf[c] * fi;
+                        kfj[j] = kf[c] * fj;
+                        qfi[j] = qf[c] * fi;
+                    }
+                    *reinterpret_cast<f32x4*>(&sQA[o]) = qfi;
+                    *reinterpret_cast<f32x4*>(&sKB[o]) = kfj;
+                    *reinterpret_cast<f32x4*>(&sKA[o]) = kfi;
+                }
+            }
+            {
+                const int c = tid & 127, qd = tid >> 7;
+                const float o1 = sWt[c], o2 = o1 + sWt[128 + c], o3 = o2 + sWt[256 + c];
+                // Gamma at rows 8 i + 7: block middles (sGM) and segment ends (sWt), plus the earlier segments
+                float gr[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const float off = (i < 2) ? 0.f : (i < 4) ? o1 : (i < 6) ? o2 : o3;
+                    gr[i] = ((i & 1) ? sWt[(i >> 1) * 128 + c] : sGM[(i >> 1) * 128 + c]) + off;
+                }
+#pragma unroll
+                for (int f = 0; f < F_ROWS; ++f) {  // unrolled: gr[] is indexed by constants only (stays in registers)
+                    if ((f & 3) != qd) continue;
+                    float x;
+                    if (f < F_B) {                       // a_I, I = f + 1: Gamma_m(I) - Gamma_{16I-1}
+                        const int I = f + 1;
+                        x = gr[2 * I] - gr[2 * I - 1];
+                    } else if (f < F_X) {                // b_IJ
+                        const int t = f - F_B;
+                        const int I = t < 1 ? 1 : (t < 3 ? 2 : 3);
+                        const int J = t - (I * (I - 1)) / 2;
+                        x = gr[2 * I - 1] - gr[2 * J];
+                    } else if (f < F_Y) {
+                        x = gr[2 * (f - F_X)];
+                    } else if (f < F_DEC) {
+                        x = gr[7] - gr[2 * (f - F_Y)];
+                    } else {
+                        x = gr[7];
+                    }
+                    sF[f * 128 + c] = exp2_(x);
+                }
+            }
+            lds_barrier();
+            // ================= P4: Gram tiles
+            if (w < 4) {
+                const int I = w, i = 16 * I + m;
+                f32x4 akk = {0.f, 0.f, 0.f, 0.f}, aqk = akk;
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    const int c0 = 32 * s + 8 * g;
+                    uint32_t kah[4], kal[4], qah[4], qal[4], kbh[4], kbl[4];  // bf16x8 fragments as 4 packed pairs
+#pragma unroll
+                    for (int hf = 0; hf < 2; ++hf) {
+                        const f32x4 ka = *reinterpret_cast<const f32x4*>(&sKA[i * RS32 + swz(c0 + 4 * hf)]);
+                        const f32x4 qa = *reinterpret_cast<const f32x4*>(&sQA[i * RS32 + swz(c0 + 4 * hf)]);
+                        const f32x4 kb = *reinterpret_cast<const f32x4*>(&sKB[i * RS32 + swz(c0 + 4 * hf)]);
+#pragma unroll
+                        for (int j = 0; j < 2; ++j) {
+                            const int e = 2 * hf + j;
+                            split_bf16x2(ka[2 * j], ka[2 * j + 1], kah[e], kal[e]);
+                            split_bf16x2(qa[2 * j], qa[2 * j + 1], qah[e], qal[e]);
+                            split_bf16x2(kb[2 * j], kb[2 * j + 1], kbh[e], kbl[e]);
+                        }
+                    }
+                    const bf16x8 Kah = as_bf16x8(kah), Kal = as_bf16x8(kal), Qah = as_bf16x8(qah), Qal = as_bf16x8(qal);
+                    const bf16x8 Kbh = as_bf16x8(kbh), Kbl = as_bf16x8(kbl);
+                    akk = mfma32bf(Kah, Kbh, akk);
+                    akk = mfma32bf(Kah, Kbl, akk);
+                    akk = mfma32bf(Kal, Kbh, akk);
+                    // transposed: lane (g, m) holds row 16 I + m, columns 16 I + 4 g .. + 3
+                    aqk = mfma32bf(Kbh, Qah, aqk);
+                    aqk = mfma32bf(Kbl, Qah, aqk);
+                    aqk = mfma32bf(Kbh, Qal, aqk);
+                }
+                f32x4 lt;
+                f16x4 aq;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int rr = 4 * g + e, rw = 16 * I + rr;
+                    lt[e] = (m < rr) ? sBeta[rw] * akk[e] : 0.f;
+                    aq[e] = (half_t)((rr <= m) ? aqk[e] : 0.f);  // A_qk[16 I + m][16 I + rr], causal within the block
+                }
+                *reinterpret_cast<f16x4*>(&sAq[i * RS16S + pos64(16 * I + 4 * g)]) = aq;
+                *reinterpret_cast<f32x4*>(&sL[(I * 16 + m) * 20 + 4 * g]) = lt;
+                // T_II = (I + L_II)^-1 of this wave's block while waves 4..7 still work on the off-diagonal blocks:
+                // lane j (every group of 16 lanes computes the same columns; lanes 0..15 write) solves column j by
+                // right-looking substitution.  The wave reads back the block it has just written: a wave's LDS
+                // operations complete in order.
+                {
+                    const float* Lb = sL + I * 16 * 20;  // column k of L_II is the contiguous row k
+                    float x[16];
+#pragma unroll
+                    for (int ii = 0; ii < 16; ++ii) x[ii] = (ii == m) ? 1.f : 0.f;
+#pragma unroll
+                    for (int k = 0; k < 15; ++k) {  // x[k] is final: push it into the rows below
+                        float col[16];
+#pragma unroll
+                        for (int q4 = 0; q4 < 4; ++q4) {
+                            const f32x4 c4 = *reinterpret_cast<const f32x4*>(&Lb[k * 20 + 4 * q4]);
+                            col[4 * q4] = c4[0]; col[4 * q4 + 1] = c4[1]; col[4 * q4 + 2] = c4[2]; col[4 * q4 + 3] = c4[3];
+                        }
+#pragma unroll
+                        for (int ii = k + 1; ii < 16; ++ii) x[ii] -= col[ii] * x[k];
+                    }
+                    if (g == 0) {
+#pragma unroll
+                        for (int ii = 0; ii < 16; ++ii) {
+                            const half_t hi = (half_t)x[ii];
+                            sAk[(16 * I + ii) * RS16S + 16 * I + m] = hi;
+                            // PREC: the low part in the A_qk block (I / 2, 2 + I % 2), a block of rows 0..31 and
+                            // columns 32..63 that the walk never reads and the Gram phase never writes
+                            if (PREC)
+                                sAq[(16 * (I >> 1) + ii) * RS16S + 32 + 16 * (I & 1) + m] = (half_t)(x[ii] - (float)hi);
+                        }
                     }
                 }
+            } else {
+                const int I = (w == 4) ? 1 : ((w == 5) ? 2 : 3);
+                const int J0 = (w == 7) ? 2 : 0;
+                const int nJ = (w == 4 || w == 7) ? 1 : 2;
+                const int i = 16 * I + m;
+                f32x4 akk[2], aqk[2];
+#pragma unroll
+                for (int t = 0; t < 2; ++t) { akk[t] = f32x4{0.f, 0.f, 0.f, 0.f}; aqk[t] = akk[t]; }
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    const int c0 = 32 * s + 8 * g;
+                    f16x8 ka, qa;
+#pragma unroll
+                    for (int hf = 0; hf < 2; ++hf) {
+                        const f32x4 a = *reinterpret_cast<const f32x4*>(&sKA[i * RS32 + swz(c0 + 4 * hf)]);
+                        const f32x4 q4 = *reinterpret_cast<const f32x4*>(&sQA[i * RS32 + swz(c0 + 4 * hf)]);
+                        const f32x4 fa = *reinterpret_cast<const f32x4*>(&sF[(F_A + I - 1) * 128 + c0 + 4 * hf]);
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+                            ka[4 * hf + j] = (half_t)(a[j] * fa[j]);
+                            qa[4 * hf + j] = (half_t)(q4[j] * fa[j]);
+                        }
+                    }
+#pragma unroll
+                    for (int t = 0; t < 2; ++t) {
+                        if (t < nJ) {
+                            const int J = J0 + t, jr = 16 * J + m;
+                            const int fb = F_B + (I * (I - 1)) / 2 + J;
+                            f16x8 kb;
+#pragma unroll
+                            for (int hf = 0; hf < 2; ++hf) {
+                                const f32x4 b = *reinterpret_cast<const f32x4*>(&sKB[jr * RS32 + swz(c0 + 4 * hf)]);
+                                const f32x4 fbv = *reinterpret_cast<const f32x4*>(&sF[fb * 128 + c0 + 4 * hf]);
+#pragma unroll
+                                for (int j = 0; j < 4; ++j) kb[4 * hf + j] = (half_t)(b[j] * fbv[j]);
+                            }
+                            akk[t] = mfma32(kb, ka, akk[t]);  // transposed tiles: lane (g, m) holds row 16 I + m,
+                            aqk[t] = mfma32(kb, qa, aqk[t]);  // columns 16 J + 4 g .. + 3
+                        }
+                    }
+                }
+                const float nb = -sBeta[i];
 #pragma unroll
                 for (int t = 0; t < 2; ++t) {
                     if (t < nJ) {
-                        const int J = J0 + t, jr = 16 * J + m;
-                        const int fb = F_B + (I * (I - 1)) / 2 + J;
-                        f16x8 kb;
+                        const int J = J0 + t;
+                        f16x4 ak, al, aq;
 #pragma unroll
-                        for (int hf = 0; hf < 2; ++hf) {
-                            const f32x4 b = *reinterpret_cast<const f32x4*>(&sKB[jr * RS32 + swz(c0 + 4 * hf)]);
-                            const f32x4 fbv = *reinterpret_cast<const f32x4*>(&sF[fb * 128 + c0 + 4 * hf]);
-#pragma unroll
-                            for (int j = 0; j < 4; ++j) kb[4 * hf + j] = (half_t)(b[j] * fbv[j]);
+                        for (int e = 0; e < 4; ++e) {
+                            const float x = nb * akk[t][e];
+                            ak[e] = (half_t)x;
+                            al[e] = (half_t)(x - (float)ak[e]);
+                            aq[e] = (half_t)aqk[t][e];
                         }
-                        akk[t] = mfma32(kb, ka, akk[t]);  // transposed tiles: lane (g, m) holds row 16 I + m,
-                        aqk[t] = mfma32(kb, qa, aqk[t]);  // columns 16 J + 4 g .. + 3
+                        *reinterpret_cast<f16x4*>(&sAk[i * RS16S + 16 * J + 4 * g]) = ak;
+                        // PREC: the low part goes to the unused mirrored block (J, I) of the same array
+                        if (PREC) *reinterpret_cast<f16x4*>(&sAk[(16 * J + m) * RS16S + 16 * I + 4 * g]) = al;
+                        *reinterpret_cast<f16x4*>(&sAq[i * RS16S + pos64(16 * J + 4 * g)]) = aq;
                     }
                 }
             }
-            const float nb = -sBeta[i];
+            // no barrier here: the reads below touch only the raw v staging and the thread's own q^ fi / k^ fj rows,
+            // which the Gram phase neither writes nor overwrites; the barrier before the layouts orders every Gram read
+            // of regions B and C before they are rewritten ================= P5: Q~, Kd^T, beta v into their walk
+            // layouts (raw threads) The initial state loads (issued in the prologue) complete here, before any
+            // next-chunk row is in flight: an empty use of S makes the compiler's wait for them fall at this point,
+            // where in every later chunk only the long-finished output stores are outstanding, instead of before each
+            // walk, where it would also wait for the prefetched rows.
 #pragma unroll
-            for (int t = 0; t < 2; ++t) {
-                if (t < nJ) {
-                    const int J = J0 + t;
-                    f16x4 ak, al, aq;
+            for (int dt = 0; dt < 8; ++dt) asm volatile("" : "+v"(S[dt]));
+            // the next chunk's q, k rows: issued here, consumed at the next P0 (their registers are free during P1..P4)
+            if (pf) load_row_qk(p, pf_h, pf_t, pf_L, r, cb, nx);
+            float qfi[16], kfj[16];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const f32x4 a = *reinterpret_cast<const f32x4*>(&sQA[r * RS32 + 16 * cb + 4 * (i ^ (cb >> 1))]);
+                const f32x4 b = *reinterpret_cast<const f32x4*>(&sKB[r * RS32 + 16 * cb + 4 * (i ^ (cb >> 1))]);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) { qfi[4 * i + j] = a[j]; kfj[4 * i + j] = b[j]; }
+            }
+            lds_barrier();  // regions B and C are rewritten below
+            {
+                const int I = r >> 4;
+                const int hb = cb & 1, blk = cb >> 1;
+#pragma unroll
+                for (int gq = 0; gq < 4; ++gq) {
+                    const f32x4 xf = *reinterpret_cast<const f32x4*>(&sF[(F_X + I) * 128 + 16 * cb + 4 * gq]);
+                    f16x4 o;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) o[e] = (half_t)(qfi[4 * gq + e] * xf[e]);
+                    *reinterpret_cast<f16x4*>(&sQt[r * RS16 + 32 * blk + 8 * gq + 4 * hb]) = o;
+                }
+                // Kd^T row of key channel k is stored at row 16 (k / 16) + (k % 16 ^ k / 16): the 8 channel blocks of a
+                // column write then land on 8 different banks
+                const int pr = pos64(r);
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const float y = sF[(F_Y + I) * 128 + 16 * cb + e];
+                    sKd[(16 * cb + (e ^ cb)) * RS16S + pr] = (half_t)(kfj[e] * y);
+                }
+            }
+            // no barrier here: the solve reads k^ fi (region A), the raw v rows, -A_kk / T_II, the factors and beta,
+            // none of which the layouts above write; it writes W into region B's upper half, whose last reader (the
+            // operand reads before the layouts) passed the barrier above.  The walk reads the layouts after the solve's
+            // barrier. ================= P6: W and U by block forward substitution (wave w: channel / value tile w)
+            if (pf) load_row_vb(p, pf_h, pf_t, pf_L, r, cb, RB, nx);
+            f32x4 Ur[4];
+            {
+                const int c = 16 * w + m;
+                f32x4 Xw[4];
+                // PREC: -A_IJ, T_II, the solved blocks X_J and the right-hand side before T_II as fp16 pairs
+                f16x4 Xh[4], Xl[4], Uh[4], Ul[4];
+                auto split4 = [](const f32x4& x, f16x4& hi, f16x4& lo) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) { hi[e] = (half_t)x[e]; lo[e] = (half_t)(x[e] - (float)hi[e]); }
+                };
+#pragma unroll
+                for (int I = 0; I < 4; ++I) {
+                    const float xI = sF[(F_X + I) * 128 + c];
+                    f32x4 aw, au;
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
-                        const float x = nb * akk[t][e];
-                        ak[e] = (half_t)x;
-                        al[e] = (half_t)(x - (float)ak[e]);
-                        aq[e] = (half_t)aqk[t][e];
+                        const int rw = 16 * I + 4 * g + e;
+                        aw[e] = sBeta[rw] * sKA[rw * RS32 + swz(c)] * xI;
+                        au[e] = sBeta[rw] * bf2f(sV[rw * RS16 + c]);  // beta v straight from the raw v row
                     }
-                    *reinterpret_cast<f16x4*>(&sAk[i * RS16S + 16 * J + 4 * g]) = ak;
-                    // PREC: the low part goes to the unused mirrored block (J, I) of the same array
-                    if (PREC) *reinterpret_cast<f16x4*>(&sAk[(16 * J + m) * RS16S + 16 * I + 4 * g]) = al;
-                    *reinterpret_cast<f16x4*>(&sAq[i * RS16S + pos64(16 * J + 4 * g)]) = aq;
-                }
-            }
-        }
-        // no barrier here: the reads below touch only the raw v staging and the thread's own q^ fi / k^ fj rows, which
-        // the Gram phase neither writes nor overwrites; the barrier before the layouts orders every Gram read of
-        // regions B and C before they are rewritten
-        // ================= P5: Q~, Kd^T, beta v into their walk layouts (raw threads)
-        // The initial state loads (issued in the prologue) complete here, before any next-chunk row is in flight: an
-        // empty use of S makes the compiler's wait for them fall at this point, where in every later chunk only the
-        // long-finished output stores are outstanding, instead of before each walk, where it would also wait for
-        // the prefetched rows.
 #pragma unroll
-        for (int dt = 0; dt < 8; ++dt) asm volatile("" : "+v"(S[dt]));
-        // the next chunk's q, k rows: issued here, consumed at the next P0 (their registers are free during P1..P4)
-        if (cl + 1 < nch) load_row_qk(p, h, t0 + 64, min(64, len - 64 * (cl + 1)), r, cb, nx);
-        float qfi[16], kfj[16];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const f32x4 a = *reinterpret_cast<const f32x4*>(&sQA[r * RS32 + 16 * cb + 4 * (i ^ (cb >> 1))]);
-            const f32x4 b = *reinterpret_cast<const f32x4*>(&sKB[r * RS32 + 16 * cb + 4 * (i ^ (cb >> 1))]);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) { qfi[4 * i + j] = a[j]; kfj[4 * i + j] = b[j]; }
-        }
-        lds_barrier();  // regions B and C are rewritten below
-        {
-            const int I = r >> 4;
-            const int hb = cb & 1, blk = cb >> 1;
-#pragma unroll
-            for (int gq = 0; gq < 4; ++gq) {
-                const f32x4 xf = *reinterpret_cast<const f32x4*>(&sF[(F_X + I) * 128 + 16 * cb + 4 * gq]);
-                f16x4 o;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) o[e] = (half_t)(qfi[4 * gq + e] * xf[e]);
-                *reinterpret_cast<f16x4*>(&sQt[r * RS16 + 32 * blk + 8 * gq + 4 * hb]) = o;
-            }
-            // Kd^T row of key channel k is stored at row 16 (k / 16) + (k % 16 ^ k / 16): the 8 channel blocks of a
-            // column write then land on 8 different banks
-            const int pr = pos64(r);
-#pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const float y = sF[(F_Y + I) * 128 + 16 * cb + e];
-                sKd[(16 * cb + (e ^ cb)) * RS16S + pr] = (half_t)(kfj[e] * y);
-            }
-        }
-        // no barrier here: the solve reads k^ fi (region A), the raw v rows, -A_kk / T_II, the factors and beta, none
-        // of which the layouts above write; it writes W into region B's upper half, whose last reader (the operand
-        // reads before the layouts) passed the barrier above.  The walk reads the layouts after the solve's barrier.
-        // ================= P6: W and U by block forward substitution (wave w: channel / value tile w)
-        if (cl + 1 < nch) load_row_vb(p, h, t0 + 64, min(64, len - 64 * (cl + 1)), r, cb, RB, nx);
-        f32x4 Ur[4];
-        {
-            const int c = 16 * w + m;
-            f32x4 Xw[4];
-            // PREC: -A_IJ, T_II, the solved blocks X_J and the right-hand side before T_II as fp16 pairs
-            f16x4 Xh[4], Xl[4], Uh[4], Ul[4];
-            auto split4 = [](const f32x4& x, f16x4& hi, f16x4& lo) {
-#pragma unroll
-                for (int e = 0; e < 4; ++e) { hi[e] = (half_t)x[e]; lo[e] = (half_t)(x[e] - (float)hi[e]); }
-            };
-#pragma unroll
-            for (int I = 0; I < 4; ++I) {
-                const float xI = sF[(F_X + I) * 128 + c];
-                f32x4 aw, au;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int rw = 16 * I + 4 * g + e;
-                    aw[e] = sBeta[rw] * sKA[rw * RS32 + swz(c)] * xI;
-                    au[e] = sBeta[rw] * bf2f(sV[rw * RS16 + c]);  // beta v straight from the raw v row
-                }
-#pragma unroll
-                for (int J = 0; J < I; ++J) {
-                    const f16x4 A = *reinterpret_cast<const f16x4*>(&sAk[(16 * I + m) * RS16S + 16 * J + 4 * g]);
-                    const f16x4 Al = PREC ? *reinterpret_cast<const f16x4*>(&sAk[(16 * J + m) * RS16S + 16 * I + 4 * g])
-                                          : f16x4{};
-                    aw = mfma16(A, Xh[J], aw);
-                    au = mfma16(A, Uh[J], au);
+                    for (int J = 0; J < I; ++J) {
+                        const f16x4 A = *reinterpret_cast<const f16x4*>(&sAk[(16 * I + m) * RS16S + 16 * J + 4 * g]);
+                        const f16x4 Al =
+                            PREC ? *reinterpret_cast<const f16x4*>(&sAk[(16 * J + m) * RS16S + 16 * I + 4 * g]) : f16x4{};
+                        aw = mfma16(A, Xh[J], aw);
+                        au = mfma16(A, Uh[J], au);
+                        if (PREC) {
+                            aw = mfma16(A, Xl[J], aw);
+                            au = mfma16(A, Ul[J], au);
+                            aw = mfma16(Al, Xh[J], aw);
+                            au = mfma16(Al, Uh[J], au);
+                        }
+                    }
+                    const f16x4 T = *reinterpret_cast<const f16x4*>(&sAk[(16 * I + m) * RS16S + 16 * I + 4 * g]);
+                    f16x4 bwh, bwl, buh, bul;
+                    split4(aw, bwh, bwl);
+                    split4(au, buh, bul);
+                    const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+                    Xw[I] = mfma16(T, bwh, z);
+                    Ur[I] = mfma16(T, buh, z);
                     if (PREC) {
-                        aw = mfma16(A, Xl[J], aw);
-                        au = mfma16(A, Ul[J], au);
-                        aw = mfma16(Al, Xh[J], aw);
-                        au = mfma16(Al, Uh[J], au);
+                        const int tl = (16 * (I >> 1) + m) * RS16S + 32 + 16 * (I & 1) + 4 * g;
+                        const f16x4 Tl = *reinterpret_cast<const f16x4*>(&sAq[tl]);
+                        Xw[I] = mfma16(Tl, bwh, mfma16(T, bwl, Xw[I]));
+                        Ur[I] = mfma16(Tl, buh, mfma16(T, bul, Ur[I]));
+                    }
+                    if (I < 3) {
+                        split4(Xw[I], Xh[I], Xl[I]);
+                        split4(Ur[I], Uh[I], Ul[I]);
                     }
                 }
-                const f16x4 T = *reinterpret_cast<const f16x4*>(&sAk[(16 * I + m) * RS16S + 16 * I + 4 * g]);
-                f16x4 bwh, bwl, buh, bul;
-                split4(aw, bwh, bwl);
-                split4(au, buh, bul);
-                const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-                Xw[I] = mfma16(T, bwh, z);
-                Ur[I] = mfma16(T, buh, z);
-                if (PREC) {
-                    const f16x4 Tl = *reinterpret_cast<const f16x4*>(&sAq[(16 * (I >> 1) + m) * RS16S + 32 + 16 * (I & 1) +
-                                                                            4 * g]);
-                    Xw[I] = mfma16(Tl, bwh, mfma16(T, bwl, Xw[I]));
-                    Ur[I] = mfma16(Tl, buh, mfma16(T, bul, Ur[I]));
-                }
-                if (I < 3) {
-                    split4(Xw[I], Xh[I], Xl[I]);
-                    split4(Ur[I], Uh[I], Ul[I]);
-                }
+                const int pc = 32 * (c >> 5) + pos32(c & 31);
+#pragma unroll
+                for (int I = 0; I < 4; ++I)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) sW[(16 * I + 4 * g + e) * RS16 + pc] = (half_t)Xw[I][e];
             }
-            const int pc = 32 * (c >> 5) + pos32(c & 31);
-#pragma unroll
-            for (int I = 0; I < 4; ++I)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) sW[(16 * I + 4 * g + e) * RS16 + pc] = (half_t)Xw[I][e];
-        }
-        lds_barrier();
-        // ================= P7: the walk
-        if (cl + 1 < nch) load_row_g<RG>(p, h, t0 + 64, min(64, len - 64 * (cl + 1)), r, cb, nx);
-        // every-n row 0 is the state before the sequence's first token: stored before the first walk changes S (here
-        // rather than in the prologue, so that nothing before the first walk waits for the state loads)
-        if (cl == 0 && ck_mode == 2 && every > 0 && first == 0) ck_store(ck_idx[ck_row0]);
-        if (fix) {  // S <- (diag(d) - Kd^T W) S + Kd^T U and P <- (diag(d) - Kd^T W) P, sharing every A fragment
-            f16x8 SB[4], PB[4];
-#pragma unroll
-            for (int s = 0; s < 4; ++s)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    SB[s][e] = (half_t)S[2 * s][e];
-                    SB[s][4 + e] = (half_t)S[2 * s + 1][e];
-                    PB[s][e] = (half_t)Pm[2 * s][e];
-                    PB[s][4 + e] = (half_t)Pm[2 * s + 1][e];
-                }
-            f32x4 Vp[4], Wp[4];
-#pragma unroll
-            for (int it = 0; it < 4; ++it) {
-                f32x4 acc = {0.f, 0.f, 0.f, 0.f}, acp = acc;
-#pragma unroll
-                for (int s = 0; s < 4; ++s) {
-                    const f16x8 A = *reinterpret_cast<const f16x8*>(&sW[(16 * it + m) * RS16 + 32 * s + 8 * g]);
-                    acc = mfma32(A, SB[s], acc);
-                    acp = mfma32(A, PB[s], acp);
-                }
-#pragma unroll
-                for (int e = 0; e < 4; ++e) { Vp[it][e] = Ur[it][e] - acc[e]; Wp[it][e] = -acp[e]; }
-            }
-            f16x8 VB[2], WB[2], VL[2], WL[2];  // V' and -W P; PREC: also their low parts (fp16 pairs)
-#pragma unroll
-            for (int s = 0; s < 2; ++s)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    VB[s][e] = (half_t)Vp[2 * s][e];
-                    VB[s][4 + e] = (half_t)Vp[2 * s + 1][e];
-                    WB[s][e] = (half_t)Wp[2 * s][e];
-                    WB[s][4 + e] = (half_t)Wp[2 * s + 1][e];
-                    VL[s][e] = (half_t)(Vp[2 * s][e] - (float)VB[s][e]);
-                    VL[s][4 + e] = (half_t)(Vp[2 * s + 1][e] - (float)VB[s][4 + e]);
-                    WL[s][e] = (half_t)(Wp[2 * s][e] - (float)WB[s][e]);
-                    WL[s][4 + e] = (half_t)(Wp[2 * s + 1][e] - (float)WB[s][4 + e]);
-                }
-            // partial O^T = S^T Q~^T + V'^T A_qk^T (fp16, to `out`) and R^T = P^T Q~^T + W'^T A_qk^T (to the workspace),
-            // transposed tiles sharing the Q~ and A_qk fragments: lane (g, m) holds token 16 it + m, columns
-            // 16 w + 4 g .. + 3
-            half_t* rdst = ws_r + ((int64_t)(chain[C_RBASE] + cl) * H + h) * (64 * D) + 16 * w + 4 * g;
-#pragma unroll
-            for (int it = 0; it < 4; ++it) {
-                f32x4 acc = {0.f, 0.f, 0.f, 0.f}, acr = acc;
-#pragma unroll
-                for (int s = 0; s < 4; ++s) {
-                    const f16x8 B = *reinterpret_cast<const f16x8*>(&sQt[(16 * it + m) * RS16 + 32 * s + 8 * g]);
-                    acc = mfma32(SB[s], B, acc);
-                    acr = mfma32(PB[s], B, acr);
-                }
-#pragma unroll
-                for (int s = 0; s < 2; ++s)
-                    if (s <= (it >> 1)) {
-                        const f16x8 B = *reinterpret_cast<const f16x8*>(&sAq[(16 * it + m) * RS16S + 32 * s + 8 * g]);
-                        acc = mfma32(VB[s], B, acc);
-                        acr = mfma32(WB[s], B, acr);
-                    }
-                f16x4 o, rr;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) { o[e] = (half_t)(p.scale * acc[e]); rr[e] = (half_t)acr[e]; }
-                if (16 * it + m < L)
-                    *reinterpret_cast<f16x4*>(p.out + ((int64_t)t0 + 16 * it + m) * p.out_rs + (int64_t)h * D + 16 * w +
-                                              4 * g) = o;
-                *reinterpret_cast<f16x4*>(rdst + (16 * it + m) * D) = rr;
-            }
-#pragma unroll
-            for (int dt = 0; dt < 8; ++dt) {
-                const f32x4 d4 = *reinterpret_cast<const f32x4*>(&sF[F_DEC * 128 + 16 * dt + 4 * g]);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) { S[dt][e] *= d4[e]; Pm[dt][e] *= d4[e]; }
-#pragma unroll
-                for (int s = 0; s < 2; ++s) {
-                    const f16x8 A = *reinterpret_cast<const f16x8*>(&sKd[(16 * dt + (m ^ dt)) * RS16S + 32 * s + 8 * g]);
-                    S[dt] = mfma32(A, VB[s], S[dt]);
-                    Pm[dt] = mfma32(A, WB[s], Pm[dt]);
-                    if (PREC) {
-                        S[dt] = mfma32(A, VL[s], S[dt]);
-                        Pm[dt] = mfma32(A, WL[s], Pm[dt]);
-                    }
-                }
-            }
-        } else {
-            f16x8 SB[4];
-#pragma unroll
-            for (int s = 0; s < 4; ++s)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    SB[s][e] = (half_t)S[2 * s][e];
-                    SB[s][4 + e] = (half_t)S[2 * s + 1][e];
-                }
-            f32x4 Vp[4];
-#pragma unroll
-            for (int it = 0; it < 4; ++it) {
-                f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+            // the next item's gate dt_bias for its first raw-row phase (this chunk's has read sDT; the barrier below
+            // publishes the new values)
+            if (RG && !pf_here && more && tid < D) sDT[tid] = dtb_next;
+            lds_barrier();
+            // ================= P7: the walk
+            if (pf) load_row_g<RG>(p, pf_h, pf_t, pf_L, r, cb, nx);
+            // every-n row 0 is the state before the sequence's first token: stored before the first walk changes S
+            // (here rather than in the prologue, so that nothing before the first walk waits for the state loads)
+            if (cl == 0 && ck_mode == 2 && every > 0 && first == 0) ck_store(ck_idx[ck_row0]);
+            if (fix) {  // S <- (diag(d) - Kd^T W) S + Kd^T U and P <- (diag(d) - Kd^T W) P, sharing every A fragment
+                f16x8 SB[4], PB[4];
 #pragma unroll
                 for (int s = 0; s < 4; ++s)
-                    acc = mfma32(*reinterpret_cast<const f16x8*>(&sW[(16 * it + m) * RS16 + 32 * s + 8 * g]), SB[s], acc);
 #pragma unroll
-                for (int e = 0; e < 4; ++e) Vp[it][e] = Ur[it][e] - acc[e];
-            }
-            f16x8 VB[2], VL[2];  // V'; PREC: also its low part (an fp16 pair)
+                    for (int e = 0; e < 4; ++e) {
+                        SB[s][e] = (half_t)S[2 * s][e];
+                        SB[s][4 + e] = (half_t)S[2 * s + 1][e];
+                        PB[s][e] = (half_t)Pm[2 * s][e];
+                        PB[s][4 + e] = (half_t)Pm[2 * s + 1][e];
+                    }
+                f32x4 Vp[4], Wp[4];
 #pragma unroll
-            for (int s = 0; s < 2; ++s)
+                for (int it = 0; it < 4; ++it) {
+                    f32x4 acc = {0.f, 0.f, 0.f, 0.f}, acp = acc;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    VB[s][e] = (half_t)Vp[2 * s][e];
-                    VB[s][4 + e] = (half_t)Vp[2 * s + 1][e];
-                    VL[s][e] = (half_t)(Vp[2 * s][e] - (float)VB[s][e]);
-                    VL[s][4 + e] = (half_t)(Vp[2 * s + 1][e] - (float)VB[s][4 + e]);
+                    for (int s = 0; s < 4; ++s) {
+                        const f16x8 A = *reinterpret_cast<const f16x8*>(&sW[(16 * it + m) * RS16 + 32 * s + 8 * g]);
+                        acc = mfma32(A, SB[s], acc);
+                        acp = mfma32(A, PB[s], acp);
+                    }
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) { Vp[it][e] = Ur[it][e] - acc[e]; Wp[it][e] = -acp[e]; }
                 }
-            // O^T = S^T Q~^T + V'^T A_qk^T: the same fragments with the MFMA operands swapped give the transposed tile, so
-            // lane (g, m) holds token 16 it + m, values 16 w + 4 g .. + 3 and stores them to `out` with one 8-byte store
-            // (the 8 waves' 32-byte pieces of a token row meet in the L2)
-#pragma unroll
-            for (int it = 0; it < 4; ++it) {
-                f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int s = 0; s < 4; ++s)
-                    acc = mfma32(SB[s], *reinterpret_cast<const f16x8*>(&sQt[(16 * it + m) * RS16 + 32 * s + 8 * g]), acc);
+                f16x8 VB[2], WB[2], VL[2], WL[2];  // V' and -W P; PREC: also their low parts (fp16 pairs)
 #pragma unroll
                 for (int s = 0; s < 2; ++s)
-                    if (s <= (it >> 1))
-                        acc = mfma32(VB[s], *reinterpret_cast<const f16x8*>(&sAq[(16 * it + m) * RS16S + 32 * s + 8 * g]),
-                                     acc);
-                const u32x2 o = {f2bf2(p.scale * acc[0], p.scale * acc[1]), f2bf2(p.scale * acc[2], p.scale * acc[3])};
-                if (16 * it + m < L)
-                    *reinterpret_cast<u32x2*>(p.out + ((int64_t)t0 + 16 * it + m) * p.out_rs + (int64_t)h * D + 16 * w +
-                                              4 * g) = o;
-            }
 #pragma unroll
-            for (int dt = 0; dt < 8; ++dt) {
-                const f32x4 d4 = *reinterpret_cast<const f32x4*>(&sF[F_DEC * 128 + 16 * dt + 4 * g]);
+                    for (int e = 0; e < 4; ++e) {
+                        VB[s][e] = (half_t)Vp[2 * s][e];
+                        VB[s][4 + e] = (half_t)Vp[2 * s + 1][e];
+                        WB[s][e] = (half_t)Wp[2 * s][e];
+                        WB[s][4 + e] = (half_t)Wp[2 * s + 1][e];
+                        VL[s][e] = (half_t)(Vp[2 * s][e] - (float)VB[s][e]);
+                        VL[s][4 + e] = (half_t)(Vp[2 * s + 1][e] - (float)VB[s][4 + e]);
+                        WL[s][e] = (half_t)(Wp[2 * s][e] - (float)WB[s][e]);
+                        WL[s][4 + e] = (half_t)(Wp[2 * s + 1][e] - (float)WB[s][4 + e]);
+                    }
+                // partial O^T = S^T Q~^T + V'^T A_qk^T (fp16, to `out`) and R^T = P^T Q~^T + W'^T A_qk^T (to the
+                // workspace), transposed tiles sharing the Q~ and A_qk fragments: lane (g, m) holds token 16 it + m,
+                // columns 16 w + 4 g .. + 3
+                half_t* rdst = ws_r + ((int64_t)(cur.e[C_RBASE] + cl) * H + h) * (64 * D) + 16 * w + 4 * g;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) S[dt][e] *= d4[e];
+                for (int it = 0; it < 4; ++it) {
+                    f32x4 acc = {0.f, 0.f, 0.f, 0.f}, acr = acc;
 #pragma unroll
-                for (int s = 0; s < 2; ++s) {
-                    const f16x8 A = *reinterpret_cast<const f16x8*>(&sKd[(16 * dt + (m ^ dt)) * RS16S + 32 * s + 8 * g]);
-                    S[dt] = mfma32(A, VB[s], S[dt]);
-                    if (PREC) S[dt] = mfma32(A, VL[s], S[dt]);
+                    for (int s = 0; s < 4; ++s) {
+                        const f16x8 B = *reinterpret_cast<const f16x8*>(&sQt[(16 * it + m) * RS16 + 32 * s + 8 * g]);
+                        acc = mfma32(SB[s], B, acc);
+                        acr = mfma32(PB[s], B, acr);
+                    }
+#pragma unroll
+                    for (int s = 0; s < 2; ++s)
+                        if (s <= (it >> 1)) {
+                            const f16x8 B = *reinterpret_cast<const f16x8*>(&sAq[(16 * it + m) * RS16S + 32 * s + 8 * g]);
+                            acc = mfma32(VB[s], B, acc);
+                            acr = mfma32(WB[s], B, acr);
+                        }
+                    f16x4 o, rr;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) { o[e] = (half_t)(p.scale * acc[e]); rr[e] = (half_t)acr[e]; }
+                    if (16 * it + m < L)
+                        *reinterpret_cast<f16x4*>(p.out + ((int64_t)t0 + 16 * it + m) * p.out_rs + (int64_t)h * D + 16 * w +
+                                                  4 * g) = o;
+                    *reinterpret_cast<f16x4*>(rdst + (16 * it + m) * D) = rr;
+                }
+#pragma unroll
+                for (int dt = 0; dt < 8; ++dt) {
+                    const f32x4 d4 = *reinterpret_cast<const f32x4*>(&sF[F_DEC * 128 + 16 * dt + 4 * g]);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) { S[dt][e] *= d4[e]; Pm[dt][e] *= d4[e]; }
+#pragma unroll
+                    for (int s = 0; s < 2; ++s) {
+                        const f16x8 A = *reinterpret_cast<const f16x8*>(&sKd[(16 * dt + (m ^ dt)) * RS16S + 32 * s + 8 * g]);
+                        S[dt] = mfma32(A, VB[s], S[dt]);
+                        Pm[dt] = mfma32(A, WB[s], Pm[dt]);
+                        if (PREC) {
+                            S[dt] = mfma32(A, VL[s], S[dt]);
+                            Pm[dt] = mfma32(A, WL[s], Pm[dt]);
+                        }
+                    }
+                }
+            } else {
+                f16x8 SB[4];
+#pragma unroll
+                for (int s = 0; s < 4; ++s)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        SB[s][e] = (half_t)S[2 * s][e];
+                        SB[s][4 + e] = (half_t)S[2 * s + 1][e];
+                    }
+                f32x4 Vp[4];
+#pragma unroll
+                for (int it = 0; it < 4; ++it) {
+                    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int s = 0; s < 4; ++s)
+                        acc = mfma32(*reinterpret_cast<const f16x8*>(&sW[(16 * it + m) * RS16 + 32 * s + 8 * g]), SB[s], acc);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) Vp[it][e] = Ur[it][e] - acc[e];
+                }
+                f16x8 VB[2], VL[2];  // V'; PREC: also its low part (an fp16 pair)
+#pragma unroll
+                for (int s = 0; s < 2; ++s)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        VB[s][e] = (half_t)Vp[2 * s][e];
+                        VB[s][4 + e] = (half_t)Vp[2 * s + 1][e];
+                        VL[s][e] = (half_t)(Vp[2 * s][e] - (float)VB[s][e]);
+                        VL[s][4 + e] = (half_t)(Vp[2 * s + 1][e] - (float)VB[s][4 + e]);
+                    }
+                // O^T = S^T Q~^T + V'^T A_qk^T: the same fragments with the MFMA operands swapped give the transposed
+                // tile, so lane (g, m) holds token 16 it + m, values 16 w + 4 g .. + 3 and stores them to `out` with
+                // one 8-byte store (the 8 waves' 32-byte pieces of a token row meet in the L2)
+#pragma unroll
+                for (int it = 0; it < 4; ++it) {
+                    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int s = 0; s < 4; ++s)
+                        acc = mfma32(SB[s], *reinterpret_cast<const f16x8*>(&sQt[(16 * it + m) * RS16 + 32 * s + 8 * g]), acc);
+#pragma unroll
+                    for (int s = 0; s < 2; ++s)
+                        if (s <= (it >> 1))
+                            acc = mfma32(VB[s], *reinterpret_cast<const f16x8*>(&sAq[(16 * it + m) * RS16S + 32 * s + 8 * g]),
+                                         acc);
+                    const u32x2 o = {f2bf2(p.scale * acc[0], p.scale * acc[1]), f2bf2(p.scale * acc[2], p.scale * acc[3])};
+                    if (16 * it + m < L)
+                        *reinterpret_cast<u32x2*>(p.out + ((int64_t)t0 + 16 * it + m) * p.out_rs + (int64_t)h * D + 16 * w +
+                                                  4 * g) = o;
+                }
+#pragma unroll
+                for (int dt = 0; dt < 8; ++dt) {
+                    const f32x4 d4 = *reinterpret_cast<const f32x4*>(&sF[F_DEC * 128 + 16 * dt + 4 * g]);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) S[dt][e] *= d4[e];
+#pragma unroll
+                    for (int s = 0; s < 2; ++s) {
+                        const f16x8 A = *reinterpret_cast<const f16x8*>(&sKd[(16 * dt + (m ^ dt)) * RS16S + 32 * s + 8 * g]);
+                        S[dt] = mfma32(A, VB[s], S[dt]);
+                        if (PREC) S[dt] = mfma32(A, VL[s], S[dt]);
+                    }
                 }
             }
-        }
-        // checkpoints at chunk boundaries, counted in chunks of the whole sequence
-        const int cs = first + cl + 1;
-        if (fix) {  // the pair (S_loc, P) of this chunk boundary; the row is composed once S_start is known
-            int wsl = -1;
-            if (ck_mode == 1 && cs == ck_single) wsl = chain[C_CKWS1];
-            if (ck_mode == 2 && every > 0 && cs % every == 0 && cs < seqch) wsl = chain[C_CKWS] + cs / every - (first / every + 1);
-            if (wsl >= 0) {
-                store_state(ws_ck + ((int64_t)(2 * wsl) * H + h) * D * D, S, w, g, m);
-                store_state(ws_ck + ((int64_t)(2 * wsl + 1) * H + h) * D * D, Pm, w, g, m);
+            // checkpoints at chunk boundaries, counted in chunks of the whole sequence
+            const int cs = first + cl + 1;
+            if (fix) {  // the pair (S_loc, P) of this chunk boundary; the row is composed once S_start is known
+                int wsl = -1;
+                if (ck_mode == 1 && cs == ck_single) wsl = cur.e[C_CKWS1];
+                if (ck_mode == 2 && every > 0 && cs % every == 0 && cs < seqch)
+                    wsl = cur.e[C_CKWS] + cs / every - (first / every + 1);
+                if (wsl >= 0) {
+                    store_state(ws_ck + ((int64_t)(2 * wsl) * H + h) * D * D, S, w, g, m);
+                    store_state(ws_ck + ((int64_t)(2 * wsl + 1) * H + h) * D * D, Pm, w, g, m);
+                }
+            } else {
+                if (ck_mode == 1 && cs == ck_single) ck_store(ck_idx[n]);
+                if (ck_mode == 2 && every > 0 && cs % every == 0 && cs < seqch) ck_store(ck_idx[ck_row0 + cs / every]);
             }
-        } else {
-            if (ck_mode == 1 && cs == ck_single) ck_store(ck_idx[n]);
-            if (ck_mode == 2 && every > 0 && cs % every == 0 && cs < seqch) ck_store(ck_idx[ck_row0 + cs / every]);
+            // no barrier here: the walk writes no LDS (its outputs go straight to `out`) and reads none of what the
+            // next chunk's raw-row phase writes (raw v rows, gate rows, beta); the barrier after that phase orders
+            // everything the walk reads before the cumsum and factors overwrite it
         }
-        // no barrier here: the walk writes no LDS (its outputs go straight to `out`) and reads none of what the next
-        // chunk's raw-row phase writes (raw v rows, gate rows, beta); the barrier after that phase orders everything
-        // the walk reads before the cumsum and factors overwrite it
-    }
-    if (fix) {  // the piece's local end state (blocked order) and transition (fp16) for the scan; LDS is free now
-        float* st0 = reinterpret_cast<float*>(lds);
-        float* st1 = st0 + D * RS32;
-        lds_barrier();  // every wave has finished the walk's LDS reads
-        stage_state(st0, S, w, g, m);
-        stage_state(st1, Pm, w, g, m);
-        lds_barrier();
-        copy_staged_blocked(ws_h, st0);
-        copy_staged_h(reinterpret_cast<half_t*>(ws_h + ws_arr), st1);
-        return;
-    }
-    if (P1 && (pflags & PIECE_STORE_END)) {  // the first piece of a split sequence: the second piece's start state
-        store_state(p.ws + 2 * ws_arr + ((int64_t)(slot + 1) * H + h) * D * D, S, w, g, m);
-        return;
-    }
-    // ---- final state (the last piece of a sequence)
-    if (!(pflags & PIECE_LAST)) return;
-    if (pool) {
-        if (row >= 0 && row < p.state_slots) store_state(p.state_pool + row * p.state_ss + (int64_t)h * D * D, S, w, g, m);
-    } else {
-        store_state(p.final_state + ((int64_t)n * H + h) * D * D, S, w, g, m);
-    }
+        if (fix) {  // the piece's local end state (blocked order) and transition (fp16) for the scan; LDS is free now
+            float* st0 = reinterpret_cast<float*>(lds);
+            float* st1 = st0 + D * RS32;
+            lds_barrier();  // every wave has finished the walk's LDS reads
+            stage_state(st0, S, w, g, m);
+            stage_state(st1, Pm, w, g, m);
+            lds_barrier();
+            copy_staged_blocked(ws_h, st0);
+            copy_staged_h(reinterpret_cast<half_t*>(ws_h + ws_arr), st1);
+            return;
+        }
+        if (P1 && (pflags & PIECE_STORE_END)) {  // the first piece of a split sequence: the second piece's start state
+            store_state(p.ws + 2 * ws_arr + ((int64_t)(slot + 1) * H + h) * D * D, S, w, g, m);
+            return;
+        }
+        // ---- final state (the last piece of a sequence)
+        if (pflags & PIECE_LAST) {
+            if (pool) {
+                if (cur.row >= 0 && cur.row < p.state_slots)
+                    store_state(p.state_pool + cur.row * p.state_ss + (int64_t)h * D * D, S, w, g, m);
+            } else {
+                store_state(p.final_state + ((int64_t)n * H + h) * D * D, S, w, g, m);
+            }
+        }
+        if (!more) break;
+        // ---- the next item.  Its rows and dt_bias came in during this item's last chunk, unless this item had none.
+        const bool prefetched = nch > 0;
+        cur = load_item(++kpos);
+        if (!prefetched) {
+            load_row<RG>(p, cur.h, cur.tstart, cur.nch > 0 ? min(64, cur.len) : 0, r, cb, RB, nx);
+            if (RG && threadIdx.x < D) sDT[threadIdx.x] = dtb_next;
+            lds_barrier();
+        }
+        load_start_state(state_source(cur));
+        if (RG) Aexp = __expf(cur.alog);
+    }  // the workgroup's items
 }
 
 // Row-block composition used by the scan and the checkpoint compose: out[v][k] = L[v][k] + sum_k' X[v][k'] P[k'][k]
@@ -1401,7 +1487,7 @@ __global__ void __launch_bounds__(FX_THREADS) __attribute__((amdgpu_waves_per_eu
 }
 
 template <bool RG, bool P1, bool PREC>
-hipError_t launch_chunk(const PfParams& p, int list_off, int entries, hipStream_t s) {
+hipError_t launch_chunk(const PfParams& p, int list_off, int wgs, hipStream_t s) {
     static bool attr_set = false;  // idempotent; a race only repeats the call
     if (!attr_set) {
         const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&chunk_kernel<RG, P1, PREC>),
@@ -1409,14 +1495,14 @@ hipError_t launch_chunk(const PfParams& p, int list_off, int entries, hipStream_
         if (e != hipSuccess) return e;
         attr_set = true;
     }
-    hipLaunchKernelGGL((chunk_kernel<RG, P1, PREC>), dim3(entries * p.H), dim3(PF_THREADS), LDS_TOTAL, s, p, p.tab,
-                       p.ck_idx, list_off);
+    hipLaunchKernelGGL((chunk_kernel<RG, P1, PREC>), dim3(wgs), dim3(PF_THREADS), LDS_TOTAL, s, p, p.tab, p.ck_idx,
+                       list_off);
     return hipGetLastError();
 }
 template <bool P1>
-hipError_t launch_chunk_any(const PfParams& p, bool rg, bool prec, int list_off, int entries, hipStream_t s) {
-    return rg ? (prec ? launch_chunk<true, P1, true>(p, list_off, entries, s) : launch_chunk<true, P1, false>(p, list_off, entries, s))
-              : (prec ? launch_chunk<false, P1, true>(p, list_off, entries, s) : launch_chunk<false, P1, false>(p, list_off, entries, s));
+hipError_t launch_chunk_any(const PfParams& p, bool rg, bool prec, int list_off, int wgs, hipStream_t s) {
+    return rg ? (prec ? launch_chunk<true, P1, true>(p, list_off, wgs, s) : launch_chunk<true, P1, false>(p, list_off, wgs, s))
+              : (prec ? launch_chunk<false, P1, true>(p, list_off, wgs, s) : launch_chunk<false, P1, false>(p, list_off, wgs, s));
 }
 template <typename K>
 hipError_t launch_composer(K kernel, const PfParams& p, int entries, int threads, int smem, hipStream_t s,
@@ -1640,10 +1726,51 @@ extern "C" int kda355_prefill_plan(const KdaPrefillPlanIn* in, KdaPrefillPlan* p
         }
     }
     const int nfinal = (int)pieces.size(), nck = (int)cktasks.size();
+    // chain list: longest pieces first (they start earliest when the grid runs in several rounds)
+    std::vector<int> order(nfinal);
+    std::iota(order.begin(), order.end(), 0);
+    std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return pieces[a].count > pieces[b].count; });
+    // Workgroup lists (unsplit layouts whose (chain, head) items outnumber the CUs): one workgroup per CU walks a list
+    // of items in turn, fetching each next item's first rows and start state while the one before it finishes, so
+    // only its first item pays the start-up.  Items go in launch order (longest first) to the list with the least work
+    // so far.  Costed like the cuts above (one start-up per list, PASS_QUARTERS per later item), the lists are used
+    // when their schedule beats one workgroup per item dealt out by the hardware.
+    constexpr int64_t PASS_QUARTERS = 1;
+    const int64_t items = (int64_t)nfinal * in->H;
+    int grid = 0;
+    std::vector<std::vector<int32_t>> lists;
+    if (nsplit == 0 && items > num_cus && items < (1 << 30)) {
+        std::vector<int64_t> ld(num_cus, 0);
+        int64_t span_dyn = 0, wg = 0;
+        for (int i = 0; i < nfinal; ++i)
+            for (int hh = 0; hh < in->H; ++hh, ++wg) {
+                const auto b = ld.begin() + (wg % ngrp) * cus_per_grp, e = b + cus_per_grp;
+                std::pop_heap(b, e, std::greater<int64_t>());
+                *(e - 1) += 4 * pieces[order[i]].count + START_QUARTERS;
+                span_dyn = std::max(span_dyn, *(e - 1));
+                std::push_heap(b, e, std::greater<int64_t>());
+            }
+        typedef std::pair<int64_t, int> LoadWg;
+        std::priority_queue<LoadWg, std::vector<LoadWg>, std::greater<LoadWg>> q;
+        for (int b = 0; b < num_cus; ++b) q.push({0, b});
+        lists.assign(num_cus, {});
+        int64_t span_lst = 0;
+        for (int i = 0; i < nfinal; ++i)
+            for (int hh = 0; hh < in->H; ++hh) {
+                LoadWg top = q.top();
+                q.pop();
+                top.first += 4 * pieces[order[i]].count + (lists[top.second].empty() ? START_QUARTERS : PASS_QUARTERS);
+                lists[top.second].push_back(i * in->H + hh);
+                span_lst = std::max(span_lst, top.first);
+                q.push(top);
+            }
+        if (span_lst < span_dyn) grid = num_cus;
+    }
     const int64_t off_final = H_WORDS, off_fix = off_final + (int64_t)C_WORDS * nfinal;
     const int64_t off_scan = off_fix + (int64_t)X_WORDS * nfix;
     const int64_t off_ckc = off_scan + (int64_t)S_WORDS * nsplit;
-    const int64_t words = off_ckc + (int64_t)K_WORDS * nck;
+    const int64_t off_wg = off_ckc + (int64_t)K_WORDS * nck;
+    const int64_t words = off_wg + (grid ? grid + 1 + items : 0);
     plan->T = T;
     plan->N = N;
     plan->H = in->H;
@@ -1668,6 +1795,7 @@ extern "C" int kda355_prefill_plan(const KdaPrefillPlanIn* in, KdaPrefillPlan* p
     plan->num_split = nsplit;
     plan->num_fix_tasks = nfix;
     plan->num_ck_tasks = nck;
+    plan->chunk_grid = grid;
     if (!tables) return 0;
     KDA_CHECK_ARG(capacity >= words, "prefill_plan: table capacity %lld < %lld words", (long long)capacity, (long long)words);
     int32_t* t = tables;
@@ -1705,11 +1833,17 @@ extern "C" int kda355_prefill_plan(const KdaPrefillPlanIn* in, KdaPrefillPlan* p
         e[C_CKWS] = pc.ckws;
         e[C_CKWS1] = pc.ckws1;
     };
-    // chain list: longest pieces first (they start earliest when the grid runs in several rounds)
-    std::vector<int> order(nfinal);
-    std::iota(order.begin(), order.end(), 0);
-    std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return pieces[a].count > pieces[b].count; });
     for (int i = 0; i < nfinal; ++i) fill(t + off_final + (int64_t)C_WORDS * i, pieces[order[i]]);
+    if (grid) {  // [grid + 1] list starts, then the items of list 0, 1, ...
+        t[H_OFF_WG] = (int32_t)off_wg;
+        int32_t* ws = t + off_wg;
+        int32_t pos = 0;
+        for (int b = 0; b < grid; ++b) {
+            ws[b] = pos;
+            for (int32_t it : lists[b]) ws[grid + 1 + pos++] = it;
+        }
+        ws[grid] = pos;
+    }
     int xi = 0, si = 0;
     for (const Piece& pc : pieces) {
         if (pc.flags & PIECE_FIX) {
@@ -1749,6 +1883,9 @@ extern "C" int kda355_prefill_launch(const KdaPrefillArgs* a, kda355_stream_t st
     KDA_CHECK_ARG(a && a->plan, "prefill: null args or plan");
     const KdaPrefillPlan* pl = a->plan;
     KDA_CHECK_ARG(pl->magic == PLAN_MAGIC, "prefill: plan is not a kda355_prefill_plan() result");
+    KDA_CHECK_ARG(pl->chunk_grid >= 0 && (int64_t)pl->chunk_grid <= (int64_t)pl->num_chains * pl->H &&
+                      (pl->chunk_grid == 0 || pl->num_split == 0),
+                  "prefill: plan has an invalid chunk_grid %d", pl->chunk_grid);
     KDA_CHECK_ARG(pl->N == a->N && pl->T == a->T && pl->H == a->H,
                   "prefill: plan was made for another layout (N/T/H %d/%lld/%d vs %d/%lld/%d)", pl->N, (long long)pl->T,
                   pl->H, a->N, (long long)a->T, a->H);
@@ -1818,7 +1955,7 @@ extern "C" int kda355_prefill_launch(const KdaPrefillArgs* a, kda355_stream_t st
         // one chunk launch for every piece (first pieces from their true start states, later pieces from zero with their
         // transitions), then the start / final states of the split sequences, the later pieces' outputs and their
         // checkpoints
-        e = launch_chunk_any<true>(p, rg, prec, off_final, pl->num_chains, s);
+        e = launch_chunk_any<true>(p, rg, prec, off_final, pl->num_chains * a->H, s);
         // every split sequence has >= 2 pieces, so the most-cut one has at most num_pieces - 2 (num_split - 1)
         const bool lean = pl->num_pieces - 2 * (pl->num_split - 1) <= 3;
         if (pl->num_pieces == 2 * pl->num_split) {  // every split sequence in 2 pieces: the scan joins the tail launch
@@ -1828,7 +1965,9 @@ extern "C" int kda355_prefill_launch(const KdaPrefillArgs* a, kda355_stream_t st
             if (e == hipSuccess) e = launch_tail(p, 0, pl->num_fix_tasks, pl->num_ck_tasks, s);
         }
     } else {
-        e = launch_chunk_any<false>(p, rg, prec, off_final, pl->num_chains, s);
+        // one workgroup per (chain, head), or the plan's workgroup lists
+        const int wgs = pl->chunk_grid > 0 ? pl->chunk_grid : pl->num_chains * a->H;
+        e = launch_chunk_any<false>(p, rg, prec, off_final, wgs, s);
     }
     if (e != hipSuccess) {
         set_error("prefill: launch failed: %s", hipGetErrorString(e));

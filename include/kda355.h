@@ -213,6 +213,9 @@ typedef struct KdaPrefillPlan {
     int32_t num_fix_tasks;      /* groups of <= 2 chunks of the later pieces of split sequences (outputs completed after
                                    the scan) */
     int32_t num_ck_tasks;       /* checkpoints inside later pieces (composed after the scan) */
+    int32_t chunk_grid;         /* workgroups of the chunk launch: 0 = one per (chain, head); > 0 (layouts without
+                                   split sequences whose (chain, head) pairs outnumber the CUs) = that many
+                                   workgroups, each walking a list of (chain, head) pairs in turn */
 } KdaPrefillPlan;
 
 /*

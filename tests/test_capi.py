@@ -166,6 +166,37 @@ def test_prefill_plan_host_only():
     assert L.kda355_prefill_plan(ctypes.byref(pin), ctypes.byref(pl), None, 0) == _lib.EINVAL
 
 
+def _lists(pl, tab, H):
+    """The workgroup lists of a plan: per list, the (chain entry, head) items and their chunk counts."""
+    G, off = int(pl.chunk_grid), int(tab[17])
+    starts = tab[off:off + G + 1]
+    items = tab[off + G + 1:off + G + 1 + int(starts[-1])]
+    nch = lambda it: int(tab[20 + 13 * (int(it) // H) + 1])  # noqa: E731
+    return [[(int(it), nch(it)) for it in items[starts[b]:starts[b + 1]]] for b in range(G)]
+
+
+def test_prefill_plan_workgroup_lists():
+    """Unsplit layouts with more (chain, head) items than CUs get workgroup lists when the list schedule is shorter
+    (one workgroup per CU walks its items in turn): the lists partition the items and each runs longest first.
+    Layouts that fit the CUs, split layouts and layouts the lists would not shorten keep one workgroup per item."""
+    pl, tab = _plan([128] * 64, 12, 256)                 # the reference's p_64x128: 768 two-chunk items
+    assert pl.num_split == 0 and pl.chunk_grid == 256
+    ls = _lists(pl, tab, 12)
+    assert sorted(it for lst in ls for it, _ in lst) == list(range(768)) and {len(lst) for lst in ls} == {3}
+    lens, H = [130, 0, 777, 64, 1, 250, 64], 5       # mixed lengths, an empty sequence, on 3 CUs
+    pl, tab = _plan(lens, H, 3)
+    assert pl.num_split == 0 and pl.chunk_grid == 3
+    ls = _lists(pl, tab, H)
+    assert sorted(it for lst in ls for it, _ in lst) == list(range(len(lens) * H))
+    for lst in ls:
+        assert [c for _, c in lst] == sorted((c for _, c in lst), reverse=True)
+    loads = [sum(c for _, c in lst) for lst in ls]
+    assert max(loads) - min(loads) <= 13                 # within one longest item
+    for lens, H, cus in (([131072], 32, 256), ([704, 1216, 512], 96, 256), ([100] * 10, 4, 256)):
+        pl, tab = _plan(lens, H, cus)                    # split / no gain (p96_light8k_0) / fits the CUs
+        assert pl.chunk_grid == 0 and tab[17] == 0
+
+
 def test_prefill_plan_splits_long_sequences():
     """With idle CUs, long sequences are cut into pieces of >= 2 chunks; full chips are not split."""
     pl, tab = _plan([131072], 32, 256)                   # configuration 2: 2048 chunks x 32 heads on 256 CUs

@@ -34,9 +34,17 @@ def _check_out(got, ref, what, cu=None):
     return check_out(got, ref, what, cu)
 
 
-def _plain_case(oracle, H, lens, seed, init=True, gscale=1.0, heads_checked=None, gmod=None, precise=False):
+def _list_meta(kda, lens, H, cus, **kw):
+    """A plan for `cus` CUs that uses workgroup lists (one workgroup per CU walking several (sequence, head) items)."""
+    meta = kda.plan(torch.tensor(_cu(lens)), H, device=DEV, num_cus=cus, **kw)
+    assert meta.split == (0, 0) and int(meta.plan.chunk_grid) == cus, (meta.split, int(meta.plan.chunk_grid))
+    return meta
+
+
+def _plain_case(oracle, H, lens, seed, init=True, gscale=1.0, heads_checked=None, gmod=None, precise=False, cus=None):
     kda = _kda()
-    _say(f"plain H={H} lens={lens[:10]} init={init} seed={seed}" + (" precise" if precise else ""))
+    _say(f"plain H={H} lens={lens[:10]} init={init} seed={seed}" + (" precise" if precise else "") +
+         (f" lists on {cus} CUs" if cus else ""))
     g = gen(seed)
     T = int(sum(lens))
     q, k, v, gg, beta = config_inputs(T, H, g)
@@ -46,9 +54,10 @@ def _plain_case(oracle, H, lens, seed, init=True, gscale=1.0, heads_checked=None
     N = len(lens)
     h0 = torch.randn(N, H, D, D, generator=g) * 0.02 if init else None
     cu = torch.tensor(_cu(lens), dtype=torch.int32)
+    meta = _list_meta(kda, lens, H, cus) if cus else None
     o, fin = kda.chunk_kda(q[None].to(DEV), k[None].to(DEV), v[None].to(DEV), gg[None].to(DEV), beta[None].to(DEV),
                            initial_state=h0.to(DEV) if init else None, output_final_state=True, cu_seqlens=cu.to(DEV),
-                           precise=precise)
+                           precise=precise, meta=meta)
     torch.cuda.synchronize()
     hs = list(range(H)) if heads_checked is None else heads_checked
     sel = lambda x: np.ascontiguousarray(f32(x)[:, hs])  # noqa: E731
@@ -78,6 +87,18 @@ def test_precise_mode_whole_and_split(oracle):
 
 def test_ragged_tiny_and_empty(oracle):
     _plain_case(oracle, 3, [1, 17, 33, 0, 1, 63, 65, 128, 2], 2)
+
+
+def test_workgroup_lists_plain(oracle):
+    """Workgroup lists: unsplit layouts with more (sequence, head) items than workgroups, each workgroup walking its
+    list in turn (the next item's rows prefetched in the last chunk of the one before, its start state loaded after
+    that one's final state is stored).  Planned for 4 and 3 CUs: lists of 10-27 items mixing empty, one-token, ragged
+    and multi-chunk sequences, with and without initial states, and at the bench's p_64x128 shape on the device's CUs
+    (three two-chunk items per list)."""
+    _plain_case(oracle, 3, [1, 17, 33, 0, 1, 63, 65, 128, 2, 0, 300, 64, 200], 90, cus=4)
+    _plain_case(oracle, 5, [130, 0, 777, 64, 1, 250, 64], 91, init=False, cus=3)
+    cus = torch.cuda.get_device_properties(DEV).multi_processor_count
+    _plain_case(oracle, 12, [128] * 64, 92, heads_checked=[0, 5, 11], cus=cus)
 
 
 def test_other_head_counts(oracle):
@@ -221,15 +242,17 @@ def _pages(slots, H, taps, g):
     return raw, ssm
 
 
-def test_serving_pool_checkpoints_page_layout(oracle):
+@pytest.mark.parametrize("cus", [None, 4])
+def test_serving_pool_checkpoints_page_layout(oracle, cus):
     """prefill_prepare + prefill on the page layout: has_initial_state with NaN rows, one checkpoint per sequence,
-    strided raw_beta, out a slice behind 256 leading rows; only out and the named rows change."""
+    strided raw_beta, out a slice behind 256 leading rows; only out and the named rows change.  cus = 4: planned as
+    workgroup lists on 4 CUs (7 items per list, gates in the kernel: each item's dt_bias handed to the next)."""
     kda = _kda()
     H = 4
     lens = [777, 64, 1, 130, 1024, 17, 255]
     hinit = [1, 0, 1, 0, 1, 1, 0]
     ck_off = [704, 64, 0, 0, 1024, 0, 192]
-    _say(f"serving pool H={H} lens={lens}")
+    _say(f"serving pool H={H} lens={lens} cus={cus}")
     g = gen(40)
     T, N = sum(lens), len(lens)
     q, k, v, raw_g, raw_b, A_log, dt_bias = _raw_inputs(g, T, H)
@@ -253,7 +276,8 @@ def test_serving_pool_checkpoints_page_layout(oracle):
     out = parent[:, 256:256 + T]
     parent_before = parent.clone()
     cu_cpu = torch.tensor(_cu(lens), dtype=torch.int32)
-    meta = kda.prefill_prepare(cu_cpu, H, torch.tensor(ck_off, dtype=torch.int32), cidx, device=DEV)
+    meta = (kda.prefill_prepare(cu_cpu, H, torch.tensor(ck_off, dtype=torch.int32), cidx, device=DEV) if cus is None
+            else _list_meta(kda, lens, H, cus, checkpoint_offsets=torch.tensor(ck_off, dtype=torch.int32)))
     kda.prefill(q[None].to(DEV), k[None].to(DEV), v[None].to(DEV), raw_g[None].to(DEV), beta_view, A_log.to(DEV),
                 dt_bias.to(DEV), D ** -0.5, -5.0, ssm, sidx.to(DEV), torch.tensor(hinit, dtype=torch.bool).to(DEV),
                 cu_cpu.to(DEV), out, torch.tensor(ck_off, dtype=torch.int32).to(DEV), cidx.to(DEV), meta=meta)
@@ -303,13 +327,15 @@ def test_serving_no_sync_with_meta():
     assert torch.isfinite(out.float()).all()
 
 
-@pytest.mark.parametrize("every", [64, 256])
-def test_every_n_checkpoints_fp32_and_bf16(oracle, every):
+@pytest.mark.parametrize("every,cus", [(64, None), (256, None), (64, 4)])
+def test_every_n_checkpoints_fp32_and_bf16(oracle, every, cus):
     """B200 every-n rows (kda/b200/test_kda_b200.py:213-240): fp32 rows match the oracle; bf16 rows are exactly the
-    fp32 rows rounded to nearest even; output and pool are identical across checkpoint dtypes."""
+    fp32 rows rounded to nearest even; output and pool are identical across checkpoint dtypes.  cus = 4: planned as
+    workgroup lists on 4 CUs."""
     kda = _kda()
     H, lens = 4, [300, 64, 1, 1000, 77]
-    _say(f"every-n every={every}")
+    _say(f"every-n every={every} cus={cus}")
+    meta = _list_meta(kda, lens, H, cus, ck_every=every) if cus else None
     g = gen(50 + every)
     T, N = sum(lens), len(lens)
     q, k, v, raw_g, raw_b, A_log, dt_bias = _raw_inputs(g, T, H)
@@ -326,7 +352,7 @@ def test_every_n_checkpoints_fp32_and_bf16(oracle, every):
         res = kda.kda_prefill(q[None].to(DEV), k[None].to(DEV), v[None].to(DEV), raw_g[None].to(DEV),
                               raw_b[None].to(DEV), A_log.to(DEV), dt_bias.to(DEV), pool,
                               torch.tensor(_cu(lens)).to(DEV), ssm_state_indices=idx.to(DEV), state_checkpoints=ck,
-                              checkpoint_cu_starts=ccs.to(DEV), checkpoint_every_n_tokens=every)
+                              checkpoint_cu_starts=ccs.to(DEV), checkpoint_every_n_tokens=every, meta=meta)
         torch.cuda.synchronize()
         assert len(res) == 3 and res[2] is ck and res[1] is pool
         got[dt] = (res[0].clone(), pool.clone(), ck)
