@@ -197,6 +197,29 @@ def test_prefill_plan_workgroup_lists():
         assert pl.chunk_grid == 0 and tab[17] == 0
 
 
+def test_prefill_plan_workgroup_lists_random_layouts():
+    """Planner invariants over seeded random layouts and CU counts: a plan with workgroup lists splits nothing, has
+    more items than lists, and its lists partition the items, each longest first; a plan without lists has no list
+    section."""
+    rng = np.random.default_rng(7)
+    with_lists = 0
+    for _ in range(60):
+        N, H, cus = int(rng.integers(1, 40)), int(rng.integers(1, 9)), int(rng.choice([2, 3, 8, 32, 64, 256]))
+        lens = [int(x) for x in rng.integers(0, 1500, size=N)]
+        lens[int(rng.integers(0, N))] = 0
+        pl, tab = _plan(lens, H, cus)
+        if pl.chunk_grid == 0:
+            assert tab[17] == 0
+            continue
+        with_lists += 1
+        assert pl.num_split == 0 and pl.chunk_grid == cus < pl.num_chains * H
+        ls = _lists(pl, tab, H)
+        assert sorted(it for lst in ls for it, _ in lst) == list(range(pl.num_chains * H))
+        for lst in ls:
+            assert [c for _, c in lst] == sorted((c for _, c in lst), reverse=True)
+    assert with_lists >= 10
+
+
 def test_prefill_plan_splits_long_sequences():
     """With idle CUs, long sequences are cut into pieces of >= 2 chunks; full chips are not split."""
     pl, tab = _plan([131072], 32, 256)                   # configuration 2: 2048 chunks x 32 heads on 256 CUs

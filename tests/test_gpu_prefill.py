@@ -101,6 +101,18 @@ def test_workgroup_lists_plain(oracle):
     _plain_case(oracle, 12, [128] * 64, 92, heads_checked=[0, 5, 11], cus=cus)
 
 
+def test_workgroup_lists_random_layouts(oracle):
+    """Workgroup lists on seeded random layouts (empty, one-token and up to 12-chunk sequences; 2 to 7 CUs, so lists of
+    many items of mixed lengths), with and without initial states, given gates; against the oracle."""
+    rng = np.random.default_rng(11)
+    for i in range(3):
+        N, H, cus = int(rng.integers(6, 16)), int(rng.integers(2, 6)), int(rng.integers(2, 8))
+        lens = [int(x) for x in rng.integers(0, 768, size=N)]
+        lens[int(rng.integers(0, N))] = 0
+        lens[int(rng.integers(0, N))] = 1
+        _plain_case(oracle, H, lens, 95 + i, init=bool(i % 2 == 0), cus=cus)
+
+
 def test_other_head_counts(oracle):
     for i, (H, lens) in enumerate([(1, [700]), (8, [37, 200]), (16, [129, 64])]):
         _plain_case(oracle, H, lens, 10 + i)
