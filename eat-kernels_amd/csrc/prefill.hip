@@ -509,10 +509,10 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
             const bool pf_here = cl + 1 < nch, pf = pf_here || more;
             const int pf_h = pf_here ? h : nx_h, pf_t = pf_here ? t0 + 64 : nx_t;
             const int pf_L = pf_here ? min(64, len - 64 * (cl + 1)) : (nx_nch > 0 ? min(64, nx_len) : 0);
-            // ================= P0: this chunk's raw rows (prefetched during the previous chunk) The raw q and k stay
-            // in registers until P2 (the next chunk's q, k loads reuse them from P5 on); the raw v goes to an LDS slot
-            // that only this thread reads back (the W area, which is free until P6), so its registers die here and the
-            // next chunk's v loads reuse them without a loop-carried copy.
+            // ================= P0: this chunk's raw rows (prefetched during the previous chunk)
+            // The raw q and k stay in registers until P2 (the next chunk's q, k loads reuse them from P5 on); the raw v
+            // goes to an LDS slot that only this thread reads back (the W area, which is free until P6), so its
+            // registers die here and the next chunk's v loads reuse them without a loop-carried copy.
             *reinterpret_cast<u32x4*>(lds + LDS_W + r * (2 * RS16) + 32 * cb) = nx.v[0];
             *reinterpret_cast<u32x4*>(lds + LDS_W + r * (2 * RS16) + 32 * cb + 16) = nx.v[1];
             float gv[16];
@@ -773,8 +773,9 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
             }
             // no barrier here: the reads below touch only the raw v staging and the thread's own q^ fi / k^ fj rows,
             // which the Gram phase neither writes nor overwrites; the barrier before the layouts orders every Gram read
-            // of regions B and C before they are rewritten ================= P5: Q~, Kd^T, beta v into their walk
-            // layouts (raw threads) The initial state loads (issued in the prologue) complete here, before any
+            // of regions B and C before they are rewritten
+            // ================= P5: Q~, Kd^T, beta v into their walk layouts (raw threads)
+            // The initial state loads (issued in the prologue or at the item's start) complete here, before any
             // next-chunk row is in flight: an empty use of S makes the compiler's wait for them fall at this point,
             // where in every later chunk only the long-finished output stores are outstanding, instead of before each
             // walk, where it would also wait for the prefetched rows.
@@ -814,7 +815,8 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
             // no barrier here: the solve reads k^ fi (region A), the raw v rows, -A_kk / T_II, the factors and beta,
             // none of which the layouts above write; it writes W into region B's upper half, whose last reader (the
             // operand reads before the layouts) passed the barrier above.  The walk reads the layouts after the solve's
-            // barrier. ================= P6: W and U by block forward substitution (wave w: channel / value tile w)
+            // barrier.
+            // ================= P6: W and U by block forward substitution (wave w: channel / value tile w)
             if (pf) load_row_vb(p, pf_h, pf_t, pf_L, r, cb, RB, nx);
             f32x4 Ur[4];
             {
