@@ -605,7 +605,8 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
                 }
             }
             {
-                const int c = tid & 127, qd = tid >> 7;
+                // qd is wave-uniform (128 threads per value): the row selection below branches on the scalar unit
+                const int c = tid & 127, qd = __builtin_amdgcn_readfirstlane(tid >> 7);
                 const float o1 = sWt[c], o2 = o1 + sWt[128 + c], o3 = o2 + sWt[256 + c];
                 // Gamma at rows 8 i + 7: block middles (sGM) and segment ends (sWt), plus the earlier segments
                 float gr[8];
@@ -670,10 +671,13 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
                 }
                 f32x4 lt;
                 f16x4 aq;
+                // beta of rows 16 I + 4 g .. + 3, read whatever the mask (a read under the mask would branch and wait
+                // for every outstanding LDS operation)
+                const f32x4 bt4 = *reinterpret_cast<const f32x4*>(&sBeta[16 * I + 4 * g]);
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const int rr = 4 * g + e, rw = 16 * I + rr;
-                    lt[e] = (m < rr) ? sBeta[rw] * akk[e] : 0.f;
+                    const int rr = 4 * g + e;
+                    lt[e] = (m < rr) ? bt4[e] * akk[e] : 0.f;
                     aq[e] = (half_t)((rr <= m) ? aqk[e] : 0.f);  // A_qk[16 I + m][16 I + rr], causal within the block
                 }
                 *reinterpret_cast<f16x4*>(&sAq[i * RS16S + pos64(16 * I + 4 * g)]) = aq;
