@@ -520,16 +520,25 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
                 float rg[16];
                 const u32x4 gg[2] = {nx.g[0], nx.g[1]};
                 unpack16(gg, rg);
+                // every row is computed and rows >= L are zeroed after (their raw gate reads as 0): a computation under
+                // the row mask would branch per value and wait for every outstanding LDS read
 #pragma unroll
-                for (int c = 0; c < 16; ++c)
-                    gv[c] = (r < L) ? clamp_decay(p.lb * sigmoidf_(Aexp * (rg[c] + sDT[16 * cb + c]))) : 0.f;
+                for (int q4 = 0; q4 < 4; ++q4) {
+                    const f32x4 dt4 = *reinterpret_cast<const f32x4*>(&sDT[16 * cb + 4 * q4]);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float x = clamp_decay(p.lb * sigmoidf_(Aexp * (rg[4 * q4 + e] + dt4[e])));
+                        gv[4 * q4 + e] = (r < L) ? x : 0.f;
+                    }
+                }
             } else {
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
 #pragma unroll
                     for (int j = 0; j < 4; ++j) gv[4 * i + j] = clamp_decay(__uint_as_float(nx.g[i][j]));
             }
-            const float bt = (r >= L) ? 0.f : (RB ? sigmoidf_(bf2f(nx.beta)) : __uint_as_float(nx.beta));
+            const float bx = RB ? sigmoidf_(bf2f(nx.beta)) : __uint_as_float(nx.beta);
+            const float bt = (r >= L) ? 0.f : bx;
 #pragma unroll
             for (int c = 0; c < 16; ++c) gv[c] *= 1.4426950408889634f;  // log2(e): the cumsum runs in log2 units
             float rq = 1.f, rk = 1.f;
