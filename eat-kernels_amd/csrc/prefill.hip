@@ -128,6 +128,9 @@ __device__ __forceinline__ bf16x8 as_bf16x8(const uint32_t (&w)[4]) {
 }
 // 2^x (v_exp_f32)
 __device__ __forceinline__ float exp2_(float x) { return __builtin_amdgcn_exp2f(x); }
+// sigmoid through the hardware reciprocal (v_rcp_f32, within 1 ulp): the IEEE division of sigmoidf_ is a sequence of
+// about ten instructions, and the raw-row phase takes 17 sigmoids per thread and chunk
+__device__ __forceinline__ float sigmoid_rcp(float x) { return __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
 // A per-token log-decay below KDA355_MIN_LOG_DECAY (-9) is raised to it: the diagonal Gram blocks hold e^{+-8 g} over
 // 8 tokens, inside 2^{+-104} for g >= -9, where the factors and the low halves of their bf16 pairs stay normal (the
 // MFMAs flush subnormal operands; at -11 the factors reach 2^-127).  The state change this makes is below e^{-9} =
@@ -527,7 +530,7 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
                     const f32x4 dt4 = *reinterpret_cast<const f32x4*>(&sDT[16 * cb + 4 * q4]);
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
-                        const float x = clamp_decay(p.lb * sigmoidf_(Aexp * (rg[4 * q4 + e] + dt4[e])));
+                        const float x = clamp_decay(p.lb * sigmoid_rcp(Aexp * (rg[4 * q4 + e] + dt4[e])));
                         gv[4 * q4 + e] = (r < L) ? x : 0.f;
                     }
                 }
@@ -537,7 +540,7 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
 #pragma unroll
                     for (int j = 0; j < 4; ++j) gv[4 * i + j] = clamp_decay(__uint_as_float(nx.g[i][j]));
             }
-            const float bx = RB ? sigmoidf_(bf2f(nx.beta)) : __uint_as_float(nx.beta);
+            const float bx = RB ? sigmoid_rcp(bf2f(nx.beta)) : __uint_as_float(nx.beta);
             const float bt = (r >= L) ? 0.f : bx;
 #pragma unroll
             for (int c = 0; c < 16; ++c) gv[c] *= 1.4426950408889634f;  // log2(e): the cumsum runs in log2 units
