@@ -557,8 +557,9 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
                 for (int c = 0; c < 16; ++c) { sq += qf[c] * qf[c]; sk += kf[c] * kf[c]; }
                 sq = sum8(sq);
                 sk = sum8(sk);
-                rq = __builtin_amdgcn_rcpf(fmaxf(sqrtf(sq), 1e-6f));
-                rk = __builtin_amdgcn_rcpf(fmaxf(sqrtf(sk), 1e-6f));
+                // 1 / max(|x|, 1e-6) = rsqrt(max(|x|^2, 1e-12)) through v_rsq_f32 (the IEEE sqrt is a sequence)
+                rq = __builtin_amdgcn_rsqf(fmaxf(sq, 1e-12f));
+                rk = __builtin_amdgcn_rsqf(fmaxf(sk, 1e-12f));
             }
 #pragma unroll
             for (int i = 0; i < 4; ++i)
