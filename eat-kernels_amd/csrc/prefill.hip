@@ -1925,6 +1925,11 @@ extern "C" int kda355_prefill_launch(const KdaPrefillArgs* a, kda355_stream_t st
                                            : (aligned(a->g, 16) && a->g_row_stride % 4 == 0),
                   "prefill: g rows must be 16-byte aligned");
     KDA_CHECK_ARG(aligned(a->out, 16) && a->out_row_stride % 8 == 0, "prefill: out rows must be 16-byte aligned");
+    // the kernels address the rows of one 64-token chunk with 32-bit offsets
+    KDA_CHECK_ARG(a->qkv_row_stride < (1 << 21) && a->g_row_stride < (1 << 21) && a->beta_row_stride < (1 << 21) &&
+                      a->out_row_stride < (1 << 21) && a->qkv_row_stride >= 0 && a->g_row_stride >= 0 &&
+                      a->beta_row_stride >= 0 && a->out_row_stride >= 0,
+                  "prefill: row strides must be in [0, 2^21) elements");
     KDA_CHECK_ARG(!pool || (aligned(a->state_pool, 16) && a->state_slot_stride % 4 == 0), "prefill: state pool misaligned");
     KDA_CHECK_ARG(pool || (aligned(a->final_state, 16) && (!a->initial_state || aligned(a->initial_state, 16))),
                   "prefill: states misaligned");

@@ -252,7 +252,8 @@ typedef struct KdaPrefillArgs {
     const int32_t* ck_idx;           /* CK_SINGLE: [N] rows; CK_EVERY: [ck_rows] rows */
     const int32_t* tables;           /* device copy of the plan's schedule table */
     void* workspace;                 /* >= plan->workspace_bytes, 256-byte aligned */
-    int64_t qkv_row_stride, g_row_stride, beta_row_stride, out_row_stride;  /* elements between tokens */
+    int64_t qkv_row_stride, g_row_stride, beta_row_stride, out_row_stride;  /* elements between tokens, each
+                                                                              in [0, 2^21) */
     int64_t state_slot_stride, state_slots, ck_slot_stride, ck_slots;
     int64_t T;
     int32_t N, H;

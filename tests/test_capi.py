@@ -46,6 +46,33 @@ def test_noalloc_rejects_oversized_layout():
     assert b"static scratch" in _lib.lib().kda355_last_error()
 
 
+def test_prefill_rejects_oversized_row_strides():
+    """Row strides of 2^21 elements or more (the kernels address a chunk's rows with 32-bit offsets) are rejected with
+    KDA355_EINVAL before any device call; a stride just below passes that check and the call fails on the next one
+    (a pool slot stride that is not a multiple of 4, on purpose), still before any device call."""
+    import kda355
+    from kda355 import _lib
+    L = _lib.lib()
+    T, H = 256, 2
+    meta = kda355.plan(np.array([0, T], np.int64), H, device=None)
+    a = _lib.KdaPrefillArgs()
+    fake = ctypes.c_void_p(1 << 20)                      # never dereferenced: the call is rejected first
+    for f in ("q", "k", "v", "g", "beta", "out", "tables", "final_state"):
+        setattr(a, f, fake)
+    a.T, a.N, a.H = T, 1, H
+    a.plan = ctypes.pointer(meta.plan)
+    a.qkv_row_stride, a.g_row_stride, a.beta_row_stride, a.out_row_stride = H * 128, H * 128, H, 1 << 21
+    assert L.kda355_prefill_launch(ctypes.byref(a), None) == _lib.EINVAL
+    assert b"row strides" in L.kda355_last_error()
+    a.out_row_stride, a.qkv_row_stride = H * 128, (1 << 21) + 8
+    assert L.kda355_prefill_launch(ctypes.byref(a), None) == _lib.EINVAL
+    assert b"row strides" in L.kda355_last_error()
+    a.qkv_row_stride, a.flags = (1 << 21) - 8, 8          # KDA355_PF_POOL
+    a.state_pool, a.state_idx, a.has_initial_state, a.state_slot_stride = fake, fake, fake, 3
+    assert L.kda355_prefill_launch(ctypes.byref(a), None) == _lib.EINVAL
+    assert b"state pool misaligned" in L.kda355_last_error()
+
+
 def test_invalid_arguments_rejected_without_gpu():
     from kda355 import _lib
     L = _lib.lib()
