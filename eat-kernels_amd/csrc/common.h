@@ -68,7 +68,8 @@ __device__ __forceinline__ float sum16(float x) {
     return x;
 }
 
-__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + __expf(-x)); }
+// through the hardware reciprocal (v_rcp_f32, within 1 ulp): an IEEE division is a sequence of about ten instructions
+__device__ __forceinline__ float sigmoidf_(float x) { return __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
 
 // Workgroup barrier that orders LDS only: __syncthreads() also waits for every outstanding global load and store
 // (vmcnt(0)), which would stall on loads issued for later phases.
