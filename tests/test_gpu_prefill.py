@@ -601,6 +601,48 @@ def test_split_pool_every_n_checkpoints(oracle, ckdt):
             assert np.isnan(got[i]).all(), f"checkpoint row {i} should be untouched"
 
 
+def test_split_random_layouts_raw_gates_every_n(oracle):
+    """Seeded random layouts planned for 32 or 64 CUs, so that the longer sequences are cut into pieces, through the
+    gate-in-kernel call on a pool with every-n checkpoints (rows in later pieces are composed after the scan): output,
+    final pool rows and every fp32 checkpoint row against the oracle."""
+    kda = _kda()
+    rng = np.random.default_rng(17)
+    for i in range(3):
+        N, H, cus, every = int(rng.integers(2, 6)), int(rng.integers(1, 5)), int(rng.choice([32, 64])), 128
+        lens = [int(x) for x in rng.integers(1, 2600, size=N)]
+        lens[0] = int(rng.integers(2048, 4096))
+        g = gen(300 + i)
+        T = sum(lens)
+        q, k, v, raw_g, raw_b, A_log, dt_bias = _raw_inputs(g, T, H)
+        P = N + 2
+        pool0 = torch.randn(P, H, D, D, generator=g) * 0.1
+        idx = torch.randperm(P, generator=g)[:N].to(torch.int32)
+        counts = [-(-L // every) for L in lens]
+        ccs = torch.tensor(_cu(counts), dtype=torch.int64)
+        C = int(sum(counts))
+        meta = kda.plan(torch.tensor(_cu(lens)), H, ck_every=every, device=DEV, num_cus=cus)
+        _say(f"split random {i}: H={H} lens={lens} cus={cus} pieces={meta.split}")
+        assert meta.split[1] >= 1, "the layout is meant to be split"
+        pool = pool0.clone().to(DEV)
+        ck = torch.full((C, H, D, D), float("nan"), device=DEV)
+        res = kda.kda_prefill(q[None].to(DEV), k[None].to(DEV), v[None].to(DEV), raw_g[None].to(DEV),
+                              raw_b[None].to(DEV), A_log.to(DEV), dt_bias.to(DEV), pool,
+                              torch.tensor(_cu(lens)).to(DEV), ssm_state_indices=idx.to(DEV), state_checkpoints=ck,
+                              checkpoint_cu_starts=ccs.to(DEV), checkpoint_every_n_tokens=every, meta=meta)
+        torch.cuda.synchronize()
+        qn, kn, vf, gl, bt = _oracle_gated(oracle, q, k, v, raw_g, raw_b, A_log, dt_bias)
+        ro, rf, rows, _ = oracle.checkpoints_every_n(qn, kn, vf, gl, bt, _cu(lens), every,
+                                                     initial_state=f32(pool0)[idx.numpy()], normalize_qk=False,
+                                                     precision=64)
+        _check_out(res[0][0], ro, f"split random {i}", _cu(lens))
+        fin = f32(pool)
+        for n in range(N):
+            assert rel_frob(fin[int(idx[n])], rf[n]) <= STATE_TOL, f"case {i} seq {n}: final state"
+        got = f32(ck)
+        for r in range(C):
+            assert rel_frob(got[r], rows[r]) <= STATE_TOL, f"case {i} checkpoint row {r}"
+
+
 ONE_CHUNK_LENS = [1024, 200, 130, 64]  # at H = 4 the plan cuts the first three into one-chunk pieces
 
 
