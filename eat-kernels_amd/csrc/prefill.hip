@@ -848,12 +848,13 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
 #pragma unroll
                 for (int I = 0; I < 4; ++I) {
                     const float xI = sF[(F_X + I) * 128 + c];
+                    const f32x4 b4 = *reinterpret_cast<const f32x4*>(&sBeta[16 * I + 4 * g]);  // beta of the 4 rows
                     f32x4 aw, au;
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
                         const int rw = 16 * I + 4 * g + e;
-                        aw[e] = sBeta[rw] * sKA[rw * RS32 + swz(c)] * xI;
-                        au[e] = sBeta[rw] * bf2f(sV[rw * RS16 + c]);  // beta v straight from the raw v row
+                        aw[e] = b4[e] * sKA[rw * RS32 + swz(c)] * xI;
+                        au[e] = b4[e] * bf2f(sV[rw * RS16 + c]);  // beta v straight from the raw v row
                     }
 #pragma unroll
                     for (int J = 0; J < I; ++J) {
