@@ -136,6 +136,17 @@ __device__ __forceinline__ float sigmoid_rcp(float x) { return __builtin_amdgcn_
 // MFMAs flush subnormal operands; at -11 the factors reach 2^-127).  The state change this makes is below e^{-9} =
 // 1.2e-4 of the affected channel's value (a decay of e^{-9} instead of a smaller one).  NaN passes through unchanged.
 __device__ __forceinline__ float clamp_decay(float g) { return g < KDA355_MIN_LOG_DECAY ? KDA355_MIN_LOG_DECAY : g; }
+// the same limit for a log-decay already in log2 units
+constexpr float LOG2E = 1.4426950408889634f;
+__device__ __forceinline__ float clamp_decay2(float g) {
+    constexpr float lim = KDA355_MIN_LOG_DECAY * LOG2E;
+    return g < lim ? lim : g;
+}
+// Gate-in-kernel constant of a head: An = -e^{A_log} log2(e), so that e^{-e^{A_log} (x + dt_bias)} =
+// 2^{An x + An dt_bias} is one FMA (An dt_bias per channel sits in LDS) and one v_exp_f32
+__device__ __forceinline__ float gate_an(float alog) { return -__expf(alog) * LOG2E; }
+// a float read through the scalar (constant address space) cache
+typedef const __attribute__((address_space(4))) float cfloat_t;
 
 // Workgroup barrier for LDS traffic only.  __syncthreads() also fences global memory (s_waitcnt vmcnt(0)), which
 // would wait for the next chunk's prefetched loads and for the output stores at every phase boundary; the waves of
@@ -392,7 +403,6 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
             it.row = *reinterpret_cast<cint_t*>(reinterpret_cast<uintptr_t>(p.state_idx + it.n));
             it.hword = *reinterpret_cast<cword_t*>(reinterpret_cast<uintptr_t>(p.has_init + it.n) & ~(uintptr_t)3);
         }
-        typedef const __attribute__((address_space(4))) float cfloat_t;
         it.alog = RG ? *reinterpret_cast<cfloat_t*>(reinterpret_cast<uintptr_t>(p.A_log + it.h)) : 0.f;
         return it;
     };
@@ -448,10 +458,10 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
 
     const int ck_mode = (p.flags & KDA355_PF_CK_EVERY) ? 2 : ((p.flags & KDA355_PF_CK_SINGLE) ? 1 : 0);
     // gate-in-kernel constants for this thread's 16 channels
-    float Aexp = 0.f;
+    float An = 0.f;
     if (RG) {
-        Aexp = __expf(cur.alog);
-        if (tid < D) sDT[tid] = dtb;
+        An = gate_an(cur.alog);
+        if (tid < D) sDT[tid] = An * dtb;
     }
     // A_qk blocks (0,1) and (2,3) are read by the walk and never written by the Gram phase
     for (int e = tid; e < 2 * 16 * 16; e += PF_THREADS) {
@@ -479,7 +489,9 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
             nx_nch = e2[C_NCH];
             nx_t = e2[C_TSTART];
             nx_len = e2[C_LEN];
-            if (RG) dtb_next = p.dt_bias[nx_h * D + (threadIdx.x & (D - 1))];
+            if (RG)  // An dt_bias of the next item's head (its sDT contents)
+                dtb_next = gate_an(*reinterpret_cast<cfloat_t*>(reinterpret_cast<uintptr_t>(p.A_log + nx_h))) *
+                           p.dt_bias[nx_h * D + (threadIdx.x & (D - 1))];
         }
         f32x4 Pm[8];  // fix: the transition, P[k][k'] at (k = 16dt + 4g + e, k' = 16w + m); starts as the identity
         if (fix) {
@@ -523,18 +535,20 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
                 float rg[16];
                 const u32x4 gg[2] = {nx.g[0], nx.g[1]};
                 unpack16(gg, rg);
-                // every row is computed and rows >= L are zeroed after (their raw gate reads as 0): a computation under
-                // the row mask would branch per value and wait for every outstanding LDS read
+                // g log2(e) = lb log2(e) sigmoid(e^{A_log} (x + dt_bias)), the sigmoid as 1 / (1 + 2^{An x + An dt})
+                // (one FMA, v_exp_f32, one add, v_rcp_f32), already in the log2 units of the cumsum.  Every row is
+                // computed; rows >= L get a zero multiplier (their raw gate reads as 0, so the sigmoid is finite): a
+                // computation under the row mask would branch per value and wait for every outstanding LDS read.
+                const float lbm = (r < L) ? p.lb * LOG2E : 0.f;
 #pragma unroll
                 for (int q4 = 0; q4 < 4; ++q4) {
-                    const f32x4 dt4 = *reinterpret_cast<const f32x4*>(&sDT[16 * cb + 4 * q4]);
+                    const f32x4 adt4 = *reinterpret_cast<const f32x4*>(&sDT[16 * cb + 4 * q4]);  // An dt_bias
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const float x = clamp_decay(p.lb * sigmoid_rcp(Aexp * (rg[4 * q4 + e] + dt4[e])));
-                        gv[4 * q4 + e] = (r < L) ? x : 0.f;
-                    }
+                    for (int e = 0; e < 4; ++e)
+                        gv[4 * q4 + e] = clamp_decay2(
+                            lbm * __builtin_amdgcn_rcpf(1.0f + exp2_(fmaf(An, rg[4 * q4 + e], adt4[e]))));
                 }
-            } else {
+            } else {  // natural-log units here; the cumsum scales them by log2(e) as it adds
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -542,19 +556,23 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
             }
             const float bx = RB ? sigmoid_rcp(bf2f(nx.beta)) : __uint_as_float(nx.beta);
             const float bt = (r >= L) ? 0.f : bx;
-#pragma unroll
-            for (int c = 0; c < 16; ++c) gv[c] *= 1.4426950408889634f;  // log2(e): the cumsum runs in log2 units
             float rq = 1.f, rk = 1.f;
             if (NORM) {  // F.normalize(x, eps=1e-6) = x / max(|x|, 1e-6)  (kda/mi350x/reference.py:59-60)
-                float qf[16], kf[16];
-                {
-                    const u32x4 a[2] = {nx.q[0], nx.q[1]}, b[2] = {nx.k[0], nx.k[1]};
-                    unpack16(a, qf);
-                    unpack16(b, kf);
-                }
+                // sums of squares straight from the packed bf16 pairs (v_dot2c_f32_bf16: the products are exact in
+                // fp32), so this phase unpacks no q / k value
                 float sq = 0.f, sk = 0.f;
 #pragma unroll
-                for (int c = 0; c < 16; ++c) { sq += qf[c] * qf[c]; sk += kf[c] * kf[c]; }
+                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        // element copies first: a bit cast of the vector element itself loses its index in this
+                        // compiler (every j read element 0)
+                        const uint32_t wq = nx.q[i][j], wk = nx.k[i][j];
+                        const bf16x2_t qp = __builtin_bit_cast(bf16x2_t, wq);
+                        const bf16x2_t kp = __builtin_bit_cast(bf16x2_t, wk);
+                        sq = __builtin_amdgcn_fdot2_f32_bf16(qp, qp, sq, false);
+                        sk = __builtin_amdgcn_fdot2_f32_bf16(kp, kp, sk, false);
+                    }
                 sq = sum8(sq);
                 sk = sum8(sk);
                 // 1 / max(|x|, 1e-6) = rsqrt(max(|x|^2, 1e-12)) through v_rsq_f32 (the IEEE sqrt is a sequence)
@@ -573,8 +591,14 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
                 float x[16];
 #pragma unroll
                 for (int i = 0; i < 16; ++i) x[i] = sG[(16 * s + i) * RS32 + swz(c)];
+                if (RG) {  // already in log2 units
 #pragma unroll
-                for (int i = 1; i < 16; ++i) x[i] += x[i - 1];
+                    for (int i = 1; i < 16; ++i) x[i] += x[i - 1];
+                } else {  // natural log: the log2(e) scale goes into the adds
+                    x[0] *= LOG2E;
+#pragma unroll
+                    for (int i = 1; i < 16; ++i) x[i] = fmaf(x[i], LOG2E, x[i - 1]);
+                }
 #pragma unroll
                 for (int i = 0; i < 16; ++i) sG[(16 * s + i) * RS32 + swz(c)] = x[i];
                 sWt[s * 128 + c] = x[15];
@@ -1099,7 +1123,7 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
             lds_barrier();
         }
         load_start_state(state_source(cur));
-        if (RG) Aexp = __expf(cur.alog);
+        if (RG) An = gate_an(cur.alog);
     }  // the workgroup's items
 }
 
