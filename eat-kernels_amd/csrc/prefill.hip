@@ -938,19 +938,21 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
                         PB[s][e] = (half_t)Pm[2 * s][e];
                         PB[s][4 + e] = (half_t)Pm[2 * s + 1][e];
                     }
-                f32x4 Vp[4], Wp[4];
+                f32x4 Vp[4], Wp[4];  // W S and W P, K step outermost (eight independent MFMA chains per step)
 #pragma unroll
-                for (int it = 0; it < 4; ++it) {
-                    f32x4 acc = {0.f, 0.f, 0.f, 0.f}, acp = acc;
+                for (int it = 0; it < 4; ++it) { Vp[it] = f32x4{0.f, 0.f, 0.f, 0.f}; Wp[it] = Vp[it]; }
 #pragma unroll
-                    for (int s = 0; s < 4; ++s) {
+                for (int s = 0; s < 4; ++s)
+#pragma unroll
+                    for (int it = 0; it < 4; ++it) {
                         const f16x8 A = *reinterpret_cast<const f16x8*>(&sW[(16 * it + m) * RS16 + 32 * s + 8 * g]);
-                        acc = mfma32(A, SB[s], acc);
-                        acp = mfma32(A, PB[s], acp);
+                        Vp[it] = mfma32(A, SB[s], Vp[it]);
+                        Wp[it] = mfma32(A, PB[s], Wp[it]);
                     }
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) { Vp[it][e] = Ur[it][e] - acc[e]; Wp[it][e] = -acp[e]; }
-                }
+                for (int it = 0; it < 4; ++it)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) { Vp[it][e] = Ur[it][e] - Vp[it][e]; Wp[it][e] = -Wp[it][e]; }
                 f16x8 VB[2], WB[2], VL[2], WL[2];  // V' and -W P; PREC: also their low parts (fp16 pairs)
 #pragma unroll
                 for (int s = 0; s < 2; ++s)
@@ -1019,15 +1021,20 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
                         SB[s][4 + e] = (half_t)S[2 * s + 1][e];
                     }
                 f32x4 Vp[4];
+                // W S with the K step outermost: the four token tiles' MFMAs of one step are independent, so none
+                // waits for the previous one's accumulator
 #pragma unroll
-                for (int it = 0; it < 4; ++it) {
-                    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+                for (int it = 0; it < 4; ++it) Vp[it] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                    for (int s = 0; s < 4; ++s)
-                        acc = mfma32(*reinterpret_cast<const f16x8*>(&sW[(16 * it + m) * RS16 + 32 * s + 8 * g]), SB[s], acc);
+                for (int s = 0; s < 4; ++s)
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) Vp[it][e] = Ur[it][e] - acc[e];
-                }
+                    for (int it = 0; it < 4; ++it)
+                        Vp[it] = mfma32(*reinterpret_cast<const f16x8*>(&sW[(16 * it + m) * RS16 + 32 * s + 8 * g]), SB[s],
+                                        Vp[it]);
+#pragma unroll
+                for (int it = 0; it < 4; ++it)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) Vp[it][e] = Ur[it][e] - Vp[it][e];
                 f16x8 VB[2], VL[2];  // V'; PREC: also its low part (an fp16 pair)
 #pragma unroll
                 for (int s = 0; s < 2; ++s)
@@ -1041,21 +1048,30 @@ __global__ void __launch_bounds__(PF_THREADS, 1)
                 // O^T = S^T Q~^T + V'^T A_qk^T: the same fragments with the MFMA operands swapped give the transposed
                 // tile, so lane (g, m) holds token 16 it + m, values 16 w + 4 g .. + 3 and stores them to `out` with
                 // one 8-byte store (the 8 waves' 32-byte pieces of a token row meet in the L2)
+                {
+                    f32x4 ao[4];  // K step outermost here too
 #pragma unroll
-                for (int it = 0; it < 4; ++it) {
-                    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+                    for (int it = 0; it < 4; ++it) ao[it] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                     for (int s = 0; s < 4; ++s)
-                        acc = mfma32(SB[s], *reinterpret_cast<const f16x8*>(&sQt[(16 * it + m) * RS16 + 32 * s + 8 * g]), acc);
+#pragma unroll
+                        for (int it = 0; it < 4; ++it)
+                            ao[it] = mfma32(SB[s], *reinterpret_cast<const f16x8*>(&sQt[(16 * it + m) * RS16 + 32 * s + 8 * g]),
+                                            ao[it]);
 #pragma unroll
                     for (int s = 0; s < 2; ++s)
-                        if (s <= (it >> 1))
-                            acc = mfma32(VB[s], *reinterpret_cast<const f16x8*>(&sAq[(16 * it + m) * RS16S + 32 * s + 8 * g]),
-                                         acc);
-                    const u32x2 o = {f2bf2(p.scale * acc[0], p.scale * acc[1]), f2bf2(p.scale * acc[2], p.scale * acc[3])};
-                    if (16 * it + m < L)
-                        *reinterpret_cast<u32x2*>(p.out + ((int64_t)t0 + 16 * it + m) * p.out_rs + (int64_t)h * D + 16 * w +
-                                                  4 * g) = o;
+#pragma unroll
+                        for (int it = 2 * s; it < 4; ++it)
+                            ao[it] = mfma32(VB[s], *reinterpret_cast<const f16x8*>(&sAq[(16 * it + m) * RS16S + 32 * s + 8 * g]),
+                                            ao[it]);
+#pragma unroll
+                    for (int it = 0; it < 4; ++it) {
+                        const u32x2 o = {f2bf2(p.scale * ao[it][0], p.scale * ao[it][1]),
+                                         f2bf2(p.scale * ao[it][2], p.scale * ao[it][3])};
+                        if (16 * it + m < L)
+                            *reinterpret_cast<u32x2*>(p.out + ((int64_t)t0 + 16 * it + m) * p.out_rs + (int64_t)h * D +
+                                                      16 * w + 4 * g) = o;
+                    }
                 }
 #pragma unroll
                 for (int dt = 0; dt < 8; ++dt) {
