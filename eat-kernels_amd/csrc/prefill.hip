@@ -1564,6 +1564,8 @@ hipError_t launch_chunk_any(const PfParams& p, bool rg, bool prec, int list_off,
     return rg ? (prec ? launch_chunk<true, P1, true>(p, list_off, wgs, s) : launch_chunk<true, P1, false>(p, list_off, wgs, s))
               : (prec ? launch_chunk<false, P1, true>(p, list_off, wgs, s) : launch_chunk<false, P1, false>(p, list_off, wgs, s));
 }
+#include "chunk32.h"
+
 template <typename K>
 hipError_t launch_composer(K kernel, const PfParams& p, int entries, int threads, int smem, hipStream_t s,
                            bool& attr_set) {
@@ -1797,7 +1799,7 @@ extern "C" int kda355_prefill_plan(const KdaPrefillPlanIn* in, KdaPrefillPlan* p
     // when their schedule beats one workgroup per item dealt out by the hardware.
     constexpr int64_t PASS_QUARTERS = 1;
     const int64_t items = (int64_t)nfinal * in->H;
-    int grid = 0;
+    int grid = 0, chunk32 = 0;
     std::vector<std::vector<int32_t>> lists;
     if (nsplit == 0 && items > num_cus && items < (1 << 30)) {
         std::vector<int64_t> ld(num_cus, 0);
@@ -1825,6 +1827,45 @@ extern "C" int kda355_prefill_plan(const KdaPrefillPlanIn* in, KdaPrefillPlan* p
                 q.push(top);
             }
         if (span_lst < span_dyn) grid = num_cus;
+        // The 32-token kernel's schedule (chunk32.h): one workgroup per item, two per CU, items in launch order, the
+        // first 2 x num_cus dealt two to a CU and every later one to the CU that frees a slot first.  A workgroup
+        // advances C32_PAIRED chunk times per 64 tokens while it shares its CU and C32_ALONE when alone, plus
+        // C32_START of start-up (measured on MI355X against the 64-token kernel's chunk: 512 items of 8-32 chunks run
+        // 7-11 % faster paired; a 47-chunk chain mostly alone runs 30 % slower).  It is used when this simulated span
+        // beats the 64-token kernel's best (lists or one workgroup per item) by 3 %.
+        constexpr double C32_ALONE = 1.3, C32_PAIRED = 1.85, C32_START = 0.5;
+        struct Cu { double t = 0, w[2] = {0, 0}; int n = 0, ver = 0; };
+        std::vector<Cu> cu(num_cus);
+        typedef std::pair<double, std::pair<int, int>> Ev;  // (finish time, (CU, version))
+        std::priority_queue<Ev, std::vector<Ev>, std::greater<Ev>> ev;
+        int64_t next = 0;
+        auto item_work = [&](int64_t it) { return (double)pieces[order[it / in->H]].count + C32_START; };
+        auto schedule = [&](int c) {  // the CU's next completion
+            Cu& u = cu[c];
+            if (u.n == 0) return;
+            const double r = u.n == 2 ? C32_PAIRED : C32_ALONE;
+            ev.push({u.t + std::min(u.w[0], u.n == 2 ? u.w[1] : u.w[0]) * r, {c, ++u.ver}});
+        };
+        for (int rnd = 0; rnd < 2; ++rnd)
+            for (int c = 0; c < num_cus && next < items; ++c) cu[c].w[cu[c].n++] = item_work(next++);
+        for (int c = 0; c < num_cus; ++c) schedule(c);
+        double span32 = 0;
+        while (!ev.empty()) {
+            const Ev e = ev.top();
+            ev.pop();
+            Cu& u = cu[e.second.first];
+            if (e.second.second != u.ver) continue;  // superseded by a later change of this CU
+            const double r = u.n == 2 ? C32_PAIRED : C32_ALONE, dt = e.first - u.t;
+            for (int j = 0; j < u.n; ++j) u.w[j] -= dt / r;
+            u.t = e.first;
+            span32 = std::max(span32, e.first);
+            const int done = (u.n == 2 && u.w[1] < u.w[0]) ? 1 : 0;  // the workgroup that finished
+            u.w[done] = u.w[u.n - 1];
+            --u.n;
+            if (next < items) u.w[u.n++] = item_work(next++);
+            schedule(e.second.first);
+        }
+        if (span32 < 0.97 * 0.25 * (double)std::min(span_lst, span_dyn)) chunk32 = 1;
     }
     const int64_t off_final = H_WORDS, off_fix = off_final + (int64_t)C_WORDS * nfinal;
     const int64_t off_scan = off_fix + (int64_t)X_WORDS * nfix;
@@ -1856,6 +1897,7 @@ extern "C" int kda355_prefill_plan(const KdaPrefillPlanIn* in, KdaPrefillPlan* p
     plan->num_fix_tasks = nfix;
     plan->num_ck_tasks = nck;
     plan->chunk_grid = grid;
+    plan->chunk32 = chunk32;
     if (!tables) return 0;
     KDA_CHECK_ARG(capacity >= words, "prefill_plan: table capacity %lld < %lld words", (long long)capacity, (long long)words);
     int32_t* t = tables;
@@ -1946,6 +1988,8 @@ extern "C" int kda355_prefill_launch(const KdaPrefillArgs* a, kda355_stream_t st
     KDA_CHECK_ARG(pl->chunk_grid >= 0 && (int64_t)pl->chunk_grid <= (int64_t)pl->num_chains * pl->H &&
                       (pl->chunk_grid == 0 || pl->num_split == 0),
                   "prefill: plan has an invalid chunk_grid %d", pl->chunk_grid);
+    KDA_CHECK_ARG((pl->chunk32 == 0 || pl->chunk32 == 1) && (pl->chunk32 == 0 || pl->num_split == 0),
+                  "prefill: plan has an invalid chunk32 %d", pl->chunk32);
     KDA_CHECK_ARG(pl->N == a->N && pl->T == a->T && pl->H == a->H,
                   "prefill: plan was made for another layout (N/T/H %d/%lld/%d vs %d/%lld/%d)", pl->N, (long long)pl->T,
                   pl->H, a->N, (long long)a->T, a->H);
@@ -2030,9 +2074,14 @@ extern "C" int kda355_prefill_launch(const KdaPrefillArgs* a, kda355_stream_t st
             if (e == hipSuccess) e = launch_tail(p, 0, pl->num_fix_tasks, pl->num_ck_tasks, s);
         }
     } else {
-        // one workgroup per (chain, head), or the plan's workgroup lists
-        const int wgs = pl->chunk_grid > 0 ? pl->chunk_grid : pl->num_chains * a->H;
-        e = launch_chunk_any<false>(p, rg, prec, off_final, wgs, s);
+        // one workgroup per (chain, head), or the plan's workgroup lists; or, when the plan chose it, the 32-token
+        // kernel (one workgroup per item, two per CU), outside the precise mode and unless the caller keeps the
+        // 64-token kernel (KDA355_PF_CHUNK64)
+        const int items = pl->num_chains * a->H;
+        if (pl->chunk32 && !prec && !(f & KDA355_PF_CHUNK64))
+            e = rg ? launch_chunk32<true>(p, off_final, items, s) : launch_chunk32<false>(p, off_final, items, s);
+        else
+            e = launch_chunk_any<false>(p, rg, prec, off_final, pl->chunk_grid > 0 ? pl->chunk_grid : items, s);
     }
     if (e != hipSuccess) {
         set_error("prefill: launch failed: %s", hipGetErrorString(e));

@@ -73,7 +73,7 @@ class KdaPrefillPlan(ctypes.Structure):
         ("T", I64), ("N", I32), ("H", I32), ("num_chunks", I32), ("num_chains", I32), ("max_chain_chunks", I32),
         ("ck_every", I32), ("table_words", I64), ("workspace_bytes", I64), ("ck_rows", I64), ("magic", U32),
         ("flags", U32), ("num_pieces", I32), ("num_split", I32), ("num_fix_tasks", I32), ("num_ck_tasks", I32),
-        ("chunk_grid", I32),
+        ("chunk_grid", I32), ("chunk32", I32),
     ]
 
 

@@ -39,6 +39,7 @@ PF_POOL = 8
 PF_CK_SINGLE = 16
 PF_CK_EVERY = 32
 PF_PRECISE = 64  # KDA355_PF_PRECISE: the solve's and state update's fp16 operands as fp16 pairs (precise=True)
+PF_CHUNK64 = 128  # KDA355_PF_CHUNK64: keep the 64-token kernel (and its workgroup lists) on layouts with more items than CUs
 
 
 def _ptr(t):
@@ -48,7 +49,7 @@ def _ptr(t):
 class PrefillMeta:
     """Schedule of one batch layout: the host plan, its device table and the layout it was made for."""
 
-    def __init__(self, plan, tables, num_heads, ck_every, any_ck, lens):
+    def __init__(self, plan, tables, num_heads, ck_every, any_ck, lens, chunk64=False):
         self.plan = plan
         self.lens = lens            # host int64 [N] sequence lengths
         self.tables = tables
@@ -57,6 +58,7 @@ class PrefillMeta:
         self.T = plan.T
         self.ck_every = ck_every
         self.any_ck = any_ck
+        self.chunk64 = bool(chunk64)  # launches keep the 64-token kernel (KDA355_PF_CHUNK64)
 
     @property
     def workspace_bytes(self):
@@ -75,7 +77,7 @@ class PrefillMeta:
         """(plan, plan_table): the host plan as a CPU uint8 tensor (the KdaPrefillPlan bytes, then an int32 flag for
         planned checkpoints and the sequence lengths as int64) and its device table -- the metadata tensors that the
         torch.ops entry points take where vLLM's chunk op takes chunk_indices / chunk_offsets."""
-        head = bytes(self.plan) + np.array([int(self.any_ck), 0], np.int32).tobytes()
+        head = bytes(self.plan) + np.array([int(self.any_ck), int(self.chunk64)], np.int32).tobytes()
         raw = head + np.ascontiguousarray(self.lens, np.int64).tobytes()
         return torch.frombuffer(bytearray(raw), dtype=torch.uint8), self.tables
 
@@ -92,17 +94,22 @@ class PrefillMeta:
             raise ValueError("kda355: plan is too short to hold a prefill plan")
         pl = _lib.KdaPrefillPlan.from_buffer_copy(raw[:n])
         any_ck = int(np.frombuffer(raw[n:n + 4], np.int32)[0]) != 0
+        chunk64 = int(np.frombuffer(raw[n + 4:n + 8], np.int32)[0]) != 0
         lens = np.frombuffer(raw[n + 8:], np.int64).copy()
         if lens.size != pl.N or int(lens.sum()) != pl.T or plan_table.numel() != pl.table_words:
             raise ValueError("kda355: plan and plan_table do not come from one PrefillMeta.as_tensors() call")
-        return cls(pl, plan_table, int(pl.H), int(pl.ck_every), any_ck, lens)
+        return cls(pl, plan_table, int(pl.H), int(pl.ck_every), any_ck, lens, chunk64)
 
 
-def plan(cu_seqlens, num_heads, checkpoint_offsets=None, ck_every=0, device=None, num_cus=None):
+def plan(cu_seqlens, num_heads, checkpoint_offsets=None, ck_every=0, device=None, num_cus=None, chunk64=None):
     """Host-only schedule from the layout (never the data); one H2D copy of the table when device is a GPU.
     num_cus: CUs to fill (default: the device's); when the (sequence, head) chains alone leave CUs idle or the longest
     chains would finish well after the rest, long sequences are split into pieces of >= 2 chunks (later pieces run
-    from a zero state carrying their transition; a scan and an output fixup complete them, with a workspace)."""
+    from a zero state carrying their transition; a scan and an output fixup complete them, with a workspace).  An
+    unsplit layout with more (sequence, head) items than CUs runs the 32-token kernel (two workgroups per CU) when the
+    plan's schedule model says it finishes first.  chunk64: None leaves that choice to the plan; True keeps the
+    64-token kernel (and its workgroup lists); False takes the 32-token kernel for any unsplit layout (a comparison and
+    test switch)."""
     cu = np.ascontiguousarray(torch.as_tensor(cu_seqlens).detach().cpu().numpy(), dtype=np.int64)
     N = cu.size - 1
     if N < 1:
@@ -134,7 +141,9 @@ def plan(cu_seqlens, num_heads, checkpoint_offsets=None, ck_every=0, device=None
     if device is not None and torch.device(device).type == "cuda":
         t = t.to(device)
     any_ck = ck is not None and bool(np.any(ck > 0))
-    return PrefillMeta(pl, t, int(num_heads), int(ck_every), any_ck, np.diff(cu))
+    if chunk64 is False and int(pl.num_split) == 0:
+        pl.chunk32 = 1
+    return PrefillMeta(pl, t, int(num_heads), int(ck_every), any_ck, np.diff(cu), chunk64 is True)
 
 
 def _need(name, t, dtype, device):
@@ -207,7 +216,7 @@ def _launch(meta, q, k, v, gt, bt, out, flags, scale, lower_bound, A_log=None, d
     a.workspace = _ptr(workspace)
     a.T, a.N, a.H = T, meta.N, H
     a.scale, a.lower_bound = float(scale), float(lower_bound)
-    a.flags = flags
+    a.flags = flags | (PF_CHUNK64 if getattr(meta, "chunk64", False) else 0)
     a.plan = ctypes.pointer(meta.plan)
     stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
     if static:

@@ -186,6 +186,9 @@ int kda355_decode_launch(const KdaDecodeArgs* args, kda355_stream_t stream);
 #define KDA355_PF_PRECISE 64u      /* the solve's and the state update's fp16 operands as fp16 pairs (22 bits): about half
                                       the state error on chunks of nearly parallel keys with beta ~ 1, ~11 % more time.
                                       No counterpart in the reference (its prefill precision is fixed). */
+#define KDA355_PF_CHUNK64 128u     /* keep the 64-token kernel (and the plan's workgroup lists) where the plan chose the
+                                      32-token kernel (KdaPrefillPlan.chunk32); a comparison and test switch.  No
+                                      counterpart in the reference. */
 
 /* Host-side plan input: the layout only (never the data). */
 typedef struct KdaPrefillPlanIn {
@@ -216,6 +219,11 @@ typedef struct KdaPrefillPlan {
     int32_t chunk_grid;         /* workgroups of the chunk launch: 0 = one per (chain, head); > 0 (layouts without
                                    split sequences whose (chain, head) pairs outnumber the CUs) = that many
                                    workgroups, each walking a list of (chain, head) pairs in turn */
+    int32_t chunk32;            /* 1: the launch runs the 32-token chunk kernel, one workgroup per (chain, head) and two
+                                   per CU (layouts without split sequences whose items outnumber the CUs, when its
+                                   simulated schedule beats chunk_grid's); launches with KDA355_PF_PRECISE or
+                                   KDA355_PF_CHUNK64 keep the 64-token kernel.  May be set to 1 by the caller for any
+                                   plan without split sequences. */
 } KdaPrefillPlan;
 
 /*

@@ -224,6 +224,25 @@ def test_prefill_plan_workgroup_lists():
         assert pl.chunk_grid == 0 and tab[17] == 0
 
 
+def test_prefill_plan_chunk32_choice():
+    """The 32-token kernel (two workgroups per CU) is chosen for unsplit layouts with more items than CUs when the
+    plan's schedule model has it finish first: items of similar length that keep both workgroups of a CU busy; not
+    when a few long chains would run alone on their CUs (p96_loaded8k_1), not for short items (p_64x128, where the
+    lists win), nor for split layouts or layouts that fit the CUs."""
+    for lens, H in (([512] * 32, 12), ([512] * 32, 16), ([1024] * 32, 16), ([256] * 64, 16), ([2048] * 16, 32)):
+        pl, _ = _plan(lens, H, 256)
+        assert pl.num_split == 0 and pl.chunk32 == 1, (lens[:2], H)
+    for lens, H in (([384, 1344, 3008, 2176, 320, 832], 96), ([128] * 64, 12), ([131072], 32), ([8192] * 8, 32),
+                    ([100] * 10, 4)):
+        pl, _ = _plan(lens, H, 256)
+        assert pl.chunk32 == 0, (lens[:2], H)
+    rng = np.random.default_rng(9)
+    for _ in range(40):
+        N, H, cus = int(rng.integers(1, 40)), int(rng.integers(1, 9)), int(rng.choice([2, 3, 8, 32, 256]))
+        pl, _ = _plan([int(x) for x in rng.integers(0, 1500, size=N)], H, cus)
+        assert pl.chunk32 in (0, 1) and (pl.chunk32 == 0 or (pl.num_split == 0 and pl.num_chains * H > cus))
+
+
 def test_prefill_plan_workgroup_lists_random_layouts():
     """Planner invariants over seeded random layouts and CU counts: a plan with workgroup lists splits nothing, has
     more items than lists, and its lists partition the items, each longest first; a plan without lists has no list

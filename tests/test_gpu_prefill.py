@@ -34,17 +34,20 @@ def _check_out(got, ref, what, cu=None):
     return check_out(got, ref, what, cu)
 
 
-def _list_meta(kda, lens, H, cus, **kw):
-    """A plan for `cus` CUs that uses workgroup lists (one workgroup per CU walking several (sequence, head) items)."""
-    meta = kda.plan(torch.tensor(_cu(lens)), H, device=DEV, num_cus=cus, **kw)
+def _list_meta(kda, lens, H, cus, chunk64=True, **kw):
+    """A plan for `cus` CUs with more (sequence, head) items than CUs: chunk64 = True runs the 64-token kernel on its
+    workgroup lists (one workgroup per CU walking several items), False the 32-token kernel (one workgroup per item, two
+    per CU)."""
+    meta = kda.plan(torch.tensor(_cu(lens)), H, device=DEV, num_cus=cus, chunk64=chunk64, **kw)
     assert meta.split == (0, 0) and int(meta.plan.chunk_grid) == cus, (meta.split, int(meta.plan.chunk_grid))
     return meta
 
 
-def _plain_case(oracle, H, lens, seed, init=True, gscale=1.0, heads_checked=None, gmod=None, precise=False, cus=None):
+def _plain_case(oracle, H, lens, seed, init=True, gscale=1.0, heads_checked=None, gmod=None, precise=False, cus=None,
+                chunk64=True):
     kda = _kda()
     _say(f"plain H={H} lens={lens[:10]} init={init} seed={seed}" + (" precise" if precise else "") +
-         (f" lists on {cus} CUs" if cus else ""))
+         (f" {'lists' if chunk64 else '32-token kernel'} on {cus} CUs" if cus else ""))
     g = gen(seed)
     T = int(sum(lens))
     q, k, v, gg, beta = config_inputs(T, H, g)
@@ -54,7 +57,7 @@ def _plain_case(oracle, H, lens, seed, init=True, gscale=1.0, heads_checked=None
     N = len(lens)
     h0 = torch.randn(N, H, D, D, generator=g) * 0.02 if init else None
     cu = torch.tensor(_cu(lens), dtype=torch.int32)
-    meta = _list_meta(kda, lens, H, cus) if cus else None
+    meta = _list_meta(kda, lens, H, cus, chunk64) if cus else None
     o, fin = kda.chunk_kda(q[None].to(DEV), k[None].to(DEV), v[None].to(DEV), gg[None].to(DEV), beta[None].to(DEV),
                            initial_state=h0.to(DEV) if init else None, output_final_state=True, cu_seqlens=cu.to(DEV),
                            precise=precise, meta=meta)
@@ -89,28 +92,66 @@ def test_ragged_tiny_and_empty(oracle):
     _plain_case(oracle, 3, [1, 17, 33, 0, 1, 63, 65, 128, 2], 2)
 
 
-def test_workgroup_lists_plain(oracle):
-    """Workgroup lists: unsplit layouts with more (sequence, head) items than workgroups, each workgroup walking its
-    list in turn (the next item's rows prefetched in the last chunk of the one before, its start state loaded after
-    that one's final state is stored).  Planned for 4 and 3 CUs: lists of 10-27 items mixing empty, one-token, ragged
-    and multi-chunk sequences, with and without initial states, and at the bench's p_64x128 shape on the device's CUs
-    (three two-chunk items per list)."""
-    _plain_case(oracle, 3, [1, 17, 33, 0, 1, 63, 65, 128, 2, 0, 300, 64, 200], 90, cus=4)
-    _plain_case(oracle, 5, [130, 0, 777, 64, 1, 250, 64], 91, init=False, cus=3)
+@pytest.mark.parametrize("chunk64", [True, False], ids=["lists", "chunk32"])
+def test_workgroup_lists_plain(oracle, chunk64):
+    """Unsplit layouts with more (sequence, head) items than CUs.  lists: the 64-token kernel's workgroup lists, each
+    workgroup walking its list in turn (the next item's rows prefetched in the last chunk of the one before, its start
+    state loaded after that one's final state is stored).  chunk32: the 32-token kernel, one workgroup per item.
+    Planned for 4 and 3 CUs: 10-27 items per CU mixing empty, one-token, ragged and multi-chunk sequences, with and
+    without initial states, and at the bench's p_64x128 shape on the device's CUs (three two-chunk items per CU)."""
+    _plain_case(oracle, 3, [1, 17, 33, 0, 1, 63, 65, 128, 2, 0, 300, 64, 200], 90, cus=4, chunk64=chunk64)
+    _plain_case(oracle, 5, [130, 0, 777, 64, 1, 250, 64], 91, init=False, cus=3, chunk64=chunk64)
     cus = torch.cuda.get_device_properties(DEV).multi_processor_count
-    _plain_case(oracle, 12, [128] * 64, 92, heads_checked=[0, 5, 11], cus=cus)
+    _plain_case(oracle, 12, [128] * 64, 92, heads_checked=[0, 5, 11], cus=cus, chunk64=chunk64)
 
 
-def test_workgroup_lists_random_layouts(oracle):
-    """Workgroup lists on seeded random layouts (empty, one-token and up to 12-chunk sequences; 2 to 7 CUs, so lists of
-    many items of mixed lengths), with and without initial states, given gates; against the oracle."""
+@pytest.mark.parametrize("chunk64", [True, False], ids=["lists", "chunk32"])
+def test_workgroup_lists_random_layouts(oracle, chunk64):
+    """Seeded random layouts with more items than CUs (empty, one-token and up to 12-chunk sequences; 2 to 7 CUs, so
+    many items of mixed lengths per CU), with and without initial states, given gates; the 64-token kernel's workgroup
+    lists and the 32-token kernel, against the oracle."""
     rng = np.random.default_rng(11)
     for i in range(3):
         N, H, cus = int(rng.integers(6, 16)), int(rng.integers(2, 6)), int(rng.integers(2, 8))
         lens = [int(x) for x in rng.integers(0, 768, size=N)]
         lens[int(rng.integers(0, N))] = 0
         lens[int(rng.integers(0, N))] = 1
-        _plain_case(oracle, H, lens, 95 + i, init=bool(i % 2 == 0), cus=cus)
+        _plain_case(oracle, H, lens, 95 + i, init=bool(i % 2 == 0), cus=cus, chunk64=chunk64)
+
+
+def test_chunk32_device_scale(oracle):
+    """The 32-token kernel as the launch picks it on the device: unsplit layouts with more (sequence, head) items than
+    CUs (512 and 720 items at H = 16, ragged, with empty, one-token and 31 / 32 / 33 / 63 / 64 / 65-token sequences,
+    with and without initial states), against the oracle on a few heads; and with the gates, beta and q / k norms in
+    the kernel (kda_prefill), against the 64-token kernel on the same plan (both within the north-star state bar of
+    each other)."""
+    kda = _kda()
+    cus = torch.cuda.get_device_properties(DEV).multi_processor_count
+    rng = np.random.default_rng(31)
+    lens = [int(x) for x in rng.integers(100, 700, size=30)] + [0, 1]
+    _plain_case(oracle, 16, lens, 120, heads_checked=[0, 5, 15], cus=cus, chunk64=False)
+    lens = [int(x) for x in rng.integers(1, 300, size=39)] + [31, 32, 33, 63, 64, 65]
+    _plain_case(oracle, 16, lens, 121, init=False, heads_checked=[3, 9], cus=cus, chunk64=False)
+    H, lens = 16, [int(x) for x in rng.integers(50, 600, size=32)]
+    T = sum(lens)
+    _say(f"chunk32 against chunk64, gates in the kernel, H={H} N={len(lens)}")
+    g = gen(122)
+    q, k, v, raw_g, raw_b, A_log, dt_bias = _raw_inputs(g, T, H)
+    h0 = (torch.randn(len(lens), H, D, D, generator=g) * 0.05).to(DEV)
+    cu = torch.tensor(_cu(lens), dtype=torch.int32)
+    res = {}
+    for c64 in (True, False):
+        meta = _list_meta(kda, lens, H, cus, c64)
+        o, f = kda.kda_prefill(q[None].to(DEV), k[None].to(DEV), v[None].to(DEV), raw_g[None].to(DEV),
+                               raw_b[None].to(DEV), A_log.to(DEV), dt_bias.to(DEV), h0.clone(), cu_seqlens=cu.to(DEV),
+                               meta=meta)
+        torch.cuda.synchronize()
+        res[c64] = (f32(o[0]), f32(f))
+    (o64, f64), (o32, f32_) = res[True], res[False]
+    rel = float(np.linalg.norm(o32 - o64) / np.linalg.norm(o64))
+    worst = max(rel_frob(f32_[n], f64[n]) for n in range(len(lens)))
+    _say(f"  output relL2 {rel:.3e}, worst final-state relF {worst:.3e}")
+    assert rel <= 2e-2 and worst <= STATE_TOL, (rel, worst)
 
 
 def test_other_head_counts(oracle):
@@ -254,17 +295,18 @@ def _pages(slots, H, taps, g):
     return raw, ssm
 
 
-@pytest.mark.parametrize("cus", [None, 4])
-def test_serving_pool_checkpoints_page_layout(oracle, cus):
+@pytest.mark.parametrize("cus,chunk64", [(None, True), (4, True), (4, False)], ids=["whole", "lists", "chunk32"])
+def test_serving_pool_checkpoints_page_layout(oracle, cus, chunk64):
     """prefill_prepare + prefill on the page layout: has_initial_state with NaN rows, one checkpoint per sequence,
-    strided raw_beta, out a slice behind 256 leading rows; only out and the named rows change.  cus = 4: planned as
-    workgroup lists on 4 CUs (7 items per list, gates in the kernel: each item's dt_bias handed to the next)."""
+    strided raw_beta, out a slice behind 256 leading rows; only out and the named rows change.  cus = 4: 28 items for
+    4 CUs, run as the 64-token kernel's workgroup lists (7 items per list, gates in the kernel: each item's dt_bias
+    handed to the next) and as the 32-token kernel (one workgroup per item)."""
     kda = _kda()
     H = 4
     lens = [777, 64, 1, 130, 1024, 17, 255]
     hinit = [1, 0, 1, 0, 1, 1, 0]
     ck_off = [704, 64, 0, 0, 1024, 0, 192]
-    _say(f"serving pool H={H} lens={lens} cus={cus}")
+    _say(f"serving pool H={H} lens={lens} cus={cus} chunk64={chunk64}")
     g = gen(40)
     T, N = sum(lens), len(lens)
     q, k, v, raw_g, raw_b, A_log, dt_bias = _raw_inputs(g, T, H)
@@ -289,7 +331,7 @@ def test_serving_pool_checkpoints_page_layout(oracle, cus):
     parent_before = parent.clone()
     cu_cpu = torch.tensor(_cu(lens), dtype=torch.int32)
     meta = (kda.prefill_prepare(cu_cpu, H, torch.tensor(ck_off, dtype=torch.int32), cidx, device=DEV) if cus is None
-            else _list_meta(kda, lens, H, cus, checkpoint_offsets=torch.tensor(ck_off, dtype=torch.int32)))
+            else _list_meta(kda, lens, H, cus, chunk64, checkpoint_offsets=torch.tensor(ck_off, dtype=torch.int32)))
     kda.prefill(q[None].to(DEV), k[None].to(DEV), v[None].to(DEV), raw_g[None].to(DEV), beta_view, A_log.to(DEV),
                 dt_bias.to(DEV), D ** -0.5, -5.0, ssm, sidx.to(DEV), torch.tensor(hinit, dtype=torch.bool).to(DEV),
                 cu_cpu.to(DEV), out, torch.tensor(ck_off, dtype=torch.int32).to(DEV), cidx.to(DEV), meta=meta)
@@ -339,15 +381,17 @@ def test_serving_no_sync_with_meta():
     assert torch.isfinite(out.float()).all()
 
 
-@pytest.mark.parametrize("every,cus", [(64, None), (256, None), (64, 4)])
-def test_every_n_checkpoints_fp32_and_bf16(oracle, every, cus):
+@pytest.mark.parametrize("every,cus,chunk64", [(64, None, True), (256, None, True), (64, 4, True), (64, 4, False),
+                                               (256, 4, False)])
+def test_every_n_checkpoints_fp32_and_bf16(oracle, every, cus, chunk64):
     """B200 every-n rows (kda/b200/test_kda_b200.py:213-240): fp32 rows match the oracle; bf16 rows are exactly the
-    fp32 rows rounded to nearest even; output and pool are identical across checkpoint dtypes.  cus = 4: planned as
-    workgroup lists on 4 CUs."""
+    fp32 rows rounded to nearest even; output and pool are identical across checkpoint dtypes.  cus = 4: 20 items for
+    4 CUs, as the 64-token kernel's workgroup lists (chunk64) or the 32-token kernel, whose checkpoints fall after every
+    second 32-token chunk."""
     kda = _kda()
     H, lens = 4, [300, 64, 1, 1000, 77]
-    _say(f"every-n every={every} cus={cus}")
-    meta = _list_meta(kda, lens, H, cus, ck_every=every) if cus else None
+    _say(f"every-n every={every} cus={cus} chunk64={chunk64}")
+    meta = _list_meta(kda, lens, H, cus, chunk64, ck_every=every) if cus else None
     g = gen(50 + every)
     T, N = sum(lens), len(lens)
     q, k, v, raw_g, raw_b, A_log, dt_bias = _raw_inputs(g, T, H)

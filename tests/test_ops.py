@@ -96,7 +96,7 @@ def test_plan_tensor_round_trip():
     assert bytes(back.plan) == bytes(meta.plan)
     assert back.tables is table and back.any_ck == meta.any_ck and back.H == 4 and back.N == 5
     assert np.array_equal(back.lens, meta.lens)
-    assert back.workspace_bytes == meta.workspace_bytes and back.split == meta.split
+    assert back.workspace_bytes == meta.workspace_bytes and back.split == meta.split and back.chunk64 == meta.chunk64
 
 
 def test_plan_tensor_mismatch_rejected():
