@@ -6,13 +6,14 @@
 // workgroups whose barriers and dependent chains do not line up.  Per token the work is the same (the Gram and solve
 // blocks shrink with the chunk; the per-chunk state work -- decay, fp16 copies of S -- doubles).  Each wave keeps a
 // 128 x 32 slice of S (64 VGPRs), so a piece that also carries its transition does not fit: this kernel runs unsplit
-// layouts only, and the launch picks it when the plan has more (sequence, head) items than CUs (the layouts the plan
-// gives workgroup lists for chunk_kernel), outside the precise mode.
+// layouts only: the plan picks it (KdaPrefillPlan.chunk32) for layouts whose items outnumber the CUs when its schedule
+// model has it finish first, and launches in the precise mode keep chunk_kernel.
 //
 // Same algorithm, phases and operand conventions as chunk_kernel, with two row blocks of 16 instead of four:
 //   P0 raw rows (gate, beta, q / k sums of squares), P1 gate cumsum in 2 segments, P2 element and block factors
-//   (7 factor rows), P4 Gram tiles (wave 0 / 1: diagonal blocks with the bf16 hi / lo split and T_II; wave 2: block
-//   (1, 0)), P5 Q~ and Kd^T layouts (tokens permuted by pos32), P6 W / U (wave w: channel / value tiles 2 w, 2 w + 1),
+//   (7 factor rows), P4 Gram tiles (wave I = 0 / 1: diagonal block I's A_kk with the bf16 hi / lo split, then T_II;
+//   wave 2 + I: its A_qk, then one product of block (1, 0)), P5 Q~ and Kd^T layouts (tokens permuted by pos32),
+//   P6 W / U (wave w: channel / value tiles 2 w, 2 w + 1),
 //   P7 the walk (wave w: S[:, 32 w .. 32 w + 31], K step outermost).  Checkpoints fall on 64-token boundaries, i.e.
 //   after every second chunk (or after the last chunk of the sequence).
 constexpr int C32_THREADS = 256;
@@ -270,50 +271,48 @@ __global__ void __launch_bounds__(C32_THREADS) __attribute__((amdgpu_waves_per_e
             }
         }
         lds_barrier();
-        // ================= P4: Gram tiles
-        if (w < 2) {  // diagonal block I = w: bf16 hi + lo products, then T_II = (I + L_II)^-1
-            const int I = w, i = 16 * I + m;
-            f32x4 akk = {0.f, 0.f, 0.f, 0.f}, aqk = akk;
+        // ================= P4: Gram tiles.  Wave I (0, 1): the diagonal block's A_kk (bf16 hi + lo products of
+        // k^ fi and k^ fj), then T_II = (I + L_II)^-1; wave 2 + I: the same block's A_qk (k^ fj and q^ fi), then one
+        // product of block (1, 0) from fp16 operands <= 1 (reference row 15): A_kk on wave 2, A_qk on wave 3.
+        {
+            const int I = w & 1, i = 16 * I + m;
+            const bool kk = w < 2;  // wave-uniform
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+            const float* sX = kk ? sKA : sQA;  // the product's second operand: k^ fi (A_kk) or q^ fi (A_qk)
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
                 const int c0 = 32 * s + 8 * g;
-                uint32_t kah[4], kal[4], qah[4], qal[4], kbh[4], kbl[4];
+                uint32_t xh[4], xl[4], kbh[4], kbl[4];
 #pragma unroll
                 for (int hf = 0; hf < 2; ++hf) {
-                    const f32x4 ka = *reinterpret_cast<const f32x4*>(&sKA[i * RS32 + swz(c0 + 4 * hf)]);
-                    const f32x4 qa = *reinterpret_cast<const f32x4*>(&sQA[i * RS32 + swz(c0 + 4 * hf)]);
+                    const f32x4 xa = *reinterpret_cast<const f32x4*>(&sX[i * RS32 + swz(c0 + 4 * hf)]);
                     const f32x4 kb = *reinterpret_cast<const f32x4*>(&sKB[i * RS32 + swz(c0 + 4 * hf)]);
 #pragma unroll
                     for (int j = 0; j < 2; ++j) {
                         const int ee = 2 * hf + j;
-                        split_bf16x2(ka[2 * j], ka[2 * j + 1], kah[ee], kal[ee]);
-                        split_bf16x2(qa[2 * j], qa[2 * j + 1], qah[ee], qal[ee]);
+                        split_bf16x2(xa[2 * j], xa[2 * j + 1], xh[ee], xl[ee]);
                         split_bf16x2(kb[2 * j], kb[2 * j + 1], kbh[ee], kbl[ee]);
                     }
                 }
-                const bf16x8 Kah = as_bf16x8(kah), Kal = as_bf16x8(kal), Qah = as_bf16x8(qah), Qal = as_bf16x8(qal);
-                const bf16x8 Kbh = as_bf16x8(kbh), Kbl = as_bf16x8(kbl);
-                akk = mfma32bf(Kah, Kbh, akk);
-                akk = mfma32bf(Kah, Kbl, akk);
-                akk = mfma32bf(Kal, Kbh, akk);
-                aqk = mfma32bf(Kbh, Qah, aqk);  // transposed: lane (g, m) holds row 16 I + m
-                aqk = mfma32bf(Kbl, Qah, aqk);
-                aqk = mfma32bf(Kbh, Qal, aqk);
+                const bf16x8 Xh = as_bf16x8(xh), Xl = as_bf16x8(xl), Kbh = as_bf16x8(kbh), Kbl = as_bf16x8(kbl);
+                if (kk) {  // A_kk: lane (g, m) holds row 16 I + 4 g + e, column 16 I + m
+                    acc = mfma32bf(Xh, Kbh, acc);
+                    acc = mfma32bf(Xh, Kbl, acc);
+                    acc = mfma32bf(Xl, Kbh, acc);
+                } else {   // A_qk transposed: lane (g, m) holds row 16 I + m, columns 16 I + 4 g .. + 3
+                    acc = mfma32bf(Kbh, Xh, acc);
+                    acc = mfma32bf(Kbl, Xh, acc);
+                    acc = mfma32bf(Kbh, Xl, acc);
+                }
             }
-            f32x4 lt;
-            f16x4 aq;
-            const f32x4 bt4 = *reinterpret_cast<const f32x4*>(&sBeta[16 * I + 4 * g]);
+            if (kk) {
+                f32x4 lt;
+                const f32x4 bt4 = *reinterpret_cast<const f32x4*>(&sBeta[16 * I + 4 * g]);
 #pragma unroll
-            for (int ee = 0; ee < 4; ++ee) {
-                const int rr = 4 * g + ee;
-                lt[ee] = (m < rr) ? bt4[ee] * akk[ee] : 0.f;
-                aq[ee] = (half_t)((rr <= m) ? aqk[ee] : 0.f);  // causal within the block
-            }
-            *reinterpret_cast<f16x4*>(&sAq[i * RS16T + pos32(16 * I + 4 * g)]) = aq;
-            *reinterpret_cast<f32x4*>(&sL[(I * 16 + m) * 20 + 4 * g]) = lt;
-            {
-                const float* Lb = sL + I * 16 * 20;  // column k of L_II is the contiguous row k
-                float x[16];
+                for (int ee = 0; ee < 4; ++ee) lt[ee] = (m < 4 * g + ee) ? bt4[ee] * acc[ee] : 0.f;
+                *reinterpret_cast<f32x4*>(&sL[(I * 16 + m) * 20 + 4 * g]) = lt;
+                const float* Lb = sL + I * 16 * 20;  // column k of L_II is the contiguous row k; the wave reads back
+                float x[16];                         // what it has just written (its LDS operations complete in order)
 #pragma unroll
                 for (int ii = 0; ii < 16; ++ii) x[ii] = (ii == m) ? 1.f : 0.f;
 #pragma unroll
@@ -331,40 +330,49 @@ __global__ void __launch_bounds__(C32_THREADS) __attribute__((amdgpu_waves_per_e
 #pragma unroll
                     for (int ii = 0; ii < 16; ++ii) sAk[(16 * I + ii) * RS16T + 16 * I + m] = (half_t)x[ii];
                 }
+            } else {
+                f16x4 aq;
+#pragma unroll
+                for (int ee = 0; ee < 4; ++ee) aq[ee] = (half_t)((4 * g + ee <= m) ? acc[ee] : 0.f);  // causal
+                *reinterpret_cast<f16x4*>(&sAq[i * RS16T + pos32(16 * I + 4 * g)]) = aq;
             }
-        } else if (w == 2) {  // block (1, 0) from fp16 operands <= 1 (reference row 15)
+        }
+        if (w >= 2) {  // block (1, 0): wave 2 A_kk, wave 3 A_qk (transposed tiles: lane (g, m) holds row 16 + m,
+                       // columns 4 g .. + 3)
+            const bool kk = w == 2;
             const int i = 16 + m;
-            f32x4 akk = {0.f, 0.f, 0.f, 0.f}, aqk = akk;
+            const float* sX = kk ? sKA : sQA;
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
                 const int c0 = 32 * s + 8 * g;
-                f16x8 ka, qa, kb;
+                f16x8 xa, kb;
 #pragma unroll
                 for (int hf = 0; hf < 2; ++hf) {
-                    const f32x4 a = *reinterpret_cast<const f32x4*>(&sKA[i * RS32 + swz(c0 + 4 * hf)]);
-                    const f32x4 q4 = *reinterpret_cast<const f32x4*>(&sQA[i * RS32 + swz(c0 + 4 * hf)]);
+                    const f32x4 a = *reinterpret_cast<const f32x4*>(&sX[i * RS32 + swz(c0 + 4 * hf)]);
                     const f32x4 fa = *reinterpret_cast<const f32x4*>(&sF[F32_A * 128 + c0 + 4 * hf]);
                     const f32x4 b = *reinterpret_cast<const f32x4*>(&sKB[m * RS32 + swz(c0 + 4 * hf)]);
                     const f32x4 fb = *reinterpret_cast<const f32x4*>(&sF[F32_B * 128 + c0 + 4 * hf]);
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
-                        ka[4 * hf + j] = (half_t)(a[j] * fa[j]);
-                        qa[4 * hf + j] = (half_t)(q4[j] * fa[j]);
+                        xa[4 * hf + j] = (half_t)(a[j] * fa[j]);
                         kb[4 * hf + j] = (half_t)(b[j] * fb[j]);
                     }
                 }
-                akk = mfma32(kb, ka, akk);  // transposed tiles: lane (g, m) holds row 16 + m, columns 4 g .. + 3
-                aqk = mfma32(kb, qa, aqk);
+                acc = mfma32(kb, xa, acc);
             }
-            const float nb = -sBeta[i];
-            f16x4 ak, aq;
+            if (kk) {
+                const float nb = -sBeta[i];
+                f16x4 ak;
 #pragma unroll
-            for (int ee = 0; ee < 4; ++ee) {
-                ak[ee] = (half_t)(nb * akk[ee]);
-                aq[ee] = (half_t)aqk[ee];
+                for (int ee = 0; ee < 4; ++ee) ak[ee] = (half_t)(nb * acc[ee]);
+                *reinterpret_cast<f16x4*>(&sAk[i * RS16T + 4 * g]) = ak;
+            } else {
+                f16x4 aq;
+#pragma unroll
+                for (int ee = 0; ee < 4; ++ee) aq[ee] = (half_t)acc[ee];
+                *reinterpret_cast<f16x4*>(&sAq[i * RS16T + pos32(4 * g)]) = aq;
             }
-            *reinterpret_cast<f16x4*>(&sAk[i * RS16T + 4 * g]) = ak;
-            *reinterpret_cast<f16x4*>(&sAq[i * RS16T + pos32(4 * g)]) = aq;
         }
         // ================= P5: Q~, Kd^T into their walk layouts (raw threads)
         // the start state's loads complete here in the first chunk (an empty use of S), not before a later walk
