@@ -22,6 +22,9 @@ The other configurations are reported beside it (never as `value`):
   plain        (opt-in, --configs ...,plain) the reference's 10 phase-1 plain prefill workloads at H = 12 through
                kda_prefill, timed like the reference (median of 50 flushed single calls, launch included) beside its
                published MI350X latencies
+  chunk32      (opt-in, --configs ...,chunk32) the 32-token chunk kernel (two workgroups per CU) against the 64-token
+               kernel with its workgroup lists on unsplit layouts with more (sequence, head) items than CUs: the same
+               plan made with chunk64=True and chunk64=False, timed in alternation (three rounds, best of each)
   legacy       (opt-in, --configs ...,legacy) the reference eval's two phase-1 no-regression gates: the 10 plain
                layouts through prefill() on a contiguous pool against recorded vLLM latencies, the 17 phase-1 decode
                shapes on dense pools against recorded best-baseline latencies; metric mean(recorded / ours), beside
@@ -39,6 +42,7 @@ rocprofv3 FETCH_SIZE / WRITE_SIZE summary (profiles/prefill_c1_c2_split.md), or 
 from __future__ import annotations
 
 import argparse
+import itertools
 import json
 import math
 import os
@@ -168,7 +172,7 @@ def bench_c1(kda, torch, dev, steps, warmup, flush):
     T, N, H = sum(lens), len(lens), 32
     q, k, v, g, beta = synth(T, H, dev, 1, torch)
     h0 = torch.randn(N, H, D, D, generator=torch.Generator(device=dev).manual_seed(2), device=dev) * 0.02
-    cu = torch.tensor([0] + list(__import__("itertools").accumulate(lens)), dtype=torch.int32)
+    cu = torch.tensor([0] + list(itertools.accumulate(lens)), dtype=torch.int32)
     meta = kda.plan(cu, H, device=dev)
     ws = torch.empty(meta.workspace_bytes, dtype=torch.uint8, device=dev)
     out = torch.empty(1, T, H, D, dtype=torch.bfloat16, device=dev)
@@ -533,6 +537,40 @@ def bench_legacy_decode(kda, torch, dev, name, H, B, S, reps, flush):
     return us
 
 
+# unsplit layouts with more items than CUs: (sequence lengths, H); chunk_kda plain calls on config-style inputs
+CHUNK32_LAYOUTS = {
+    "32x512 H16": ([512] * 32, 16), "32x1024 H16": ([1024] * 32, 16), "64x256 H16": ([256] * 64, 16),
+    "16x2048 H32": ([2048] * 16, 32), "32x512 H12": ([512] * 32, 12),
+    "32x(256..1023) H16": ([256 + (97 * i) % 768 for i in range(32)], 16), "64x128 H12": ([128] * 64, 12),
+}
+
+
+def bench_chunk32(kda, torch, dev, lens, H, reps, seed):
+    """ms per call of the 64-token and the 32-token chunk kernel on one layout (best of three alternated rounds of
+    `reps` back-to-back calls; the inputs stay resident)."""
+    T = sum(lens)
+    q, k, v, g, beta = synth(T, H, dev, seed, torch)
+    cu = torch.tensor([0] + list(itertools.accumulate(lens)), dtype=torch.int32)
+    metas = {c64: kda.plan(cu, H, device=dev, chunk64=c64) for c64 in (True, False)}
+    cud = cu.to(dev)
+    best = {}
+    for _ in range(3):
+        for c64, meta in metas.items():
+            for _ in range(5):
+                kda.chunk_kda(q, k, v, g, beta, cu_seqlens=cud, meta=meta)
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            a.record()
+            for _ in range(reps):
+                kda.chunk_kda(q, k, v, g, beta, cu_seqlens=cud, meta=meta)
+            b.record()
+            torch.cuda.synchronize()
+            best[c64] = min(best.get(c64, 1e9), a.elapsed_time(b) / reps)
+    assert all(m.plan.num_split == 0 for m in metas.values()), "chunk32 layouts must plan unsplit"
+    plan_choice = int(kda.plan(cu, H, device=dev).plan.chunk32)
+    return best[True], best[False], plan_choice
+
+
 def bench_plain_prefill(kda, torch, dev, lens, reps, flush, seed):
     """One plain `kda355.kda_prefill` call (the reference's phase-1 interface) on inputs drawn like
     kda/mi350x_plain/bench.py:57-67; the plan is made once outside the timed region, like the reference's prepare()."""
@@ -731,6 +769,15 @@ def main():
                                   "mean_ratio": round(sum(x["ratio"] for x in rows) / len(rows), 3),
                                   "geomean_ratio": round(gm([x["ratio"] for x in rows]), 3), "rows": rows}
 
+    if "chunk32" in cfgs:  # opt-in: the 32-token kernel against the 64-token kernel on layouts with many items
+        rows = []
+        for i, (name, (lens, H)) in enumerate(CHUNK32_LAYOUTS.items()):
+            t64, t32, choice = bench_chunk32(kda355, torch, dev, lens, H, max(args.steps, 30), 300 + i)
+            rows.append({"layout": name, "H": H, "items": len(lens) * H, "chunk64_ms": round(t64, 4),
+                         "chunk32_ms": round(t32, 4), "ratio": round(t32 / t64, 3), "plan_chooses_chunk32": choice})
+            log(f"chunk32 {name}: 64-token {t64:.4f} ms, 32-token {t32:.4f} ms ({t32 / t64:.3f}; plan: {choice})")
+        extra["chunk32"] = {"method": "chunk_kda plain calls, the plan made with chunk64=True / False, best of three "
+                                      "alternated rounds", "rows": rows}
     if cfgs & {"legacy", "legacy_prefill", "legacy_decode"}:  # opt-in: the reference eval's phase-1 no-regression
         # gates, its metric mean(recorded / ours); legacy_prefill / legacy_decode run one of the two
         prows, drows = [], []
