@@ -665,7 +665,9 @@ def main():
     ap.add_argument("--configs", default="c1,c3,c4,d1,c2")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--calib-copy", action="store_true",
-                    help="also run a 1 GiB device-to-device copy 5x (the known-size kernel for HBM counter scaling)")
+                    help="also run a 1 GiB device-to-device copy 5x (the known-size kernel for HBM counter scaling), "
+                         "timed, and a timed bf16 elementwise add (two 384 MiB reads, one write): the box's practical "
+                         "read + write stream rates, reported as hbm_streams")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -689,16 +691,38 @@ def main():
         a = torch.empty(1 << 28, dtype=torch.float32, device=dev)
         b = torch.empty_like(a)
         a.fill_(1.0)
+        b.copy_(a)  # one untimed
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
         for _ in range(5):
             b.copy_(a)
+        e1.record()
         torch.cuda.synchronize()
-        log("calibration copy: 5 x 1 GiB read + 1 GiB write")
+        copy_s = e0.elapsed_time(e1) * 1e-3 / 5
         del a, b
+        x, y = (torch.ones(3 << 27, dtype=torch.bfloat16, device=dev) for _ in range(2))
+        o = torch.empty_like(x)
+        torch.add(x, y, out=o)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(5):
+            torch.add(x, y, out=o)
+        e1.record()
+        torch.cuda.synchronize()
+        add_s = e0.elapsed_time(e1) * 1e-3 / 5
+        add_bytes = 3 * x.numel() * 2
+        del x, y, o
+        hbm_streams = {"copy_1GiB": {"us": round(copy_s * 1e6, 1), "GB_per_s": round(2 * 2 ** 30 / copy_s / 1e9, 1)},
+                       "bf16_add_2r1w": {"bytes": add_bytes, "us": round(add_s * 1e6, 1),
+                                         "GB_per_s": round(add_bytes / add_s / 1e9, 1)}}
+        log(f"calibration copy: 5 x 1 GiB read + 1 GiB write, {hbm_streams['copy_1GiB']['GB_per_s']} GB/s; "
+            f"bf16 add {hbm_streams['bf16_add_2r1w']['GB_per_s']} GB/s")
 
     log(f"c1 prefill: steps {args.steps} warmup {args.warmup}")
     c1, cpu_inputs = bench_c1(kda355, torch, dev, args.steps, args.warmup, flush)
     log(f"c1: {c1['ms']:.3f} ms/step (flushed median {c1['flushed_ms']:.3f} ms)")
-    extra = {}
+    extra = {"hbm_streams": hbm_streams} if args.calib_copy else {}
     if "c3" in cfgs:
         d = bench_decode(kda355, torch, dev, args.steps, args.warmup)
         gbs = d["state_bytes"] / (d["us"] * 1e-6) / 1e9
