@@ -1830,10 +1830,12 @@ extern "C" int kda355_prefill_plan(const KdaPrefillPlanIn* in, KdaPrefillPlan* p
         // The 32-token kernel's schedule (chunk32.h): one workgroup per item, two per CU, items in launch order, the
         // first 2 x num_cus dealt two to a CU and every later one to the CU that frees a slot first.  A workgroup
         // advances C32_PAIRED chunk times per 64 tokens while it shares its CU and C32_ALONE when alone, plus
-        // C32_START of start-up (measured on MI355X against the 64-token kernel's chunk: 512 items of 8-32 chunks run
-        // 7-11 % faster paired; a 47-chunk chain mostly alone runs 30 % slower).  It is used when this simulated span
-        // beats the 64-token kernel's best (lists or one workgroup per item) by 3 %.
-        constexpr double C32_ALONE = 1.3, C32_PAIRED = 1.85, C32_START = 0.5;
+        // C32_START of start-up, in chunk times of the 64-token kernel.  The constants are a least-squares fit (in
+        // log ratio) to eleven layouts timed on MI355X with both kernels: 384-1024 items of 2-32 chunks, where the
+        // 32-token kernel runs 3-11 % faster, a ragged layout 8 % slower, the 5-47-chunk p96 layouts 28-35 % slower
+        // (long chains alone on their CUs).  It is used when this simulated span beats the 64-token kernel's best
+        // (lists or one workgroup per item) by 3 %.
+        constexpr double C32_ALONE = 1.2, C32_PAIRED = 1.85, C32_START = 0.3;
         struct Cu { double t = 0, w[2] = {0, 0}; int n = 0, ver = 0; };
         std::vector<Cu> cu(num_cus);
         typedef std::pair<double, std::pair<int, int>> Ev;  // (finish time, (CU, version))
@@ -1849,21 +1851,37 @@ extern "C" int kda355_prefill_plan(const KdaPrefillPlanIn* in, KdaPrefillPlan* p
         for (int rnd = 0; rnd < 2; ++rnd)
             for (int c = 0; c < num_cus && next < items; ++c) cu[c].w[cu[c].n++] = item_work(next++);
         for (int c = 0; c < num_cus; ++c) schedule(c);
+        // Workgroups that finish at one instant free their slots together; the waiting items go first one to each
+        // such CU, then to the CUs that freed a second slot (the hardware spreads a burst over the CUs).
         double span32 = 0;
+        std::vector<int> freed[2];
         while (!ev.empty()) {
-            const Ev e = ev.top();
-            ev.pop();
-            Cu& u = cu[e.second.first];
-            if (e.second.second != u.ver) continue;  // superseded by a later change of this CU
-            const double r = u.n == 2 ? C32_PAIRED : C32_ALONE, dt = e.first - u.t;
-            for (int j = 0; j < u.n; ++j) u.w[j] -= dt / r;
-            u.t = e.first;
-            span32 = std::max(span32, e.first);
-            const int done = (u.n == 2 && u.w[1] < u.w[0]) ? 1 : 0;  // the workgroup that finished
-            u.w[done] = u.w[u.n - 1];
-            --u.n;
-            if (next < items) u.w[u.n++] = item_work(next++);
-            schedule(e.second.first);
+            const double t = ev.top().first;
+            freed[0].clear();
+            freed[1].clear();
+            while (!ev.empty() && ev.top().first <= t + 1e-9) {
+                const Ev e = ev.top();
+                ev.pop();
+                const int c = e.second.first;
+                Cu& u = cu[c];
+                if (e.second.second != u.ver) continue;  // superseded by a later change of this CU
+                const double r = u.n == 2 ? C32_PAIRED : C32_ALONE;
+                double w[2], wmin = 1e300;
+                for (int j = 0; j < u.n; ++j) wmin = std::min(wmin, w[j] = u.w[j] - (e.first - u.t) / r);
+                int left = 0;  // the event's workgroup finishes whatever the rounding left of its work
+                for (int j = 0; j < u.n; ++j)
+                    if (w[j] > std::max(1e-9, wmin + 1e-9)) u.w[left++] = w[j];
+                for (int j = left; j < u.n; ++j) freed[j - left].push_back(c);
+                u.n = left;
+                u.t = e.first;
+                ++u.ver;
+                span32 = std::max(span32, e.first);
+            }
+            for (int k = 0; k < 2; ++k)
+                for (const int c : freed[k])
+                    if (next < items) cu[c].w[cu[c].n++] = item_work(next++);
+            for (int k = 0; k < 2; ++k)
+                for (const int c : freed[k]) schedule(c);  // a CU listed twice is rescheduled twice: the later wins
         }
         if (span32 < 0.97 * 0.25 * (double)std::min(span_lst, span_dyn)) chunk32 = 1;
     }

@@ -227,12 +227,15 @@ def test_prefill_plan_workgroup_lists():
 def test_prefill_plan_chunk32_choice():
     """The 32-token kernel (two workgroups per CU) is chosen for unsplit layouts with more items than CUs when the
     plan's schedule model has it finish first: items of similar length that keep both workgroups of a CU busy; not
-    when a few long chains would run alone on their CUs (p96_loaded8k_1), not for short items (p_64x128, where the
-    lists win), nor for split layouts or layouts that fit the CUs."""
-    for lens, H in (([512] * 32, 12), ([512] * 32, 16), ([1024] * 32, 16), ([256] * 64, 16), ([2048] * 16, 32)):
+    when a few long chains would run alone on their CUs (p96_loaded8k_1, p96_light8k_0) or pairs of unequal items
+    would leave the longer alone (a ragged 256-1023-token layout), nor for split layouts or layouts that fit the CUs.
+    Each case is one the model was fitted on, timed on MI355X with both kernels."""
+    for lens, H in (([512] * 32, 12), ([512] * 32, 16), ([1024] * 32, 16), ([256] * 64, 16), ([2048] * 16, 32),
+                    ([128] * 64, 12), ([128] * 128, 12)):
         pl, _ = _plan(lens, H, 256)
         assert pl.num_split == 0 and pl.chunk32 == 1, (lens[:2], H)
-    for lens, H in (([384, 1344, 3008, 2176, 320, 832], 96), ([128] * 64, 12), ([131072], 32), ([8192] * 8, 32),
+    for lens, H in (([384, 1344, 3008, 2176, 320, 832], 96), ([704, 1216, 512], 96),
+                    ([256 + (97 * i) % 768 for i in range(32)], 16), ([131072], 32), ([8192] * 8, 32),
                     ([100] * 10, 4)):
         pl, _ = _plan(lens, H, 256)
         assert pl.chunk32 == 0, (lens[:2], H)
