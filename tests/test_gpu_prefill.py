@@ -164,24 +164,44 @@ def test_slow_and_fast_decay(oracle):
     _plain_case(oracle, 2, [1000], 21, gscale=4.0)         # fast decay
 
 
+def _deep_gates(gg, g):
+    """-20 and -30 on random channels and tokens (a quarter of all values), the rest as given."""
+    pick = torch.rand(gg.shape, generator=g)
+    return torch.where(pick < 0.125, torch.full_like(gg, -20.0), torch.where(pick < 0.25, torch.full_like(gg, -30.0), gg))
+
+
 def test_log_decay_below_range_is_clamped(oracle):
     """Given per-token log-decays far below KDA355_MIN_LOG_DECAY (-9): -20 and -30 on random channels and tokens (a
     quarter of all values), on a split layout (one long sequence in many pieces) and a whole one.  The kernel raises
     them to -9, a decay of e^-9 instead of a smaller one, which moves the state by less than 1.2e-4 of the affected
     channel; outputs and states stay finite and within the bars of the exact fp64 oracle."""
-    def deep(gg, g):
-        pick = torch.rand(gg.shape, generator=g)
-        return torch.where(pick < 0.125, torch.full_like(gg, -20.0), torch.where(pick < 0.25, torch.full_like(gg, -30.0), gg))
-    _plain_case(oracle, 2, [6000, 300], 22, gmod=deep)
-    _plain_case(oracle, 4, [700, 1], 23, gmod=deep)
+    _plain_case(oracle, 2, [6000, 300], 22, gmod=_deep_gates)
+    _plain_case(oracle, 4, [700, 1], 23, gmod=_deep_gates)
 
 
-def test_raw_gate_lower_bound_below_range(oracle):
+def test_chunk32_decay_extremes(oracle):
+    """The 32-token kernel (planned for 4 CUs: 16 items, one workgroup each) at the decay extremes the 64-token kernel
+    is tested at: long memory (g x 0.01), fast decay (g x 4), and given log-decays of -20 / -30 raised to -9, on ragged
+    sequences with empty, one-token and one-chunk-plus-one ones, against the fp64 oracle."""
+    lens = [600, 300, 130, 1, 0, 65, 700, 33]
+    _plain_case(oracle, 2, lens, 140, gscale=0.01, cus=4, chunk64=False)
+    _plain_case(oracle, 2, lens, 141, gscale=4.0, cus=4, chunk64=False)
+    _plain_case(oracle, 2, lens, 142, gmod=_deep_gates, cus=4, chunk64=False)
+
+
+@pytest.mark.parametrize("chunk64", [None, False], ids=["plan", "chunk32"])
+def test_raw_gate_lower_bound_below_range(oracle, chunk64):
     """kda_prefill with lower_bound = -20 and saturated gates (dt_bias 20..30, so g = lower_bound * sigmoid(.) reaches
-    -20 on every channel): the in-kernel gate is raised to -9 like a given one, and the result matches the oracle."""
+    -20 on every channel): the in-kernel gate is raised to -9 like a given one, and the result matches the oracle.  plan:
+    the launch's own plan (the long sequence in pieces); chunk32: more sequences, planned for 4 CUs as the 32-token
+    kernel, one of them a single token.  Every final state meets the state bar against the oracle with its gates raised
+    to -9 (the kernel's definition).  Against the exact oracle, the clamp adds e^-9 of the start state: relative to a
+    state of many tokens that is ~1e-4, inside the bar.  After a single token whose update is small beside a start
+    state of scale 0.25, it is 9.8e-4 on its own (measured on MI355X: both chunk kernels then read 1.028e-3 against
+    the exact oracle and 3.0e-4 against the clamped one), so that sequence is held to the clamped oracle alone."""
     kda = _kda()
-    H, lens = 2, [1100, 64]
-    _say("kda_prefill lower_bound=-20, saturated gates")
+    H, lens = (2, [1100, 64]) if chunk64 is None else (2, [600, 500, 300, 64, 1])
+    _say(f"kda_prefill lower_bound=-20, saturated gates, {'plan' if chunk64 is None else '32-token kernel'}")
     g = gen(33)
     T = sum(lens)
     q, k, v, raw_g, raw_b, A_log, dt_bias = _raw_inputs(g, T, H)
@@ -189,17 +209,21 @@ def test_raw_gate_lower_bound_below_range(oracle):
     dt_bias = torch.linspace(20.0, 30.0, D).repeat(H)
     h0 = torch.randn(len(lens), H, D, D, generator=g) * 0.25
     cu = torch.tensor(_cu(lens), dtype=torch.int64)
+    meta = None if chunk64 is None else _list_meta(kda, lens, H, 4, chunk64)
     o, fin = kda.kda_prefill(q[None].to(DEV), k[None].to(DEV), v[None].to(DEV), raw_g[None].to(DEV),
                              raw_b[None].to(DEV), A_log.to(DEV), dt_bias.to(DEV), h0.to(DEV), cu.to(DEV),
-                             lower_bound=-20.0)
+                             lower_bound=-20.0, meta=meta)
     torch.cuda.synchronize()
     qn, kn, vf, gl, bt = _oracle_gated(oracle, q, k, v, raw_g, raw_b, A_log, dt_bias, lb=-20.0)
     assert gl.min() < -19.0, "the case must drive the gate below the range"
     ro, rf, _ = oracle.chains(qn, kn, vf, gl, bt, _cu(lens), D ** -0.5, f32(h0), precision=64)
+    _, rf9, _ = oracle.chains(qn, kn, vf, np.maximum(gl, -9.0), bt, _cu(lens), D ** -0.5, f32(h0), precision=64)
     _check_out(o[0], ro, "lower_bound=-20", _cu(lens))
     for n in range(len(lens)):
-        e = rel_frob(f32(fin[n]), rf[n])
-        assert np.isfinite(f32(fin[n])).all() and e <= STATE_TOL, f"seq {n}: final state relF {e:.3e}"
+        got = f32(fin[n])
+        e, e9 = rel_frob(got, rf[n]), rel_frob(got, rf9[n])
+        assert np.isfinite(got).all() and e9 <= STATE_TOL, f"seq {n}: final state relF {e9:.3e} (gates at -9)"
+        assert lens[n] == 1 or e <= STATE_TOL, f"seq {n}: final state relF {e:.3e}"
 
 
 def test_config1_layout_subset_of_heads(oracle):
