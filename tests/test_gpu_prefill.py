@@ -83,9 +83,12 @@ def test_varlen_with_initial_states(oracle):
 
 def test_precise_mode_whole_and_split(oracle):
     """precise=True (fp16-pair operands in the solve and the state updates) on whole sequences and on a layout cut
-    into pieces (later pieces carry their transition, whose update takes the pair too), against the fp64 oracle."""
+    into pieces (later pieces carry their transition, whose update takes the pair too), and on a plan that chose the
+    32-token kernel (which has no precise form: the launch runs the 64-token kernel on the plan's workgroup lists),
+    against the fp64 oracle."""
     _plain_case(oracle, 4, [300, 64, 1, 1000, 77], 1, precise=True)
     _plain_case(oracle, 2, [8192, 300], 70, precise=True)
+    _plain_case(oracle, 2, [600, 300, 130, 1, 0, 65, 700, 33], 71, precise=True, cus=4, chunk64=False)
 
 
 def test_ragged_tiny_and_empty(oracle):
