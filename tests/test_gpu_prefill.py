@@ -459,15 +459,18 @@ def test_every_n_checkpoints_fp32_and_bf16(oracle, every, cus, chunk64):
         assert rel_frob(fin[int(idx[n])], rf[n]) <= STATE_TOL
 
 
-def test_graph_capture_prefill(oracle):
-    """The launch is capturable: replay after refilling q/k/v/g/beta and the initial states in place."""
+@pytest.mark.parametrize("kind", ["plan", "lists", "chunk32"])
+def test_graph_capture_prefill(oracle, kind):
+    """The launch is capturable: replay after refilling q/k/v/g/beta and the initial states in place.  plan: the
+    device's own plan of two sequences (the longer cut into pieces: chunk, scan and tail launches in the graph); lists /
+    chunk32: six sequences planned for 4 CUs, as the 64-token kernel's workgroup lists or the 32-token kernel."""
     kda = _kda()
-    H, lens = 2, [200, 70]
+    H, lens = (2, [200, 70]) if kind == "plan" else (2, [200, 70, 130, 1, 65, 300])
     T, N = sum(lens), len(lens)
-    _say("prefill graph capture")
+    _say(f"prefill graph capture ({kind})")
     g = gen(60)
     cu = torch.tensor(_cu(lens), dtype=torch.int32)
-    meta = kda.plan(cu, H, device=DEV)
+    meta = kda.plan(cu, H, device=DEV) if kind == "plan" else _list_meta(kda, lens, H, 4, kind == "lists")
     ws = torch.empty(meta.workspace_bytes, dtype=torch.uint8, device=DEV)
     bufs = [torch.empty(1, T, H, D, dtype=torch.bfloat16, device=DEV) for _ in range(3)]
     gbuf = torch.empty(1, T, H, D, device=DEV)
